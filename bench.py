@@ -1,0 +1,335 @@
+#!/usr/bin/env python3
+"""Benchmark of HyMT2Sharp's attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the one the headline metric is quoted on):
+one full 32-layer decode step, batch 1, at context 4096 -- per layer 16 q /
+4 kv heads, head_dim 128, fp32 q, fp16 KV cache, RoPE at position 4096,
+per-head RMSNorm on q and k -- as 32 launches of the fused decode kernel over
+32 distinct layers' KV.  A step is one such 32-layer pass; inputs are resident
+in HBM (device pointers) before the timed region.  Four independent KV sets
+(4 x 32 layers, > 1 GiB) rotate so the 256 MiB MALL cannot serve the reads.
+
+Also measured (secondary): causal prefill of 2048
+tokens through one layer, bf16 inputs, bf16 MFMA with fp32 accumulation,
+K/V written into an empty cache.
+
+Printed: ONE JSON line.  `value` is decode-attention HBM GB/s (algorithmic
+bytes per step / wall time per step); `roofline` prices the decode kernel's
+average duration (HIP events around each launch, second pass) against 8 TB/s;
+`prefill` carries the prefill TFLOP/s with its own MFMA roofline;
+`cpu_baseline` is the C oracle (port of Ops.cs) on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from hymt2sharp_amd import BF16, F16, HipBackend  # noqa: E402
+from hymt2sharp_amd import synth as S  # noqa: E402
+
+HQ, HKV, D = 16, 4, 128
+BASE, EPS = 10000.0, 1e-6
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+CTX = 4096                      # cached positions; the new token sits at 4096
+LAYERS = 32
+NSETS = 4                       # KV sets rotated across steps
+
+
+def decode_bytes_per_layer(L, kv_bytes=2):
+    """Algorithmic HBM bytes of one layer's decode: K+V rows read, q in,
+    out, the appended K/V row, the two gamma vectors."""
+    return 2 * L * HKV * D * kv_bytes + HQ * D * 4 * 2 + 2 * HKV * D * kv_bytes + 2 * D * 4
+
+
+def prefill_flops(P0, seq):
+    """Causal prefill FLOPs: 4*D*Hq*sum_i (P0 + i + 1) (QK^T and PV)."""
+    return 4 * D * HQ * (seq * P0 + seq * (seq + 1) // 2)
+
+
+class HipEvents:
+    """hipEvent timing on the backend's own stream."""
+
+    def __init__(self, stream):
+        self.L = ctypes.CDLL("libamdhip64.so")
+        self.stream = ctypes.c_void_p(stream)
+        for f in ("hipEventCreate", "hipEventRecord", "hipEventSynchronize",
+                  "hipEventElapsedTime", "hipEventDestroy"):
+            getattr(self.L, f).restype = ctypes.c_int
+
+    def new(self):
+        e = ctypes.c_void_p()
+        assert self.L.hipEventCreate(ctypes.byref(e)) == 0
+        return e
+
+    def record(self, e):
+        assert self.L.hipEventRecord(e, self.stream) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.L.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.L.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, e):
+        self.L.hipEventDestroy(e)
+
+
+def bench_decode(steps, warmup):
+    L = CTX + 1
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS)
+    be.create_cache(LAYERS * NSETS, L, F16)
+    scale = 1.0 / np.sqrt(D)
+    # 8 distinct cache contents spread over the 128 layers (distinct addresses)
+    pool = [(S.f32_to_bf16_bits(S.normal(S.seed(2, S.KCACHE, i), (CTX, HKV * D), scale)),
+             S.f32_to_bf16_bits(S.normal(S.seed(2, S.VCACHE, i), (CTX, HKV * D), scale)))
+            for i in range(8)]
+    for layer in range(LAYERS * NSETS):
+        kb, vb = pool[layer % 8]
+        be.UploadKv(layer, 0, CTX, kb, vb)
+    nl = LAYERS * NSETS
+    q = S.normal(S.seed(2, S.Q), (nl, HQ * D), scale)
+    k = S.normal(S.seed(2, S.KNEW), (nl, HKV * D), scale)
+    v = S.normal(S.seed(2, S.VNEW), (nl, HKV * D), scale)
+    gq = S.uniform(S.seed(2, S.GQ), (nl, D), 0.9, 1.1)
+    gk = S.uniform(S.seed(2, S.GK), (nl, D), 0.9, 1.1)
+    dq, dk, dv = be.alloc(q.nbytes), be.alloc(k.nbytes), be.alloc(v.nbytes)
+    dgq, dgk, dout = be.alloc(gq.nbytes), be.alloc(gk.nbytes), be.alloc(q.nbytes)
+    for dptr, arr in ((dq, q), (dk, k), (dv, v), (dgq, gq), (dgk, gk)):
+        be.upload(dptr, arr)
+
+    def step(s):
+        base_layer = (s % NSETS) * LAYERS
+        for l in range(LAYERS):
+            i = base_layer + l
+            be.decode_dev(i, CTX, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
+                          dgq + i * D * 4, dgk + i * D * 4, dout + i * HQ * D * 4)
+
+    ev = HipEvents(be.stream())
+    for s in range(warmup):
+        step(s)
+    be.sync()
+    # timed region: K whole steps between two events, synchronised both sides
+    e0, e1 = ev.new(), ev.new()
+    be.sync()
+    t0 = time.perf_counter()
+    ev.record(e0)
+    for s in range(steps):
+        step(s)
+    ev.record(e1)
+    be.sync()
+    wall = time.perf_counter() - t0
+    gpu_ms = ev.elapsed_ms(e0, e1)
+
+    # second pass: an event pair around every launch -> per-kernel duration
+    pairs = [(ev.new(), ev.new()) for _ in range(LAYERS)]
+    durs = []
+    for s in range(steps):
+        base_layer = (s % NSETS) * LAYERS
+        for l in range(LAYERS):
+            i = base_layer + l
+            ev.record(pairs[l][0])
+            be.decode_dev(i, CTX, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
+                          dgq + i * D * 4, dgk + i * D * 4, dout + i * HQ * D * 4)
+            ev.record(pairs[l][1])
+        be.sync()
+        durs += [ev.elapsed_ms(a, b) for a, b in pairs]
+    for a, b in pairs:
+        ev.destroy(a)
+        ev.destroy(b)
+    ev.destroy(e0)
+    ev.destroy(e1)
+
+    out = np.empty((nl, HQ * D), np.float32)
+    be.download(out, dout)
+    assert np.all(np.isfinite(out))
+    for p in (dq, dk, dv, dgq, dgk, dout):
+        be.free(p)
+    be.Dispose()
+
+    bpl = decode_bytes_per_layer(L)
+    ms_step = gpu_ms / steps
+    kern_us = float(np.mean(durs)) * 1e3
+    return {
+        "ms_per_step": ms_step,
+        "wall_ms_per_step": wall * 1e3 / steps,
+        "gbs": bpl * LAYERS / (ms_step * 1e-3) / 1e9,
+        "bytes_per_layer": bpl,
+        "kernel_us": kern_us,
+        "kernel_us_p10": float(np.percentile(durs, 10)) * 1e3,
+        "kernel_us_p90": float(np.percentile(durs, 90)) * 1e3,
+        "kernel_gbs": bpl / (kern_us * 1e-6) / 1e9,
+        "tokens_per_s": 1e3 / ms_step,
+    }
+
+
+def bench_prefill(steps, warmup, seq=2048):
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, seq, BF16)
+    scale = 1.0 / np.sqrt(D)
+    q = S.f32_to_bf16_bits(S.normal(S.seed(3, S.Q), (seq, HQ * D), scale))
+    k = S.f32_to_bf16_bits(S.normal(S.seed(3, S.KNEW), (seq, HKV * D), scale))
+    v = S.f32_to_bf16_bits(S.normal(S.seed(3, S.VNEW), (seq, HKV * D), scale))
+    dq, dk, dv = be.alloc(q.nbytes), be.alloc(k.nbytes), be.alloc(v.nbytes)
+    dout = be.alloc(seq * HQ * D * 4)
+    for dptr, arr in ((dq, q), (dk, k), (dv, v)):
+        be.upload(dptr, arr)
+    ev = HipEvents(be.stream())
+
+    def run():
+        be.prefill_dev(0, 0, seq, dq, dk, dv, BF16, None, None, dout)
+
+    for _ in range(warmup):
+        run()
+    be.sync()
+    e0, e1 = ev.new(), ev.new()
+    ev.record(e0)
+    for _ in range(steps):
+        run()
+    ev.record(e1)
+    be.sync()
+    ms = ev.elapsed_ms(e0, e1) / steps
+    out = np.empty((seq, HQ * D), np.float32)
+    be.download(out, dout)
+    assert np.all(np.isfinite(out))
+    for p in (dq, dk, dv, dout):
+        be.free(p)
+    be.Dispose()
+    fl = prefill_flops(0, seq)
+    return {"ms_per_call": ms, "tflops": fl / (ms * 1e-3) / 1e12, "flops": fl,
+            "tokens_per_s": seq / (ms * 1e-3)}
+
+
+def cpu_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def cpu_baseline_decode(threads, layers=LAYERS, reps=20):
+    """The oracle (C port of Ops.AttentionDecode and the DecodeAttention steps)
+    on a sample of the same workload: `layers` layers of the 4096-context
+    step, mean of `reps` reps after one warm-up (Benchmark/Program.cs:189-211)."""
+    from oracle import oracle as O
+    L = CTX + 1
+    scale = 1.0 / np.sqrt(D)
+    kb = S.f32_to_bf16_bits(S.normal(S.seed(2, S.KCACHE, 0), (CTX, HKV * D), scale))
+    vb = S.f32_to_bf16_bits(S.normal(S.seed(2, S.VCACHE, 0), (CTX, HKV * D), scale))
+    ck = O.new_cache(L, HKV, D, O.F16)
+    cv = O.new_cache(L, HKV, D, O.F16)
+    ck[:CTX] = O.to_storage(S.bf16_bits_to_f32(kb), O.F16)
+    cv[:CTX] = O.to_storage(S.bf16_bits_to_f32(vb), O.F16)
+    q = S.normal(S.seed(2, S.Q), (HQ * D,), scale)
+    k = S.normal(S.seed(2, S.KNEW), (HKV * D,), scale)
+    v = S.normal(S.seed(2, S.VNEW), (HKV * D,), scale)
+    g = np.full(D, 1.0, np.float32)
+
+    def one():
+        for _ in range(layers):
+            O.decode_attention(q, k, v, g, g, ck, cv, O.F16, HQ, HKV, D, BASE, EPS, CTX,
+                               threads=threads)
+
+    one()
+    t = time.perf_counter()
+    for _ in range(reps):
+        one()
+    sec = (time.perf_counter() - t) / reps
+    return decode_bytes_per_layer(L) * layers / sec / 1e9, sec
+
+
+def cpu_baseline_prefill(threads, seq=2048):
+    from oracle import oracle as O
+    scale = 1.0 / np.sqrt(D)
+    q = S.bf16_bits_to_f32(S.f32_to_bf16_bits(S.normal(S.seed(3, S.Q), (seq, HQ * D), scale)))
+    k = S.bf16_bits_to_f32(S.f32_to_bf16_bits(S.normal(S.seed(3, S.KNEW), (seq, HKV * D), scale)))
+    v = S.bf16_bits_to_f32(S.f32_to_bf16_bits(S.normal(S.seed(3, S.VNEW), (seq, HKV * D), scale)))
+    ck = O.new_cache(seq, HKV, D, O.BF16)
+    cv = O.new_cache(seq, HKV, D, O.BF16)
+    t = time.perf_counter()
+    O.prefill_attention(q.reshape(seq, -1), k.reshape(seq, -1), v.reshape(seq, -1), None, None,
+                        ck, cv, O.BF16, HQ, HKV, D, BASE, EPS, 0, threads=threads)
+    sec = time.perf_counter() - t
+    return prefill_flops(0, seq) / sec / 1e12, sec
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py measures one GPU: the attention path has no multi-GPU mode in this "
+              f"build (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    dec = pre = None
+    if args.only in (None, "decode"):
+        dec = bench_decode(args.steps, args.warmup)
+    if args.only in (None, "prefill"):
+        pre = bench_prefill(args.steps, args.warmup)
+
+    cpu = None
+    if not args.no_cpu:
+        th = cpu_threads()
+        gbs, sec = cpu_baseline_decode(th)
+        tfl, psec = cpu_baseline_prefill(th)
+        cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
+               "sample": f"the 32-layer 4096-context decode step (one KV set), mean of 20 reps "
+                         f"({sec * 1e3:.1f} ms per rep), C port of Ops.AttentionDecode "
+                         f"(oracle/hymt_oracle.c), fp16 KV",
+               "prefill": {"value": round(tfl, 4), "unit": "TFLOP/s",
+                           "sample": f"one 2048-token causal prefill, {psec:.2f} s, "
+                                     f"C port of AttentionScores/SoftmaxCausal/AttentionCombine "
+                                     f"with Forward's 1024 chunking"}}
+
+    rec = {
+        "metric": "decode-attn HBM GB/s (% peak) @4k ctx; prefill-attn TFLOP/s (% MFMA peak)",
+        "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16-kv/fp32-math", "data": "synthetic (seeded xoshiro256**, N(0,1)/sqrt(128))",
+        "config": {"workload": "config 2: 32-layer decode step, batch 1, ctx 4096 (L=4097), "
+                               "16q/4kv heads, head_dim 128, fp16 KV, QK RMSNorm",
+                   "global_batch": 1, "seq_len": CTX + 1, "parallelism": "none (1 GPU)"},
+    }
+    if dec:
+        rec["value"] = round(dec["gbs"], 1)
+        rec["ms_per_step"] = round(dec["ms_per_step"], 4)
+        rec["decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}
+        rec["roofline"] = {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 1),
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                           "kernel": "decode_attn_kernel<F16>",
+                           "algorithmic_bytes": dec["bytes_per_layer"],
+                           "avg_us": round(dec["kernel_us"], 3)}
+    if pre:
+        rec["prefill"] = {"workload": "config 3: causal prefill 2048 tokens, one layer, bf16 in, "
+                                      "bf16 MFMA fp32 acc, empty cache",
+                          "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
+                          "ms_per_call": round(pre["ms_per_call"], 4),
+                          "tokens_per_s": round(pre["tokens_per_s"], 1),
+                          "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
+                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                       "traffic": None, "flops": pre["flops"]}}
+    rec["cpu_baseline"] = cpu
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,133 @@
+"""ctypes binding of libhymt_hip.so (include/hymt_hip.h).
+
+The library is built in-tree by hymt2sharp_amd/build.py.  Loading fails
+loudly when it is missing: there is no other implementation to fall back to.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libhymt_hip.so")
+SYNTH_PATH = os.path.join(PKG, "libhymt_synth.so")
+
+HYMT_OK = 0
+HYMT_E_ARG = 1
+HYMT_E_UNSUPPORTED = 2
+HYMT_E_CAPACITY = 3
+HYMT_E_NO_DEVICE = 4
+HYMT_E_DEVICE = 5
+HYMT_E_OOM = 6
+HYMT_E_STATE = 7
+
+F32, F16, BF16 = 0, 1, 2
+DEVICE_NONE = -1
+FLAG_DEVICE_PTRS = 1
+PAGE_TOKENS = 64
+
+
+class HipError(RuntimeError):
+    """A failing libhymt_hip call; `status` is the hymt_status code."""
+
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"[{status}] {msg}")
+        self.status = status
+
+
+class NotSupportedError(HipError):
+    """NotSupportedException in the reference (shape, dtype or capacity)."""
+
+
+class ArgumentError(HipError, ValueError):
+    """ArgumentException in the reference."""
+
+
+class PlatformNotSupportedError(HipError):
+    """PlatformNotSupportedException: no usable device."""
+
+
+class InvalidOperationError(HipError):
+    """InvalidOperationException: driver failure or call out of order."""
+
+
+_EXC = {
+    HYMT_E_ARG: ArgumentError,
+    HYMT_E_UNSUPPORTED: NotSupportedError,
+    HYMT_E_CAPACITY: NotSupportedError,
+    HYMT_E_NO_DEVICE: PlatformNotSupportedError,
+    HYMT_E_DEVICE: InvalidOperationError,
+    HYMT_E_OOM: MemoryError,
+    HYMT_E_STATE: InvalidOperationError,
+}
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+
+# name -> argtypes (every function returns int)
+SIGNATURES = {
+    "hymt_abi_version": [],
+    "hymt_device_count": [ctypes.POINTER(_i)],
+    "hymt_create": [_i, ctypes.POINTER(_vp)],
+    "hymt_destroy": [_vp],
+    "hymt_set_attn_config": [_vp, _i, _i, _i, _i, _f, _f],
+    "hymt_kv_create": [_vp, _i, _i, _i],
+    "hymt_kv_info": [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "hymt_kv_map": [_vp, _i, _i],
+    "hymt_kv_page": [_vp, _i, ctypes.POINTER(_i)],
+    "hymt_kv_set_len": [_vp, _i],
+    "hymt_kv_upload": [_vp, _i, _i, _i, _vp, _vp],
+    "hymt_kv_read": [_vp, _i, _i, _i, _vp, _vp],
+    "hymt_attn_decode": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint],
+    "hymt_attn_prefill": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, ctypes.c_uint],
+    "hymt_sync": [_vp],
+    "hymt_get_stream": [_vp, ctypes.POINTER(_vp)],
+    "hymt_dev_alloc": [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)],
+    "hymt_dev_free": [_vp, _vp],
+    "hymt_memcpy": [_vp, _vp, _vp, ctypes.c_size_t, _i],
+}
+
+_lib = None
+_synth = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libhymt_hip.so; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is not built; run python -m hymt2sharp_amd.build")
+        L = ctypes.CDLL(LIB_PATH)
+        L.hymt_last_error.restype = ctypes.c_char_p
+        L.hymt_last_error.argtypes = []
+        for name, args in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = _i
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != HYMT_OK:
+        msg = lib().hymt_last_error().decode(errors="replace")
+        exc = _EXC.get(status, HipError)
+        if exc is MemoryError:
+            raise MemoryError(msg)
+        raise exc(status, msg)
+
+
+def synth() -> ctypes.CDLL:
+    global _synth
+    if _synth is None:
+        if not os.path.exists(SYNTH_PATH):
+            raise ImportError(f"{SYNTH_PATH} is not built; run python -m hymt2sharp_amd.build")
+        S = ctypes.CDLL(SYNTH_PATH)
+        S.hymt_synth_uniform.argtypes = [ctypes.c_uint64, _vp, ctypes.c_long, _f, _f]
+        S.hymt_synth_normal.argtypes = [ctypes.c_uint64, _vp, ctypes.c_long, _f]
+        S.hymt_synth_index.argtypes = [ctypes.c_uint64, _vp, ctypes.c_long, ctypes.c_int64]
+        for f in (S.hymt_synth_uniform, S.hymt_synth_normal, S.hymt_synth_index):
+            f.restype = None
+        _synth = S
+    return _synth

@@ -1,0 +1,210 @@
+"""Python mirror of the reference's backend plugin surface for the attention
+path, over the C ABI of libhymt_hip.so.
+
+HipBackend follows IComputeBackend (Backends/IComputeBackend.cs:14-88) for
+the members this path owns -- Name, SupportsPrefill, UploadKv, SetCacheLen,
+Dispose -- and adds the per-layer attention unit the reference runs inside
+ForwardStep (DecodeAttention / PrefillAttention, HunyuanDenseModel.Decode.cs:64-101,
+HunyuanDenseModel.Prefill.cs:38-89).  create_backend mirrors
+BackendFactory.Create (Backends/BackendFactory.cs:15-44) with the "hip" name
+added.  Errors raise the Python counterparts of the reference's exceptions.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import _native as N
+from ._native import (ArgumentError, InvalidOperationError, NotSupportedError,  # noqa: F401
+                      PlatformNotSupportedError)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+class HipBackend:
+    """`HipBackend : IComputeBackend` for the attention path on one MI355X."""
+
+    Name = "hip"
+    SupportsPrefill = True
+    SupportsBlockStore = False
+    DeviceBlockTokens = N.PAGE_TOKENS
+
+    def __init__(self, device: int = 0):
+        self._lib = N.lib()
+        h = ctypes.c_void_p()
+        N.check(self._lib.hymt_create(device, ctypes.byref(h)))
+        self._h = h
+        self.device = device
+        self.heads = self.kv_heads = self.head_dim = 0
+
+    # -- configuration (ModelConfig, ModelConfig.cs:21-51) --------------------
+    def configure(self, heads=16, kv_heads=4, head_dim=128, rope_dim=None, rope_base=10000.0,
+                  eps=1e-6):
+        rope_dim = head_dim if rope_dim is None else rope_dim
+        N.check(self._lib.hymt_set_attn_config(self._h, heads, kv_heads, head_dim, rope_dim,
+                                               rope_base, eps))
+        self.heads, self.kv_heads, self.head_dim = heads, kv_heads, head_dim
+        self.rope_dim, self.rope_base, self.eps = rope_dim, rope_base, eps
+        return self
+
+    def create_cache(self, layers: int, max_tokens: int, kv_dtype: int = N.BF16):
+        """KV part of LoadModel (MetalBackend.cs:164-181)."""
+        N.check(self._lib.hymt_kv_create(self._h, layers, max_tokens, kv_dtype))
+        self.layers, self.kv_dtype = layers, kv_dtype
+        return self
+
+    @property
+    def handle(self):
+        return self._h
+
+    def cache_info(self):
+        a, b, c = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        N.check(self._lib.hymt_kv_info(self._h, ctypes.byref(a), ctypes.byref(b), ctypes.byref(c)))
+        return {"max_tokens": a.value, "pages_total": b.value, "pages_mapped": c.value}
+
+    def page_of(self, block: int) -> int:
+        p = ctypes.c_int()
+        N.check(self._lib.hymt_kv_page(self._h, block, ctypes.byref(p)))
+        return p.value
+
+    # -- IComputeBackend members ------------------------------------------
+    def UploadKv(self, layer: int, pos: int, length: int, k_bf16: np.ndarray, v_bf16: np.ndarray):
+        """IComputeBackend.UploadKv (IComputeBackend.cs:31-38): rows [pos, pos+len)
+        of the model's flat bf16 caches (row j at j*kv_stride)."""
+        k = np.ascontiguousarray(k_bf16, dtype=np.uint16)
+        v = np.ascontiguousarray(v_bf16, dtype=np.uint16)
+        stride = self.kv_heads * self.head_dim
+        if k.size < (pos + length) * stride or v.size < (pos + length) * stride:
+            raise ArgumentError(N.HYMT_E_ARG, "cache arrays shorter than pos+len rows")
+        N.check(self._lib.hymt_kv_upload(self._h, layer, pos, length, _ptr(k), _ptr(v)))
+
+    def SetCacheLen(self, length: int):
+        """IComputeBackend.SetCacheLen (IComputeBackend.cs:82-87)."""
+        N.check(self._lib.hymt_kv_set_len(self._h, length))
+
+    def MapRange(self, pos: int, length: int):
+        N.check(self._lib.hymt_kv_map(self._h, pos, length))
+
+    def ReadKv(self, layer: int, pos: int, length: int):
+        """Rows [pos, pos+len) of one layer as fp32 [len][kv_heads*head_dim]."""
+        stride = self.kv_heads * self.head_dim
+        k = np.empty((length, stride), dtype=np.float32)
+        v = np.empty((length, stride), dtype=np.float32)
+        N.check(self._lib.hymt_kv_read(self._h, layer, pos, length, _ptr(k), _ptr(v)))
+        return k, v
+
+    # -- attention unit ---------------------------------------------------
+    def DecodeAttention(self, layer: int, pos: int, q, k, v, qnw=None, knw=None) -> np.ndarray:
+        """Attention of DecodeAttention (Decode.cs:79-95): RoPE, QK norm, append,
+        softmax(qK^T/sqrt(D))V over [0, pos].  Host arrays in, out[heads*head_dim]."""
+        q, k, v, qnw, knw = map(_f32, (q, k, v, qnw, knw))
+        out = np.empty(self.heads * self.head_dim, dtype=np.float32)
+        N.check(self._lib.hymt_attn_decode(self._h, layer, pos, _ptr(q), _ptr(k), _ptr(v),
+                                           _ptr(qnw), _ptr(knw), _ptr(out), 0))
+        return out
+
+    def PrefillAttention(self, layer: int, pos: int, q, k, v, qnw=None, knw=None,
+                         io_dtype: int = N.F32) -> np.ndarray:
+        """Attention of PrefillAttention (Prefill.cs:53-83) for one chunk.
+        q [seq][heads*D], k/v [seq][kv_heads*D] as fp32 (or bf16 bit patterns
+        when io_dtype is BF16).  Returns out[seq][heads*D] fp32."""
+        if io_dtype == N.BF16:
+            q, k, v = (np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v))
+        else:
+            q, k, v = map(_f32, (q, k, v))
+        qnw, knw = _f32(qnw), _f32(knw)
+        seq = q.size // (self.heads * self.head_dim)
+        out = np.empty((seq, self.heads * self.head_dim), dtype=np.float32)
+        N.check(self._lib.hymt_attn_prefill(self._h, layer, pos, seq, _ptr(q), _ptr(k), _ptr(v),
+                                            io_dtype, _ptr(qnw), _ptr(knw), _ptr(out), 0))
+        return out
+
+    # -- device-pointer variants (activations resident in HBM) -------------
+    def decode_dev(self, layer, pos, q, k, v, qnw, knw, out):
+        N.check(self._lib.hymt_attn_decode(self._h, layer, pos, q, k, v, qnw, knw, out,
+                                           N.FLAG_DEVICE_PTRS))
+
+    def prefill_dev(self, layer, pos, seq, q, k, v, io_dtype, qnw, knw, out):
+        N.check(self._lib.hymt_attn_prefill(self._h, layer, pos, seq, q, k, v, io_dtype, qnw, knw,
+                                            out, N.FLAG_DEVICE_PTRS))
+
+    def alloc(self, nbytes: int) -> int:
+        p = ctypes.c_void_p()
+        N.check(self._lib.hymt_dev_alloc(self._h, nbytes, ctypes.byref(p)))
+        return p.value
+
+    def free(self, p):
+        N.check(self._lib.hymt_dev_free(self._h, p))
+
+    def upload(self, dptr, arr: np.ndarray):
+        a = np.ascontiguousarray(arr)
+        N.check(self._lib.hymt_memcpy(self._h, dptr, _ptr(a), a.nbytes, 0))
+
+    def download(self, arr: np.ndarray, dptr):
+        N.check(self._lib.hymt_memcpy(self._h, _ptr(arr), dptr, arr.nbytes, 1))
+        return arr
+
+    def sync(self):
+        N.check(self._lib.hymt_sync(self._h))
+
+    def stream(self) -> int:
+        s = ctypes.c_void_p()
+        N.check(self._lib.hymt_get_stream(self._h, ctypes.byref(s)))
+        return s.value
+
+    # -- IDisposable ------------------------------------------------------
+    def Dispose(self):
+        if self._h:
+            N.check(self._lib.hymt_destroy(self._h))
+            self._h = None
+
+    close = Dispose
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.Dispose()
+
+    def __del__(self):
+        try:
+            self.Dispose()
+        except Exception:
+            pass
+
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    N.check(N.lib().hymt_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def create_backend(preference: str | None = None):
+    """BackendFactory.Create (BackendFactory.cs:15-44) with "hip" added.
+
+    An explicit "hip" constructs the backend and raises if it cannot run;
+    "auto" returns a HipBackend when a device works and None (the CPU engine)
+    otherwise; "cpu" returns None.
+    """
+    p = (preference if preference is not None else os.environ.get("HYMT_BACKEND", "auto"))
+    p = p.strip().lower()
+    if p in ("", "auto"):
+        try:
+            if device_count() > 0:
+                return HipBackend(int(os.environ.get("HYMT_HIP_DEVICE", "0")))
+        except Exception:
+            pass
+        return None
+    if p == "cpu":
+        return None
+    if p == "hip":
+        return HipBackend(int(os.environ.get("HYMT_HIP_DEVICE", "0")))
+    raise ArgumentError(N.HYMT_E_ARG, f"unknown backend '{p}' (expected auto|cpu|hip)")

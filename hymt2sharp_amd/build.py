@@ -1,0 +1,64 @@
+"""Build the native pieces of hymt2sharp_amd in-tree.
+
+libhymt_hip.so   C ABI (include/hymt_hip.h) + gfx950 kernels, via hipcc
+libhymt_synth.so seeded input generator (plain C), via gcc
+
+Run `python -m hymt2sharp_amd.build` or call build_all().
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+HIP_LIB = os.path.join(PKG, "libhymt_hip.so")
+SYNTH_LIB = os.path.join(PKG, "libhymt_synth.so")
+
+HIP_SOURCES = ["hymt_hip.cpp", "decode_attn.hip", "prefill_attn.hip", "kv_ops.hip"]
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Packed fp32 VALU ops are kept off: hipcc -O3 would otherwise form
+# v_pk_{add,mul,fma}_f32 from scalar float code.
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(cmd, cwd=None):
+    r = subprocess.run(cmd, cwd=cwd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout)
+        raise RuntimeError("build failed: " + " ".join(cmd))
+    return r.stdout
+
+
+def build_hip(extra=()):
+    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    tmp = HIP_LIB + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, *extra, *srcs, "-o", tmp])
+    os.replace(tmp, HIP_LIB)
+    return HIP_LIB
+
+
+def build_synth():
+    tmp = SYNTH_LIB + ".tmp"
+    _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", os.path.join(CSRC, "synth.c"), "-lm",
+          "-o", tmp])
+    os.replace(tmp, SYNTH_LIB)
+    return SYNTH_LIB
+
+
+def build_all():
+    build_synth()
+    build_hip()
+
+
+if __name__ == "__main__":
+    build_all()
+    print(HIP_LIB)
+    print(SYNTH_LIB)

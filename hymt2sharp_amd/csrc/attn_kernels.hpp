@@ -1,0 +1,98 @@
+// attn_kernels.hpp -- argument blocks and host launchers of the gfx950
+// attention kernels.  Included by the C-ABI shim (hymt_hip.cpp) and by the
+// kernel sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hymt {
+
+constexpr int kHeadDim = 128;   // built head_dim (Hy-MT2-1.8B)
+constexpr int kGroup = 4;       // q heads per kv head (16 / 4)
+constexpr int kPage = 64;       // tokens per KV page
+constexpr int kMaxSplits = 128; // decode KV splits per kv head (merge width)
+
+// Paged pool addressing, per layer:
+//   K  element ((phys*Hkv + kvh)*64 + t)*D + d      (row-major rows of one head)
+//   V  element ((phys*Hkv + kvh)*D + d)*64 + t      (transposed: 64 positions per d)
+// The V transpose gives the P*V MFMA operand 8 consecutive positions per lane.
+
+struct DecodeArgs {
+    const float *q;     // [Hq*D]
+    const float *knew;  // [Hkv*D]
+    const float *vnew;  // [Hkv*D]
+    const float *qnw;   // [D] or null
+    const float *knw;   // [D] or null
+    const float *rope_cos;  // row `pos` of the cos table, [rope_half]
+    const float *rope_sin;
+    const int32_t *tab; // logical block -> physical page
+    void *kpool;        // this layer's K pool
+    void *vpool;        // this layer's V pool
+    float *part_ml;     // [Hq][kMaxSplits][2]
+    float *part_acc;    // [Hq][kMaxSplits][D]
+    uint32_t *counters; // [Hkv], zero between launches
+    float *out;         // [Hq*D]
+    int L;              // positions attended = pos + 1
+    int kv_heads;
+    int rope_half;
+    int rope_dim;
+    int nsplit;
+    int ppw;            // pages per split
+    float eps;
+    float qscale;       // log2(e) / sqrt(D)
+};
+
+struct PrepArgs {
+    const void *q;      // [seq][Hq*D]   fp32 or bf16
+    const void *k;      // [seq][Hkv*D]
+    const void *v;
+    const float *qnw, *knw;
+    const float *rope_cos; // table base [cap][rope_half]
+    const float *rope_sin;
+    const int32_t *tab;
+    void *kpool, *vpool;
+    void *qp;           // out: [Hq][seq_pad][D] MFMA-typed q, scaled by qscale
+    int pos0, seq, seq_pad;
+    int heads, kv_heads;
+    int rope_half, rope_dim;
+    int io_bf16;
+    float eps, qscale;
+};
+
+struct FlashArgs {
+    const void *qp;     // [Hq][seq_pad][D]
+    const int32_t *tab;
+    const void *kpool, *vpool;
+    float *out;         // [seq][Hq*D]
+    float *part_o;      // [items][G][32][D]  (split items only)
+    float *part_ml;     // [items][G][32][2]
+    int pos0, seq, seq_pad;
+    int heads, kv_heads;
+    int nqb;            // q blocks of 32 rows
+    int cap;            // max kv tiles per work item
+    int items_per_kvh;  // work items per kv head
+};
+
+// Number of kv tiles (pages) q block qb attends to.
+__host__ __device__ inline int flash_tiles(int pos0, int qb, int seq) {
+    int last = pos0 + qb * 32 + 31;
+    int lim = pos0 + seq - 1;
+    if (last > lim) last = lim;
+    return last / 64 + 1;
+}
+
+// kv dtype codes as in hymt_dtype.
+hipError_t launch_decode(int kv_dtype, const DecodeArgs &a, hipStream_t s);
+hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s);
+hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s);
+hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s);
+hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n, hipStream_t s);
+hipError_t launch_kv_upload(int kv_dtype, const uint16_t *k_bf16, const uint16_t *v_bf16,
+                            const int32_t *tab, void *kpool, void *vpool, int pos, int len,
+                            int kv_heads, hipStream_t s);
+hipError_t launch_kv_read(int kv_dtype, const int32_t *tab, const void *kpool, const void *vpool,
+                          float *k_out, float *v_out, int pos, int len, int kv_heads,
+                          hipStream_t s);
+
+}  // namespace hymt

@@ -1,0 +1,611 @@
+// hymt_hip.cpp -- the C ABI of libhymt_hip.so (declared in include/hymt_hip.h).
+//
+// Owns one HIP device and stream per context, the paged K/V cache of every
+// layer, the RoPE table and the kernels' workspaces.  Plays the role of the
+// reference backends' device state (VulkanBackend.cs:275-294,
+// MetalBackend.cs:160-197) for the attention path only.
+#include "../../include/hymt_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "attn_kernels.hpp"
+#include "kv_pages.hpp"
+
+using namespace hymt;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string &msg) {
+    g_err = msg;
+    return code;
+}
+
+struct HipError {
+    hipError_t e;
+    const char *what;
+};
+
+#define HIP_TRY(call)                                        \
+    do {                                                     \
+        hipError_t e_ = (call);                              \
+        if (e_ != hipSuccess) throw HipError{e_, #call};     \
+    } while (0)
+
+// A device buffer that grows on demand and never shrinks.
+struct DevBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    void reserve(size_t n) {
+        if (n <= bytes) return;
+        if (p) HIP_TRY(hipFree(p));
+        p = nullptr;
+        bytes = 0;
+        HIP_TRY(hipMalloc(&p, n));
+        bytes = n;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+// Pinned host staging for calls with host pointers.
+struct HostBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    void reserve(size_t n) {
+        if (n <= bytes) return;
+        if (p) HIP_TRY(hipHostFree(p));
+        p = nullptr;
+        bytes = 0;
+        HIP_TRY(hipHostMalloc(&p, n, hipHostMallocDefault));
+        bytes = n;
+    }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+size_t dtype_bytes(int dt) { return dt == HYMT_F32 ? 4 : 2; }
+
+}  // namespace
+
+struct hymt_ctx {
+    int device = HYMT_DEVICE_NONE;
+    hipStream_t stream = nullptr;
+
+    // attention config (ModelConfig)
+    bool configured = false;
+    int heads = 0, kv_heads = 0, head_dim = 0, rope_dim = 0;
+    float rope_base = 10000.f, eps = 1e-6f;
+
+    // paged KV
+    bool kv_ready = false;
+    int layers = 0, kv_dtype = HYMT_BF16;
+    KvPages pages;
+    DevBuf kpool, vpool, tab;
+    size_t layer_elems = 0;  // elements per layer pool
+
+    // RoPE table rows [0, rope_cap)
+    int rope_cap = 0;
+    DevBuf rope_cos, rope_sin;
+
+    // decode workspace
+    DevBuf dec_ml, dec_acc, dec_cnt;
+    // prefill workspace
+    DevBuf qp, part_o, part_ml;
+    // staging for host-pointer calls
+    DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
+    HostBuf h_in, h_out;
+
+    bool has_device() const { return device >= 0; }
+    void *klayer(int l) const { return (char *)kpool.p + (size_t)l * layer_elems * dtype_bytes(kv_dtype); }
+    void *vlayer(int l) const { return (char *)vpool.p + (size_t)l * layer_elems * dtype_bytes(kv_dtype); }
+};
+
+namespace {
+
+int map_hip(const HipError &e) {
+    if (e.e == hipErrorOutOfMemory || e.e == hipErrorMemoryAllocation)
+        return fail(HYMT_E_OOM, std::string("device allocation failed: ") + e.what);
+    return fail(HYMT_E_DEVICE, std::string(e.what) + ": " + hipGetErrorString(e.e));
+}
+
+// Mirror changed page-table entries to the device table.
+void flush_table(hymt_ctx *c) {
+    if (!c->pages.has_dirty()) return;
+    std::vector<int> idx = c->pages.take_dirty();
+    std::vector<int> val(idx.size());
+    for (size_t i = 0; i < idx.size(); i++) val[i] = c->pages.phys(idx[i]);
+    HIP_TRY(launch_tab_update((int32_t *)c->tab.p, idx.data(), val.data(), (int)idx.size(), c->stream));
+}
+
+// Ops.EnsureRopeTable (Ops.cs:170-195): capacity max(needed, 4096), grown by
+// doubling; freq_i = 1 / base^(i/half), angle = pos * freq in fp32.
+void ensure_rope(hymt_ctx *c, int needed) {
+    if (needed <= c->rope_cap) return;
+    int cap = std::max(needed, 4096);
+    if (c->rope_cap > 0) cap = std::max(cap, 2 * c->rope_cap);
+    const int half = c->rope_dim / 2;
+    std::vector<float> freqs(half), cs((size_t)cap * half), sn((size_t)cap * half);
+    for (int i = 0; i < half; i++) freqs[i] = 1.0f / powf(c->rope_base, (float)i / (float)half);
+    for (int pos = 0; pos < cap; pos++)
+        for (int i = 0; i < half; i++) {
+            float angle = (float)pos * freqs[i];
+            cs[(size_t)pos * half + i] = cosf(angle);
+            sn[(size_t)pos * half + i] = sinf(angle);
+        }
+    HIP_TRY(hipStreamSynchronize(c->stream));  // kernels may still read the old table
+    c->rope_cos.reserve(cs.size() * 4);
+    c->rope_sin.reserve(sn.size() * 4);
+    HIP_TRY(hipMemcpy(c->rope_cos.p, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy(c->rope_sin.p, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+    c->rope_cap = cap;
+}
+
+// Copy host tensors into device staging through one pinned buffer.
+struct Upload {
+    const void *src;
+    size_t bytes;
+    DevBuf *dst;
+};
+void stage_in(hymt_ctx *c, std::initializer_list<Upload> ups) {
+    size_t total = 0;
+    for (auto &u : ups) total += (u.src ? (u.bytes + 255) & ~(size_t)255 : 0);
+    HIP_TRY(hipStreamSynchronize(c->stream));  // pinned buffer may still feed a copy
+    c->h_in.reserve(total);
+    size_t off = 0;
+    for (auto &u : ups) {
+        if (!u.src) continue;
+        u.dst->reserve(u.bytes);
+        std::memcpy((char *)c->h_in.p + off, u.src, u.bytes);
+        HIP_TRY(hipMemcpyAsync(u.dst->p, (char *)c->h_in.p + off, u.bytes, hipMemcpyHostToDevice, c->stream));
+        off += (u.bytes + 255) & ~(size_t)255;
+    }
+}
+
+void stage_out(hymt_ctx *c, const void *dsrc, void *hdst, size_t bytes) {
+    c->h_out.reserve(bytes);
+    HIP_TRY(hipMemcpyAsync(c->h_out.p, dsrc, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(hipStreamSynchronize(c->stream));
+    std::memcpy(hdst, c->h_out.p, bytes);
+}
+
+int check_ctx(hymt_ctx *c, bool need_kv, bool need_dev) {
+    if (!c) return fail(HYMT_E_ARG, "null context");
+    if (need_kv && !c->kv_ready) return fail(HYMT_E_STATE, "KV cache not created (hymt_kv_create)");
+    if (need_dev && !c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    return HYMT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *hymt_last_error(void) { return g_err.c_str(); }
+
+int hymt_abi_version(void) { return HYMT_ABI_VERSION; }
+
+int hymt_device_count(int *count) {
+    if (!count) return fail(HYMT_E_ARG, "null count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    *count = (e == hipSuccess) ? n : 0;
+    return HYMT_OK;
+}
+
+int hymt_create(int device, hymt_ctx **out) {
+    if (!out) return fail(HYMT_E_ARG, "null out");
+    *out = nullptr;
+    hymt_ctx *c = new (std::nothrow) hymt_ctx();
+    if (!c) return fail(HYMT_E_OOM, "host allocation failed");
+    if (device == HYMT_DEVICE_NONE) {
+        *out = c;
+        return HYMT_OK;
+    }
+    int n = 0;
+    if (device < 0 || hipGetDeviceCount(&n) != hipSuccess || device >= n) {
+        delete c;
+        return fail(HYMT_E_NO_DEVICE, "HIP device " + std::to_string(device) + " not available (" +
+                                          std::to_string(n) + " devices)");
+    }
+    try {
+        HIP_TRY(hipSetDevice(device));
+        hipDeviceProp_t prop;
+        HIP_TRY(hipGetDeviceProperties(&prop, device));
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            delete c;
+            return fail(HYMT_E_NO_DEVICE, std::string("built for gfx950, device is ") + prop.gcnArchName);
+        }
+        HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+        c->device = device;
+    } catch (const HipError &e) {
+        delete c;
+        return map_hip(e);
+    }
+    *out = c;
+    return HYMT_OK;
+}
+
+int hymt_destroy(hymt_ctx *c) {
+    if (!c) return HYMT_OK;
+    if (c->has_device()) {
+        (void)hipSetDevice(c->device);
+        (void)hipStreamSynchronize(c->stream);
+        for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->dec_ml,
+                          &c->dec_acc, &c->dec_cnt, &c->qp, &c->part_o, &c->part_ml, &c->in_q,
+                          &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v})
+            b->release();
+        c->h_in.release();
+        c->h_out.release();
+        (void)hipStreamDestroy(c->stream);
+    }
+    delete c;
+    return HYMT_OK;
+}
+
+int hymt_set_attn_config(hymt_ctx *c, int heads, int kv_heads, int head_dim, int rope_dim,
+                         float rope_base, float eps) {
+    if (int r = check_ctx(c, false, false)) return r;
+    if (c->kv_ready) return fail(HYMT_E_STATE, "config must precede hymt_kv_create");
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || head_dim <= 0 || rope_dim < 0 ||
+        rope_dim > head_dim || (rope_dim & 1) || !(rope_base > 0.f) || !(eps >= 0.f))
+        return fail(HYMT_E_ARG, "invalid attention config");
+    if (head_dim != kHeadDim || heads / kv_heads != kGroup || 8 % kv_heads)
+        return fail(HYMT_E_UNSUPPORTED, "built for head_dim 128, 4 q heads per kv head, kv_heads dividing 8");
+    c->heads = heads;
+    c->kv_heads = kv_heads;
+    c->head_dim = head_dim;
+    c->rope_dim = rope_dim;
+    c->rope_base = rope_base;
+    c->eps = eps;
+    c->configured = true;
+    return HYMT_OK;
+}
+
+int hymt_kv_create(hymt_ctx *c, int layers, int max_tokens, int kv_dtype) {
+    if (int r = check_ctx(c, false, false)) return r;
+    if (!c->configured) return fail(HYMT_E_STATE, "hymt_set_attn_config first");
+    if (c->kv_ready) return fail(HYMT_E_STATE, "KV cache already created");
+    if (layers <= 0 || max_tokens <= 0 || kv_dtype < HYMT_F32 || kv_dtype > HYMT_BF16)
+        return fail(HYMT_E_ARG, "invalid KV cache arguments");
+    c->layers = layers;
+    c->kv_dtype = kv_dtype;
+    c->pages = KvPages(max_tokens);
+    const int P = c->pages.max_pages();
+    c->layer_elems = (size_t)P * c->kv_heads * kPage * c->head_dim;
+    if (c->has_device()) {
+        try {
+            HIP_TRY(hipSetDevice(c->device));
+            const size_t bytes = (size_t)layers * c->layer_elems * dtype_bytes(kv_dtype);
+            c->kpool.reserve(bytes);
+            c->vpool.reserve(bytes);
+            c->tab.reserve((size_t)P * 4);
+            HIP_TRY(hipMemset(c->tab.p, 0xFF, (size_t)P * 4));
+            c->dec_ml.reserve((size_t)c->heads * kMaxSplits * 2 * 4);
+            c->dec_acc.reserve((size_t)c->heads * kMaxSplits * kHeadDim * 4);
+            c->dec_cnt.reserve((size_t)c->kv_heads * 4);
+            HIP_TRY(hipMemset(c->dec_cnt.p, 0, (size_t)c->kv_heads * 4));
+        } catch (const HipError &e) {
+            c->kpool.release();
+            c->vpool.release();
+            return map_hip(e);
+        }
+    }
+    c->kv_ready = true;
+    return HYMT_OK;
+}
+
+int hymt_kv_info(hymt_ctx *c, int *max_tokens, int *pages_total, int *pages_mapped) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (max_tokens) *max_tokens = c->pages.max_tokens();
+    if (pages_total) *pages_total = c->pages.max_pages();
+    if (pages_mapped) *pages_mapped = c->pages.mapped();
+    return HYMT_OK;
+}
+
+int hymt_kv_map(hymt_ctx *c, int pos, int len) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (pos < 0 || len < 0) return fail(HYMT_E_ARG, "invalid range");
+    try {
+        c->pages.ensure_written(pos, len);
+        if (c->has_device()) {
+            HIP_TRY(hipSetDevice(c->device));
+            flush_table(c);
+        }
+    } catch (const CapacityError &e) {
+        return fail(HYMT_E_CAPACITY, e.what());
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_kv_page(hymt_ctx *c, int block, int *phys) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (!phys || block < 0 || block >= c->pages.max_pages()) return fail(HYMT_E_ARG, "invalid block");
+    *phys = c->pages.phys(block);
+    return HYMT_OK;
+}
+
+int hymt_kv_set_len(hymt_ctx *c, int len) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (len < 0) return fail(HYMT_E_ARG, "negative cache length");
+    c->pages.set_len(len);
+    return HYMT_OK;
+}
+
+int hymt_kv_upload(hymt_ctx *c, int layer, int pos, int len, const uint16_t *k_bf16,
+                   const uint16_t *v_bf16) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (layer < 0 || layer >= c->layers || pos < 0 || len < 0 || (len > 0 && (!k_bf16 || !v_bf16)))
+        return fail(HYMT_E_ARG, "invalid upload arguments");
+    if ((long)pos + len > c->pages.max_tokens())
+        return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
+                                         " exceeded at " + std::to_string((long)pos + len));
+    if (len == 0) return HYMT_OK;
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        c->pages.ensure_written(pos, len);
+        flush_table(c);
+        const size_t stride = (size_t)c->kv_heads * c->head_dim;
+        const size_t bytes = (size_t)len * stride * 2;
+        stage_in(c, {{k_bf16 + (size_t)pos * stride, bytes, &c->up_k},
+                     {v_bf16 + (size_t)pos * stride, bytes, &c->up_v}});
+        HIP_TRY(launch_kv_upload(c->kv_dtype, (const uint16_t *)c->up_k.p, (const uint16_t *)c->up_v.p,
+                                 (const int32_t *)c->tab.p, c->klayer(layer), c->vlayer(layer), pos,
+                                 len, c->kv_heads, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    } catch (const CapacityError &e) {
+        return fail(HYMT_E_CAPACITY, e.what());
+    }
+    return HYMT_OK;
+}
+
+int hymt_kv_read(hymt_ctx *c, int layer, int pos, int len, float *k_out, float *v_out) {
+    if (int r = check_ctx(c, true, true)) return r;
+    if (layer < 0 || layer >= c->layers || pos < 0 || len < 0 || (len > 0 && (!k_out || !v_out)))
+        return fail(HYMT_E_ARG, "invalid read arguments");
+    if (!c->pages.resident(pos + len)) return fail(HYMT_E_STATE, "rows not resident");
+    if (len == 0) return HYMT_OK;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        const size_t n = (size_t)len * c->kv_heads * c->head_dim;
+        c->out_o.reserve(2 * n * 4);
+        float *dk = (float *)c->out_o.p, *dv = dk + n;
+        HIP_TRY(launch_kv_read(c->kv_dtype, (const int32_t *)c->tab.p, c->klayer(layer), c->vlayer(layer),
+                               dk, dv, pos, len, c->kv_heads, c->stream));
+        stage_out(c, dk, k_out, n * 4);
+        stage_out(c, dv, v_out, n * 4);
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const float *k,
+                     const float *v, const float *qnw, const float *knw, float *out,
+                     unsigned flags) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (layer < 0 || layer >= c->layers || pos < 0 || !q || !k || !v || !out)
+        return fail(HYMT_E_ARG, "invalid decode arguments");
+    if (pos >= c->pages.max_tokens())
+        return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
+                                         " exceeded at " + std::to_string(pos + 1));
+    if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before decode");
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        c->pages.ensure_written(pos, 1);
+        flush_table(c);
+        ensure_rope(c, pos + 1);
+        const size_t D = c->head_dim, qn = (size_t)c->heads * D, kn = (size_t)c->kv_heads * D;
+        if (!dev) {
+            stage_in(c, {{q, qn * 4, &c->in_q}, {k, kn * 4, &c->in_k}, {v, kn * 4, &c->in_v},
+                         {qnw, D * 4, &c->in_qnw}, {knw, D * 4, &c->in_knw}});
+            c->out_o.reserve(qn * 4);
+        }
+        DecodeArgs a;
+        a.q = dev ? q : (const float *)c->in_q.p;
+        a.knew = dev ? k : (const float *)c->in_k.p;
+        a.vnew = dev ? v : (const float *)c->in_v.p;
+        a.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
+        a.knw = !knw ? nullptr : dev ? knw : (const float *)c->in_knw.p;
+        const int half = c->rope_dim / 2;
+        a.rope_cos = (const float *)c->rope_cos.p + (size_t)pos * half;
+        a.rope_sin = (const float *)c->rope_sin.p + (size_t)pos * half;
+        a.tab = (const int32_t *)c->tab.p;
+        a.kpool = c->klayer(layer);
+        a.vpool = c->vlayer(layer);
+        a.part_ml = (float *)c->dec_ml.p;
+        a.part_acc = (float *)c->dec_acc.p;
+        a.counters = (uint32_t *)c->dec_cnt.p;
+        a.out = dev ? out : (float *)c->out_o.p;
+        a.L = pos + 1;
+        a.kv_heads = c->kv_heads;
+        a.rope_half = half;
+        a.rope_dim = c->rope_dim;
+        const int npages = (a.L + kPage - 1) / kPage;
+        a.ppw = (npages + kMaxSplits - 1) / kMaxSplits;
+        if (const char *s = std::getenv("HYMT_HIP_DECODE_PPW")) a.ppw = std::max(a.ppw, atoi(s));
+        a.nsplit = (npages + a.ppw - 1) / a.ppw;
+        a.eps = c->eps;
+        a.qscale = 1.4426950408889634f / sqrtf((float)D);
+        HIP_TRY(launch_decode(c->kv_dtype, a, c->stream));
+        if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
+    } catch (const HipError &e) {
+        return map_hip(e);
+    } catch (const CapacityError &e) {
+        return fail(HYMT_E_CAPACITY, e.what());
+    }
+    return HYMT_OK;
+}
+
+int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, const void *k,
+                      const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
+                      unsigned flags) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (layer < 0 || layer >= c->layers || pos < 0 || seq <= 0 || !q || !k || !v || !out ||
+        (io_dtype != HYMT_F32 && io_dtype != HYMT_BF16))
+        return fail(HYMT_E_ARG, "invalid prefill arguments");
+    if (c->kv_dtype == HYMT_F32)
+        return fail(HYMT_E_UNSUPPORTED, "prefill runs on bf16/f16 MFMA; f32 KV cache has no prefill path");
+    if ((long)pos + seq > c->pages.max_tokens())
+        return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
+                                         " exceeded at " + std::to_string((long)pos + seq));
+    if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before prefill");
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        c->pages.ensure_written(pos, seq);
+        flush_table(c);
+        ensure_rope(c, pos + seq);
+        const size_t D = c->head_dim, es = dtype_bytes(io_dtype);
+        const size_t qn = (size_t)seq * c->heads * D, kn = (size_t)seq * c->kv_heads * D;
+        if (!dev) {
+            stage_in(c, {{q, qn * es, &c->in_q}, {k, kn * es, &c->in_k}, {v, kn * es, &c->in_v},
+                         {qnw, D * 4, &c->in_qnw}, {knw, D * 4, &c->in_knw}});
+            c->out_o.reserve(qn * 4);
+        }
+        const int seq_pad = (seq + 31) / 32 * 32;
+        c->qp.reserve((size_t)c->heads * seq_pad * D * 2);
+
+        PrepArgs p;
+        p.q = dev ? q : c->in_q.p;
+        p.k = dev ? k : c->in_k.p;
+        p.v = dev ? v : c->in_v.p;
+        p.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
+        p.knw = !knw ? nullptr : dev ? knw : (const float *)c->in_knw.p;
+        p.rope_cos = (const float *)c->rope_cos.p;
+        p.rope_sin = (const float *)c->rope_sin.p;
+        p.tab = (const int32_t *)c->tab.p;
+        p.kpool = c->klayer(layer);
+        p.vpool = c->vlayer(layer);
+        p.qp = c->qp.p;
+        p.pos0 = pos;
+        p.seq = seq;
+        p.seq_pad = seq_pad;
+        p.heads = c->heads;
+        p.kv_heads = c->kv_heads;
+        p.rope_half = c->rope_dim / 2;
+        p.rope_dim = c->rope_dim;
+        p.io_bf16 = io_dtype == HYMT_BF16;
+        p.eps = c->eps;
+        p.qscale = 1.4426950408889634f / sqrtf((float)D);
+        HIP_TRY(launch_prefill_prep(c->kv_dtype, p, c->stream));
+
+        FlashArgs f;
+        f.qp = c->qp.p;
+        f.tab = (const int32_t *)c->tab.p;
+        f.kpool = c->klayer(layer);
+        f.vpool = c->vlayer(layer);
+        f.out = dev ? out : (float *)c->out_o.p;
+        f.pos0 = pos;
+        f.seq = seq;
+        f.seq_pad = seq_pad;
+        f.heads = c->heads;
+        f.kv_heads = c->kv_heads;
+        f.nqb = seq_pad / 32;
+        // Work items: split the kv range of q blocks only when there are too
+        // few (kv head, q block) pairs to fill the GPU.
+        int max_tiles = 0;
+        for (int qb = 0; qb < f.nqb; qb++) max_tiles = std::max(max_tiles, flash_tiles(pos, qb, seq));
+        int cap = max_tiles;
+        const int pairs = f.nqb * c->kv_heads;
+        if (pairs < 256) {
+            const int per = (256 + pairs - 1) / pairs;
+            cap = std::max(4, (max_tiles + per - 1) / per);
+        }
+        if (const char *s = std::getenv("HYMT_HIP_PREFILL_CAP")) cap = std::max(1, atoi(s));
+        f.cap = cap;
+        int items = 0;
+        bool split = false;
+        for (int qb = 0; qb < f.nqb; qb++) {
+            const int ns = (flash_tiles(pos, qb, seq) + cap - 1) / cap;
+            items += ns;
+            split |= ns > 1;
+        }
+        f.items_per_kvh = items;
+        if (split) {
+            const size_t slots = (size_t)c->kv_heads * items;
+            c->part_o.reserve(slots * kGroup * 32 * D * 4);
+            c->part_ml.reserve(slots * kGroup * 32 * 2 * 4);
+        }
+        f.part_o = (float *)c->part_o.p;
+        f.part_ml = (float *)c->part_ml.p;
+        HIP_TRY(launch_prefill_flash(c->kv_dtype, f, items * c->kv_heads, c->stream));
+        if (split) HIP_TRY(launch_prefill_merge(f, c->stream));
+        if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
+    } catch (const HipError &e) {
+        return map_hip(e);
+    } catch (const CapacityError &e) {
+        return fail(HYMT_E_CAPACITY, e.what());
+    }
+    return HYMT_OK;
+}
+
+int hymt_sync(hymt_ctx *c) {
+    if (int r = check_ctx(c, false, true)) return r;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_get_stream(hymt_ctx *c, void **stream) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!stream) return fail(HYMT_E_ARG, "null stream out");
+    *stream = (void *)c->stream;
+    return HYMT_OK;
+}
+
+int hymt_dev_alloc(hymt_ctx *c, size_t bytes, void **dptr) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!dptr || bytes == 0) return fail(HYMT_E_ARG, "invalid allocation request");
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMalloc(dptr, bytes);
+    if (e != hipSuccess) return fail(HYMT_E_OOM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_dev_free(hymt_ctx *c, void *dptr) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!dptr) return HYMT_OK;
+    (void)hipStreamSynchronize(c->stream);
+    hipError_t e = hipFree(dptr);
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipFree: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_memcpy(hymt_ctx *c, void *dst, const void *src, size_t bytes, int kind) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!dst || !src || kind < 0 || kind > 2) return fail(HYMT_E_ARG, "invalid copy arguments");
+    if (bytes == 0) return HYMT_OK;
+    const hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice
+                            : kind == 1 ? hipMemcpyDeviceToHost
+                                        : hipMemcpyDeviceToDevice;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, k, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipMemcpy: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+}  // extern "C"

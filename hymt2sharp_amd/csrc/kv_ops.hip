@@ -1,0 +1,107 @@
+// kv_ops.hip -- page-table mirroring and bulk K/V row transfers for the
+// paged cache (layout in attn_kernels.hpp).
+#include "attn_kernels.hpp"
+#include "device_common.hpp"
+
+namespace hymt {
+
+// Up to 64 table entries per launch, passed by value so the host copy can
+// change as soon as the launch returns.
+struct TabUpdate {
+    int n;
+    int idx[64];
+    int val[64];
+};
+
+__global__ void tab_update_kernel(int32_t *tab, TabUpdate u) {
+    int i = threadIdx.x;
+    if (i < u.n) tab[u.idx[i]] = u.val[i];
+}
+
+hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n, hipStream_t s) {
+    for (int off = 0; off < n; off += 64) {
+        TabUpdate u;
+        u.n = n - off < 64 ? n - off : 64;
+        for (int i = 0; i < u.n; i++) {
+            u.idx[i] = idx[off + i];
+            u.val[i] = val[off + i];
+        }
+        hipLaunchKernelGGL(tab_update_kernel, dim3(1), dim3(64), 0, s, tab, u);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// IComputeBackend.UploadKv (IComputeBackend.cs:31-38): rows [pos, pos+len)
+// of flat bf16 [row][Hkv*D] caches (kb/vb point at row pos) -> paged cache
+// in its dtype.  One thread per (row, kvh, d).
+template <typename T>
+__global__ void kv_upload_kernel(const uint16_t *kb, const uint16_t *vb, const int32_t *tab,
+                                 typename T::storage *kpool, typename T::storage *vpool, int pos,
+                                 int len, int Hkv) {
+    constexpr int D = kHeadDim, P = kPage;
+    const long n = (long)len * Hkv * D;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+        const int d = (int)(i % D);
+        const int kvh = (int)((i / D) % Hkv);
+        const int j = pos + (int)(i / ((long)D * Hkv));
+        const int phys = tab[j / P], t = j % P;
+        const size_t pg = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
+        const size_t src = (size_t)(j - pos) * Hkv * D + (size_t)kvh * D + d;
+        kpool[pg + (size_t)t * D + d] = to_elem<T>(bf16_to_f32(kb[src]));
+        vpool[pg + (size_t)d * P + t] = to_elem<T>(bf16_to_f32(vb[src]));
+    }
+}
+
+hipError_t launch_kv_upload(int kv_dtype, const uint16_t *k_bf16, const uint16_t *v_bf16,
+                            const int32_t *tab, void *kpool, void *vpool, int pos, int len,
+                            int kv_heads, hipStream_t s) {
+    long n = (long)len * kv_heads * kHeadDim;
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) return hipSuccess;
+    switch (kv_dtype) {
+    case 0: hipLaunchKernelGGL(kv_upload_kernel<F32>, dim3(blocks), dim3(256), 0, s, k_bf16, v_bf16, tab, (float *)kpool, (float *)vpool, pos, len, kv_heads); break;
+    case 1: hipLaunchKernelGGL(kv_upload_kernel<F16>, dim3(blocks), dim3(256), 0, s, k_bf16, v_bf16, tab, (uint16_t *)kpool, (uint16_t *)vpool, pos, len, kv_heads); break;
+    case 2: hipLaunchKernelGGL(kv_upload_kernel<BF16>, dim3(blocks), dim3(256), 0, s, k_bf16, v_bf16, tab, (uint16_t *)kpool, (uint16_t *)vpool, pos, len, kv_heads); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+__global__ void kv_read_kernel(const int32_t *tab, const typename T::storage *kpool,
+                               const typename T::storage *vpool, float *ko, float *vo, int pos,
+                               int len, int Hkv) {
+    constexpr int D = kHeadDim, P = kPage;
+    const long n = (long)len * Hkv * D;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+        const int d = (int)(i % D);
+        const int kvh = (int)((i / D) % Hkv);
+        const int r = (int)(i / ((long)D * Hkv));
+        const int j = pos + r;
+        const int phys = tab[j / P], t = j % P;
+        const size_t pg = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
+        ko[i] = from_elem<T>(kpool[pg + (size_t)t * D + d]);
+        vo[i] = from_elem<T>(vpool[pg + (size_t)d * P + t]);
+    }
+}
+
+hipError_t launch_kv_read(int kv_dtype, const int32_t *tab, const void *kpool, const void *vpool,
+                          float *k_out, float *v_out, int pos, int len, int kv_heads,
+                          hipStream_t s) {
+    long n = (long)len * kv_heads * kHeadDim;
+    int blocks = (int)((n + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) return hipSuccess;
+    switch (kv_dtype) {
+    case 0: hipLaunchKernelGGL(kv_read_kernel<F32>, dim3(blocks), dim3(256), 0, s, tab, (const float *)kpool, (const float *)vpool, k_out, v_out, pos, len, kv_heads); break;
+    case 1: hipLaunchKernelGGL(kv_read_kernel<F16>, dim3(blocks), dim3(256), 0, s, tab, (const uint16_t *)kpool, (const uint16_t *)vpool, k_out, v_out, pos, len, kv_heads); break;
+    case 2: hipLaunchKernelGGL(kv_read_kernel<BF16>, dim3(blocks), dim3(256), 0, s, tab, (const uint16_t *)kpool, (const uint16_t *)vpool, k_out, v_out, pos, len, kv_heads); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace hymt

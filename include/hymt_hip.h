@@ -1,0 +1,170 @@
+/*
+ * hymt_hip.h -- C ABI of libhymt_hip.so, the MI355X (gfx950) attention path
+ * for HyMT2Sharp.
+ *
+ * The library is what a C# `HipBackend : IComputeBackend` binds through
+ * P/Invoke ([LibraryImport("hymt_hip")], the same pattern as Vk.cs:10-25 in
+ * the reference).  It owns the HIP device, one in-order stream, a paged
+ * device-resident K/V cache per layer and the attention kernels:
+ * RoPE + per-head Q/K RMSNorm + KV append + GQA softmax(QK^T)V, for causal
+ * prefill and single-token decode.
+ *
+ * Conventions
+ *  - Every function returns an int status (hymt_status); 0 is success.  A
+ *    failing call leaves a message for hymt_last_error() in thread-local
+ *    storage.  The library never aborts the process.
+ *  - All work is ordered on the context's single stream.  Calls on one
+ *    context must come from one thread at a time, as the reference's model
+ *    is not thread-safe (README_EN.md:118).
+ *  - Arguments are plain pointers, ints and floats (blittable for P/Invoke).
+ *    Without HYMT_FLAG_DEVICE_PTRS, tensor pointers are host memory and the
+ *    call returns when the result is in host memory.  With it they are
+ *    device pointers (hymt_dev_alloc) and the call only enqueues work.
+ *  - Layouts follow the reference: q [seq][heads*head_dim],
+ *    k/v [seq][kv_heads*head_dim], out [seq][heads*head_dim], fp32, rows of
+ *    the model's flat caches are pos*kv_stride (IComputeBackend.cs:31-38).
+ */
+#ifndef HYMT_HIP_H
+#define HYMT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HYMT_ABI_VERSION 1
+
+/* Status codes.  The C# binding maps them onto the exceptions the reference
+ * backends throw (VulkanBackend.cs:80-89, 893-894, 1088-1089; Vk.cs:30-34). */
+typedef enum hymt_status {
+    HYMT_OK = 0,
+    HYMT_E_ARG = 1,         /* ArgumentException: bad pointer, size or index      */
+    HYMT_E_UNSUPPORTED = 2, /* NotSupportedException: shape or dtype not built   */
+    HYMT_E_CAPACITY = 3,    /* NotSupportedException: KV capacity exceeded       */
+    HYMT_E_NO_DEVICE = 4,   /* PlatformNotSupportedException: no usable GPU      */
+    HYMT_E_DEVICE = 5,      /* InvalidOperationException: a HIP call failed      */
+    HYMT_E_OOM = 6,         /* OutOfMemoryException: device allocation failed    */
+    HYMT_E_STATE = 7        /* InvalidOperationException: call out of order      */
+} hymt_status;
+
+/* KV cache / io element types. */
+typedef enum hymt_dtype { HYMT_F32 = 0, HYMT_F16 = 1, HYMT_BF16 = 2 } hymt_dtype;
+
+/* Tokens per KV page: the reference's Metal block size (MetalBackend.cs:49-50). */
+#define HYMT_PAGE_TOKENS 64
+
+/* hymt_create(device) value for a context with host bookkeeping only: the
+ * page table works, every call that needs the GPU returns HYMT_E_NO_DEVICE. */
+#define HYMT_DEVICE_NONE (-1)
+
+/* Tensor pointers of this call are device pointers; the call is asynchronous. */
+#define HYMT_FLAG_DEVICE_PTRS 1u
+
+typedef struct hymt_ctx hymt_ctx;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *hymt_last_error(void);
+
+/* HYMT_ABI_VERSION of the loaded library. */
+int hymt_abi_version(void);
+
+/* Number of HIP devices.  Replaces the device probe of BackendFactory's auto
+ * mode (BackendFactory.cs:29-38, VulkanBackend.IsSupported). */
+int hymt_device_count(int *count);
+
+/* Open a context on `device` (or HYMT_DEVICE_NONE).  Replaces the backend
+ * constructor (VulkanBackend.cs:80-89: throws when the device is unusable). */
+int hymt_create(int device, hymt_ctx **out);
+
+/* Free every device buffer of the context.  Replaces IDisposable.Dispose
+ * (IComputeBackend.cs:14; the model disposes it, HunyuanDenseModel.cs:815-824). */
+int hymt_destroy(hymt_ctx *ctx);
+
+/* Attention hyper-parameters from ModelConfig (ModelConfig.cs:21-51): heads,
+ * kv heads, head_dim, rope_dim, rope base (already alpha-scaled, :31-34) and
+ * the RMSNorm eps (:49).  Built shapes: head_dim 128, heads/kv_heads = 4,
+ * rope_dim even and <= head_dim.  Must precede hymt_kv_create. */
+int hymt_set_attn_config(hymt_ctx *ctx, int heads, int kv_heads, int head_dim, int rope_dim,
+                         float rope_base, float eps);
+
+/* Allocate the paged K/V cache: `layers` layers, room for `max_tokens`
+ * positions (rounded up to whole pages), elements of `kv_dtype`.  Replaces
+ * the KV part of IComputeBackend.LoadModel (MetalBackend.cs:164-181). */
+int hymt_kv_create(hymt_ctx *ctx, int layers, int max_tokens, int kv_dtype);
+
+/* Capacity in tokens, pages in the pool, pages mapped by the page table. */
+int hymt_kv_info(hymt_ctx *ctx, int *max_tokens, int *pages_total, int *pages_mapped);
+
+/* Map pages for positions [pos, pos+len) ahead of writes (the reference's
+ * EnsureWrittenRange, MetalBackend.cs:294-318).  Decode, prefill and upload
+ * map what they write themselves; this is for callers that reserve early. */
+int hymt_kv_map(hymt_ctx *ctx, int pos, int len);
+
+/* Physical page of logical block `block` (-1 when unmapped): the host copy of
+ * the page table (MetalBackend.cs:55 `_tab`). */
+int hymt_kv_page(hymt_ctx *ctx, int block, int *phys);
+
+/* Live cache length: pages that start at or after `len` return to the free
+ * list.  Replaces IComputeBackend.SetCacheLen (IComputeBackend.cs:82-87). */
+int hymt_kv_set_len(hymt_ctx *ctx, int len);
+
+/* Copy rows [pos, pos+len) of one layer from the model's flat bf16 caches
+ * (row j at k_bf16 + j*kv_stride) into the device cache, converting to the
+ * cache dtype.  Replaces IComputeBackend.UploadKv (IComputeBackend.cs:31-38). */
+int hymt_kv_upload(hymt_ctx *ctx, int layer, int pos, int len, const uint16_t *k_bf16,
+                   const uint16_t *v_bf16);
+
+/* Read rows [pos, pos+len) of one layer back as fp32 in the reference's row
+ * layout (k_out[(j-pos)*kv_stride + kvh*head_dim + d]).  Host pointers.  The
+ * debug dump of VulkanBackend.cs:909-1015 (HYMT_VK_DUMP) in a testable form. */
+int hymt_kv_read(hymt_ctx *ctx, int layer, int pos, int len, float *k_out, float *v_out);
+
+/*
+ * Decode attention for one layer at position `pos` (1 token):
+ * RoPE(q), RoPE(k) at pos -> RMSNorm q, k with qnw/knw -> append k, v at
+ * row pos (rounded to the cache dtype) -> out = softmax(q K^T / sqrt(D)) V
+ * over positions [0, pos], softmax floored at -80 as Ops.SoftmaxRow.
+ * q [heads*D], k,v [kv_heads*D], qnw [D], knw [D], out [heads*D], fp32.
+ * qnw/knw NULL skip that norm.  Rows [0, pos) must be resident.
+ * Replaces HunyuanDenseModel.DecodeAttention lines 79-95
+ * (HunyuanDenseModel.Decode.cs), i.e. the attention the Vulkan dec_attn2
+ * kernel fuses (dec_attn2.comp:1-177).
+ */
+int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const float *k,
+                     const float *v, const float *qnw, const float *knw, float *out,
+                     unsigned flags);
+
+/*
+ * Causal prefill attention for one layer: `seq` tokens at positions
+ * [pos, pos+seq), attending over [0, pos+row].  Same steps as decode; K/V of
+ * the chunk are written into the cache.  q/k/v are fp32 or bf16 as io_dtype;
+ * out is fp32.  Cache dtype f16 or bf16 (MFMA operand type); f32 caches
+ * return HYMT_E_UNSUPPORTED.  Replaces HunyuanDenseModel.PrefillAttention
+ * lines 53-83 (HunyuanDenseModel.Prefill.cs), the pf_kvprep + pf_fa32 pair
+ * of the Vulkan backend (VulkanBackend.cs:786-802).
+ */
+int hymt_attn_prefill(hymt_ctx *ctx, int layer, int pos, int seq, const void *q, const void *k,
+                      const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
+                      unsigned flags);
+
+/* Wait for all work on the context's stream. */
+int hymt_sync(hymt_ctx *ctx);
+
+/* The context's hipStream_t, for callers that time or order work around it. */
+int hymt_get_stream(hymt_ctx *ctx, void **stream);
+
+/* Device buffers for callers that keep activations resident
+ * (HYMT_FLAG_DEVICE_PTRS) and host<->device copies on the context's stream.
+ * kind: 0 host->device, 1 device->host, 2 device->device.  Copies wait for
+ * completion before returning. */
+int hymt_dev_alloc(hymt_ctx *ctx, size_t bytes, void **dptr);
+int hymt_dev_free(hymt_ctx *ctx, void *dptr);
+int hymt_memcpy(hymt_ctx *ctx, void *dst, const void *src, size_t bytes, int kind);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,131 @@
+"""Decode attention on the GPU vs the CPU oracle (HunyuanDenseModel.DecodeAttention
+restated in oracle/hymt_oracle.c).
+
+Tolerance: the north star's fp32 bound, max rel <= 1e-3 with the reference's
+own metric (AttentionTests.cs:151-164), for every KV dtype: the oracle stores
+K/V in the same dtype with the same RNE rounding, so only fp32 arithmetic
+order differs.
+"""
+import numpy as np
+import pytest
+
+from hymt2sharp_amd import BF16, F16, F32, HipBackend
+from tests.attn_cases import (BASE, D, EPS, HKV, HQ, cache_rows, max_rel, new_token,
+                              oracle_cache)
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+DT = {"f32": F32, "f16": F16, "bf16": BF16}
+
+
+def make_backend(layers, cap, dtype):
+    return HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, cap, dtype)
+
+
+def run_case(oracle, dtype, pos, norm, config=1, salt=0, outlier_frac=0.0, kscale=None, layer=0,
+             layers=1):
+    cap = pos + 1
+    kb, vb = cache_rows(config, pos, dtype_scale=kscale, salt=salt, outlier_frac=outlier_frac)
+    q, k, v, qnw, knw = new_token(config, salt, norm)
+    be = make_backend(layers, cap, dtype)
+    try:
+        if pos:
+            be.UploadKv(layer, 0, pos, kb, vb)
+        got = be.DecodeAttention(layer, pos, q[0], k[0], v[0], qnw, knw)
+        krow, vrow = be.ReadKv(layer, pos, 1)
+    finally:
+        be.Dispose()
+    ck, cv = oracle_cache(kb, vb, cap, dtype)
+    ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, dtype, HQ, HKV, D, BASE,
+                                  EPS, pos)
+    return got, ref, (krow[0], vrow[0]), (oracle.from_storage(ck[pos], dtype),
+                                          oracle.from_storage(cv[pos], dtype))
+
+
+def ulp_close(a, b, dtype):
+    """Appended rows.  f16/bf16: equal up to one unit in the last place of the
+    storage dtype (the fp32 RoPE/norm values may straddle a rounding boundary).
+    f32: within 8 fp32 ulps of the row's largest element, the cancellation
+    error of x0*c - x1*s computed in a different association order."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    if dtype == F32:
+        return bool(np.max(np.abs(a - b)) <= 8 * 2.0 ** -24 * np.max(np.abs(b)))
+    mant = {F16: 10, BF16: 7}[dtype]
+    ulp = np.maximum(np.abs(b), 6.1e-5 if dtype == F16 else 1e-30) * 2.0 ** -mant
+    return bool(np.all(np.abs(a - b) <= ulp * 1.0001))
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("norm", [None, "ones"])
+def test_config1_decode_513(oracle, hip_available, dtype, norm):
+    """Config 1: one layer, cache of 512 + token at 512, fp32 (literal) and bf16 (reference)."""
+    dt = DT[dtype]
+    got, ref, (kr, vr), (kr_ref, vr_ref) = run_case(oracle, dt, 512, norm, config=1)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+    assert ulp_close(kr, kr_ref, dt) and ulp_close(vr, vr_ref, dt)
+
+
+@pytest.mark.parametrize("layer", [0, 31])
+def test_config2_decode_4097_fp16(oracle, hip_available, layer):
+    """Config 2 layer: fp16 KV, pos 4096, QK RMSNorm with gamma ~ U(0.9, 1.1)."""
+    got, ref, (kr, vr), (kr_ref, vr_ref) = run_case(oracle, F16, 4096, "gamma", config=2,
+                                                    salt=layer, layer=layer, layers=32)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+    assert ulp_close(kr, kr_ref, F16) and ulp_close(vr, vr_ref, F16)
+
+
+@pytest.mark.parametrize("L", [1024, 4096, 16384, 32768])
+def test_config5_long_context_outliers(oracle, hip_available, L):
+    """Config 5: K ~ N(0,1) with 0.1% of positions x30 (peaked logits), fp16 KV."""
+    got, ref, _, _ = run_case(oracle, F16, L - 1, None, config=5, kscale=1.0, outlier_frac=0.001)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("pos", [0, 1, 62, 63, 64, 65, 127, 128, 200, 8191, 8192, 8250])
+def test_decode_edges(oracle, hip_available, dtype, pos):
+    """Page boundaries, a single position, and the multi-page splits past 8192."""
+    dt = DT[dtype]
+    got, ref, (kr, vr), (kr_ref, vr_ref) = run_case(oracle, dt, pos, "gamma", config=7, salt=pos)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+    assert ulp_close(kr, kr_ref, dt) and ulp_close(vr, vr_ref, dt)
+
+
+def test_decode_chain_matches_oracle(oracle, hip_available):
+    """Decode steps appending one token each (the Forward([token]) loop):
+    every step's output and the whole cache match the oracle run step by step."""
+    steps = 70
+    be = make_backend(1, steps, F32)
+    ck, cv = oracle_cache(np.zeros((0, HKV * D), np.uint16), np.zeros((0, HKV * D), np.uint16),
+                          steps, F32)
+    worst = 0.0
+    try:
+        for p in range(steps):
+            q, k, v, qnw, knw = new_token(8, p, "gamma")
+            got = be.DecodeAttention(0, p, q[0], k[0], v[0], qnw, knw)
+            ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, F32, HQ, HKV, D,
+                                          BASE, EPS, p)
+            worst = max(worst, max_rel(got, ref))
+        kd, vd = be.ReadKv(0, 0, steps)
+    finally:
+        be.Dispose()
+    assert worst <= TOL, worst
+    assert all(ulp_close(kd[p], ck[p], F32) for p in range(steps))
+    assert np.array_equal(vd, cv)
+
+
+def test_decode_repeat_is_deterministic(hip_available):
+    """Re-running the same step (same pos) rewrites the same row and gives
+    the same output bit for bit (the split merge order is fixed)."""
+    kb, vb = cache_rows(9, 3000)
+    q, k, v, qnw, knw = new_token(9, 0, "gamma")
+    be = make_backend(1, 3001, F16)
+    try:
+        be.UploadKv(0, 0, 3000, kb, vb)
+        a = be.DecodeAttention(0, 3000, q[0], k[0], v[0], qnw, knw)
+        b = be.DecodeAttention(0, 3000, q[0], k[0], v[0], qnw, knw)
+    finally:
+        be.Dispose()
+    assert np.array_equal(a, b)

@@ -1,0 +1,142 @@
+"""Prefill attention on the GPU (bf16/f16 MFMA) vs the CPU oracle
+(HunyuanDenseModel.PrefillAttention with Forward's 1024-token chunking,
+restated in oracle/hymt_oracle.c), and vs an fp64 model of the kernel's
+rounding points (tests/mfma_model.py).
+
+Stated bound for the MFMA path against the fp32 oracle.  The kernel rounds
+q (after RoPE/norm and the log2(e)/sqrt(D) scale) and the softmax weights P
+to the operand type, unit roundoff u = 2^-9 (bf16) or 2^-11 (f16); K and V
+are stored in the cache dtype identically on both sides.  Rounding P moves
+each output by at most u * max|V| (the weights sum to 1); rounding q moves
+the logits by u * sum|q_d k_d| * scale, which for RMS-normalised q and k is a
+few u and enters the output through the same weights.  The tests assert
+  max |a - b|  <= 4 u max|V|     and     mean |a - b| <= u mean|V|
+and report the reference's metric rel = |a-b| / max(1e-3, |a|, |b|)
+(AttentionTests.cs:151-164) alongside.  Against the rounding model the GPU
+must agree to mean |a - b| <= 1% of its distance from the oracle and
+max |a - b| <= u max|V| (a single p landing on the other side of a rounding
+boundary).
+"""
+import numpy as np
+import pytest
+
+from hymt2sharp_amd import BF16, F16, HipBackend
+from hymt2sharp_amd import synth as S
+from tests.attn_cases import (BASE, D, EPS, HKV, HQ, cache_rows, max_rel, new_token,
+                              oracle_cache)
+from tests.mfma_model import prefill_model
+
+pytestmark = pytest.mark.gpu
+
+U = {BF16: 2.0 ** -9, F16: 2.0 ** -11}
+
+
+def make_backend(layers, cap, dtype):
+    return HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, cap, dtype)
+
+
+def check(got, ref, vals_v, dtype, model=None):
+    """Stated MFMA bound against the oracle; tight agreement with the model."""
+    got = np.asarray(got, np.float64)
+    u = U[dtype]
+    vmax, vmean = float(np.max(np.abs(vals_v))), float(np.mean(np.abs(vals_v)))
+    d = np.abs(got - ref)
+    assert d.max() <= 4 * u * vmax and d.mean() <= u * vmean, (d.max(), d.mean(), max_rel(got, ref))
+    if model is not None:
+        dm = np.abs(got - model)
+        assert dm.mean() <= 0.01 * d.mean() + 1e-9 and dm.max() <= u * vmax, (dm.mean(), dm.max())
+    return max_rel(got, ref), d.max()
+
+
+def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, with_model=True):
+    kb, vb = cache_rows(config, pos, salt=salt)
+    q, k, v, qnw, knw = new_token(config, salt, norm, seq=seq)
+    if io_bf16:  # bf16 inputs: both sides see the same bf16-representable values
+        q, k, v = (S.bf16_bits_to_f32(S.f32_to_bf16_bits(x)).reshape(x.shape) for x in (q, k, v))
+    cap = pos + seq
+    be = make_backend(1, cap, dtype)
+    try:
+        if pos:
+            be.UploadKv(0, 0, pos, kb, vb)
+        if io_bf16:
+            got = be.PrefillAttention(0, pos, S.f32_to_bf16_bits(q), S.f32_to_bf16_bits(k),
+                                      S.f32_to_bf16_bits(v), qnw, knw, io_dtype=BF16)
+        else:
+            got = be.PrefillAttention(0, pos, q, k, v, qnw, knw)
+        kd, vd = be.ReadKv(0, pos, seq)
+    finally:
+        be.Dispose()
+    ck, cv = oracle_cache(kb, vb, cap, dtype)
+    ref = oracle.prefill_attention(q, k, v, qnw, knw, ck, cv, dtype, HQ, HKV, D, BASE, EPS, pos,
+                                   threads=8)
+    kf, vf = oracle.from_storage(ck, dtype), oracle.from_storage(cv, dtype)
+    model = None
+    if with_model:
+        qh = oracle.neox_rope(q.reshape(seq, HQ, D), pos, BASE)
+        if qnw is not None:
+            qh = oracle.rmsnorm(qh, qnw, EPS)
+        model = prefill_model(qh.reshape(seq, HQ * D), kf, vf, HQ, HKV, D, pos, seq, dtype)
+    return got, ref, model, vf, (kd, vd), (kf[pos:pos + seq], vf[pos:pos + seq])
+
+
+def test_config3_prefill_2048_bf16(oracle, hip_available):
+    """Config 3: 2048 tokens at positions 0..2047, bf16 inputs, bf16 cache."""
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, BF16, 0, 2048, None, 3,
+                                                              io_bf16=True)
+    check(got, ref, vf, BF16, model)
+    assert np.array_equal(vd, vref)
+    assert max_rel(kd, kref) <= 2.0 ** -7
+
+
+def test_config4_chunk_256_over_8192_fp16(oracle, hip_available):
+    """Config 4: 256 new tokens at 8192..8447 over an 8192-position fp16 cache
+    (kv range split over several workgroups, then merged)."""
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, F16, 8192, 256, None, 4)
+    check(got, ref, vf, F16, model)
+    assert np.array_equal(vd, vref)
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("pos,seq", [(0, 1), (0, 31), (0, 33), (0, 64), (0, 100), (37, 29),
+                                     (64, 64), (100, 300), (1000, 1100)])
+def test_prefill_shapes(oracle, hip_available, dtype, pos, seq):
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, dtype, pos, seq, "gamma", 11,
+                                                              salt=pos + seq)
+    check(got, ref, vf, dtype, model)
+    assert np.array_equal(vd, vref)
+
+
+def test_decode_equals_prefill_row(oracle, hip_available):
+    """Benchmark --verify-prefill invariant (Benchmark/Program.cs:124-145):
+    decoding token p over a cache of p rows equals row p of a prefill, up to
+    the MFMA bound (decode keeps q and P in fp32)."""
+    seq = 200
+    q, k, v, qnw, knw = new_token(12, 0, "gamma", seq=seq)
+    be = make_backend(2, seq, BF16)
+    try:
+        pf = be.PrefillAttention(0, 0, q, k, v, qnw, knw)
+        be.PrefillAttention(1, 0, q[:seq - 1], k[:seq - 1], v[:seq - 1], qnw, knw)
+        dec = be.DecodeAttention(1, seq - 1, q[seq - 1], k[seq - 1], v[seq - 1], qnw, knw)
+        _, vf = be.ReadKv(1, 0, seq)
+    finally:
+        be.Dispose()
+    check(pf[seq - 1], dec, vf, BF16)
+
+
+def test_chunked_equals_monolithic(hip_available):
+    """Prefill in chunks over the cache the earlier chunks wrote equals one
+    call (the 1024-chunking argument of HunyuanDenseModel.cs:344-347), up to
+    the different split points of the online softmax (P rounding)."""
+    seq = 700
+    q, k, v, qnw, knw = new_token(13, 0, "gamma", seq=seq)
+    be = make_backend(2, seq, BF16)
+    try:
+        mono = be.PrefillAttention(0, 0, q, k, v, qnw, knw)
+        parts = [be.PrefillAttention(1, a, q[a:b], k[a:b], v[a:b], qnw, knw)
+                 for a, b in ((0, 256), (256, 300), (300, 700))]
+        k0, v0 = be.ReadKv(0, 0, seq)
+        k1, v1 = be.ReadKv(1, 0, seq)
+    finally:
+        be.Dispose()
+    check(np.concatenate(parts), mono, v0, BF16)
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
