@@ -13,10 +13,18 @@ constexpr int kGroup = 4;       // q heads per kv head (16 / 4)
 constexpr int kPage = 64;       // tokens per KV page
 constexpr int kMaxSplits = 128; // decode KV splits per kv head (merge width)
 
-// Paged pool addressing, per layer:
-//   K  element ((phys*Hkv + kvh)*64 + t)*D + d      (row-major rows of one head)
-//   V  element ((phys*Hkv + kvh)*D + d)*64 + t      (transposed: 64 positions per d)
-// The V transpose gives the P*V MFMA operand 8 consecutive positions per lane.
+// Paged pool addressing, per layer.  A page holds 64 positions of one kv head
+// for K and for V (16 KiB each in f16/bf16):
+//   K  element  page_base + t*D + d                      (row-major rows)
+//   V  element  page_base + ((t/16)*D + d)*16 + t%16     (transposed in
+//               16-position sub-tiles: [4][D][16])
+//   page_base = (phys*Hkv + kvh) * 64 * D
+// The transposed V gives the P*V MFMA operand 8 consecutive positions per
+// lane (prefill); the 16-position sub-tiles keep one decode wave's share of a
+// page (16 positions x 128 dims) one contiguous 4 KiB block.
+__host__ __device__ inline size_t v_off(int t, int d) {
+    return ((size_t)(t >> 4) * kHeadDim + d) * 16 + (t & 15);
+}
 
 struct DecodeArgs {
     const float *q;     // [Hq*D]
@@ -41,6 +49,7 @@ struct DecodeArgs {
     int ppw;            // pages per split
     float eps;
     float qscale;       // log2(e) / sqrt(D)
+    int merge_inline;   // 1: last workgroup merges splits; 0: decode_merge_kernel
 };
 
 struct PrepArgs {

@@ -93,6 +93,34 @@ template <int WIDTH> __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Sum over each row of 16 lanes with DPP (quad_perm xor 1, xor 2, then
+// half-row and row mirrors); every lane of the row receives the sum.
+__device__ __forceinline__ float dpp_sum16(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    return v;
+}
+// Sum over groups of 2 / 4 consecutive lanes (quad_perm).
+__device__ __forceinline__ float dpp_sum2(float v) {
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_sum4(float v) {
+    v = dpp_sum2(v);
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+// Sum over WIDTH consecutive lanes (WIDTH in 2, 4, 16, 32, 64): DPP inside a
+// 16-lane row, a lane shuffle across rows.
+template <int WIDTH> __device__ __forceinline__ float lane_sum(float v) {
+    if constexpr (WIDTH == 2) return dpp_sum2(v);
+    if constexpr (WIDTH == 4) return dpp_sum4(v);
+    v = dpp_sum16(v);
+#pragma unroll
+    for (int o = 16; o < WIDTH; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
 // log2(e) and the softmax floor of Ops.SoftmaxRow (exp(max(x - max, -80)),
 // Ops.cs:231,245,256) in base-2 units.
 constexpr float kLog2e = 1.4426950408889634f;

@@ -104,8 +104,9 @@ struct hymt_ctx {
     int rope_cap = 0;
     DevBuf rope_cos, rope_sin;
 
-    // decode workspace
+    // decode workspace; splits merged in-kernel (1) or by a second launch (0)
     DevBuf dec_ml, dec_acc, dec_cnt;
+    int decode_merge_inline = 1;
     // prefill workspace
     DevBuf qp, part_o, part_ml;
     // staging for host-pointer calls
@@ -233,6 +234,8 @@ int hymt_create(int device, hymt_ctx **out) {
         }
         HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
         c->device = device;
+        if (const char *m = std::getenv("HYMT_HIP_DECODE_MERGE"))
+            c->decode_merge_inline = std::strcmp(m, "kernel") != 0;
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -449,6 +452,7 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         a.nsplit = (npages + a.ppw - 1) / a.ppw;
         a.eps = c->eps;
         a.qscale = 1.4426950408889634f / sqrtf((float)D);
+        a.merge_inline = c->decode_merge_inline;
         HIP_TRY(launch_decode(c->kv_dtype, a, c->stream));
         if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
     } catch (const HipError &e) {

@@ -82,9 +82,9 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(PrepArgs a) {
         } else {
             const int h = row - Hq - Hkv;
             const size_t off = (size_t)m * Hkv * D + (size_t)h * D;
-            S *vp = (S *)a.vpool + ((size_t)phys * Hkv + h) * (size_t)(P * D) + t;
-            vp[(size_t)lane * P] = to_elem<T>(load(a.v, off + lane));
-            vp[(size_t)(lane + 64) * P] = to_elem<T>(load(a.v, off + lane + 64));
+            S *vp = (S *)a.vpool + ((size_t)phys * Hkv + h) * (size_t)(P * D);
+            vp[v_off(t, lane)] = to_elem<T>(load(a.v, off + lane));
+            vp[v_off(t, lane + 64)] = to_elem<T>(load(a.v, off + lane + 64));
         }
     }
 }
@@ -217,7 +217,8 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
             const int idx = tid + 256 * j;
             rk[j] = *(const uint4 *)(kp + (size_t)idx * 8);
             uint4 v = *(const uint4 *)(vp + (size_t)idx * 8);
-            const int col0 = (idx % 8) * 8;
+            // idx -> sub-tile idx/256, d (idx%256)/2, positions 16*sub + 8*(idx%2) + [0,8)
+            const int col0 = (idx / 256) * 16 + (idx % 2) * 8;
             if (col0 + 8 > nvalid) {  // zero V^T entries of unwritten positions
                 uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -236,8 +237,8 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
             const int idx = tid + 256 * j;
             const int kr = idx / 16, kc = idx % 16;
             *(uint4 *)(&sK[buf][kswz(kr) * KLD + kc * 8]) = rk[j];
-            const int vr = idx / 8, vc = idx % 8;
-            *(uint4 *)(&sV[buf][vr * VLD + vc * 8]) = rv[j];
+            const int vr = (idx % 256) / 2, vcol = (idx / 256) * 16 + (idx % 2) * 8;
+            *(uint4 *)(&sV[buf][vr * VLD + vcol]) = rv[j];
         }
     };
 

@@ -13,7 +13,7 @@ few u and enters the output through the same weights.  The tests assert
   max |a - b|  <= 4 u max|V|     and     mean |a - b| <= u mean|V|
 and report the reference's metric rel = |a-b| / max(1e-3, |a|, |b|)
 (AttentionTests.cs:151-164) alongside.  Against the rounding model the GPU
-must agree to mean |a - b| <= 1% of its distance from the oracle and
+must agree to mean |a - b| <= 10% of its distance from the oracle and
 max |a - b| <= u max|V| (a single p landing on the other side of a rounding
 boundary).
 """
@@ -44,7 +44,7 @@ def check(got, ref, vals_v, dtype, model=None):
     assert d.max() <= 4 * u * vmax and d.mean() <= u * vmean, (d.max(), d.mean(), max_rel(got, ref))
     if model is not None:
         dm = np.abs(got - model)
-        assert dm.mean() <= 0.01 * d.mean() + 1e-9 and dm.max() <= u * vmax, (dm.mean(), dm.max())
+        assert dm.mean() <= 0.1 * d.mean() and dm.max() <= u * vmax, (dm.mean(), dm.max())
     return max_rel(got, ref), d.max()
 
 
