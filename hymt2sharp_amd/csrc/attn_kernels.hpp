@@ -12,6 +12,7 @@ constexpr int kHeadDim = 128;   // built head_dim (Hy-MT2-1.8B)
 constexpr int kGroup = 4;       // q heads per kv head (16 / 4)
 constexpr int kPage = 64;       // tokens per KV page
 constexpr int kMaxSplits = 128; // decode KV splits per kv head (merge width)
+constexpr int kArgPages = 256;  // decode page lists passed in kernel arguments
 
 // Paged pool addressing, per layer.  A page holds 64 positions of one kv head
 // for K and for V (16 KiB each in f16/bf16):
@@ -50,6 +51,9 @@ struct DecodeArgs {
     float eps;
     float qscale;       // log2(e) / sqrt(D)
     int merge_inline;   // 1: last workgroup merges splits; 0: decode_merge_kernel
+    int pages_in_args;  // 1: pages[] below holds tab[0, npages) (npages <= kArgPages)
+    int32_t pages[kArgPages];  // physical page of each logical block, saving a
+                               // dependent table load before the K/V stream
 };
 
 struct PrepArgs {

@@ -106,7 +106,7 @@ struct hymt_ctx {
 
     // decode workspace; splits merged in-kernel (1) or by a second launch (0)
     DevBuf dec_ml, dec_acc, dec_cnt;
-    int decode_merge_inline = 1;
+    int decode_merge_inline = 0;
     // prefill workspace
     DevBuf qp, part_o, part_ml;
     // staging for host-pointer calls
@@ -235,7 +235,7 @@ int hymt_create(int device, hymt_ctx **out) {
         HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
         c->device = device;
         if (const char *m = std::getenv("HYMT_HIP_DECODE_MERGE"))
-            c->decode_merge_inline = std::strcmp(m, "kernel") != 0;
+            c->decode_merge_inline = std::strcmp(m, "inline") == 0;
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -447,12 +447,17 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         a.rope_half = half;
         a.rope_dim = c->rope_dim;
         const int npages = (a.L + kPage - 1) / kPage;
-        a.ppw = (npages + kMaxSplits - 1) / kMaxSplits;
+        // two pages per split once there are enough pages: half the partials
+        // to merge at the same streaming time (both pages' loads issue at once)
+        a.ppw = std::max(npages >= 32 ? 2 : 1, (npages + kMaxSplits - 1) / kMaxSplits);
         if (const char *s = std::getenv("HYMT_HIP_DECODE_PPW")) a.ppw = std::max(a.ppw, atoi(s));
         a.nsplit = (npages + a.ppw - 1) / a.ppw;
         a.eps = c->eps;
         a.qscale = 1.4426950408889634f / sqrtf((float)D);
         a.merge_inline = c->decode_merge_inline;
+        a.pages_in_args = npages <= kArgPages;
+        if (a.pages_in_args)
+            for (int b = 0; b < npages; b++) a.pages[b] = c->pages.phys(b);
         HIP_TRY(launch_decode(c->kv_dtype, a, c->stream));
         if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
     } catch (const HipError &e) {
