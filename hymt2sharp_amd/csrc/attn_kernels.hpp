@@ -57,31 +57,34 @@ struct DecodeArgs {
 };
 
 struct PrepArgs {
-    const void *q;      // [seq][Hq*D]   fp32 or bf16
-    const void *k;      // [seq][Hkv*D]
+    const void *k;      // [seq][Hkv*D]   fp32 or bf16 (io_bf16)
     const void *v;
-    const float *qnw, *knw;
+    const float *knw;   // [D] or null
     const float *rope_cos; // table base [cap][rope_half]
     const float *rope_sin;
     const int32_t *tab;
     void *kpool, *vpool;
-    void *qp;           // out: [Hq][seq_pad][D] MFMA-typed q, scaled by qscale
-    int pos0, seq, seq_pad;
-    int heads, kv_heads;
+    int pos0, seq;
+    int kv_heads;
     int rope_half, rope_dim;
     int io_bf16;
-    float eps, qscale;
+    float eps;
 };
 
 struct FlashArgs {
-    const void *qp;     // [Hq][seq_pad][D]
+    const void *q;      // [seq][Hq*D]    fp32 or bf16 (io_bf16), before RoPE/norm
+    const float *qnw;   // [D] or null
+    const float *rope_cos, *rope_sin;  // table base [cap][rope_half]
     const int32_t *tab;
     const void *kpool, *vpool;
     float *out;         // [seq][Hq*D]
-    float *part_o;      // [items][G][32][D]  (split items only)
-    float *part_ml;     // [items][G][32][2]
-    int pos0, seq, seq_pad;
+    float *part_o;      // [Hkv*items][G][32][D]  (split items only)
+    float *part_ml;     // [Hkv*items][G][32][2]
+    int pos0, seq;
     int heads, kv_heads;
+    int rope_half, rope_dim;  // rope_dim in {0, 64, 128}
+    int io_bf16;
+    float eps, qscale;  // qscale = log2(e) / sqrt(D)
     int nqb;            // q blocks of 32 rows
     int cap;            // max kv tiles per work item
     int items_per_kvh;  // work items per kv head

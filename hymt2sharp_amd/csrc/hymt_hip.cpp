@@ -108,7 +108,7 @@ struct hymt_ctx {
     DevBuf dec_ml, dec_acc, dec_cnt;
     int decode_merge_inline = 0;
     // prefill workspace
-    DevBuf qp, part_o, part_ml;
+    DevBuf part_o, part_ml;
     // staging for host-pointer calls
     DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
     HostBuf h_in, h_out;
@@ -250,7 +250,7 @@ int hymt_destroy(hymt_ctx *c) {
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
         for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->dec_ml,
-                          &c->dec_acc, &c->dec_cnt, &c->qp, &c->part_o, &c->part_ml, &c->in_q,
+                          &c->dec_acc, &c->dec_cnt, &c->part_o, &c->part_ml, &c->in_q,
                           &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v})
             b->release();
         c->h_in.release();
@@ -477,6 +477,8 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         return fail(HYMT_E_ARG, "invalid prefill arguments");
     if (c->kv_dtype == HYMT_F32)
         return fail(HYMT_E_UNSUPPORTED, "prefill runs on bf16/f16 MFMA; f32 KV cache has no prefill path");
+    if (c->rope_dim % 64)
+        return fail(HYMT_E_UNSUPPORTED, "prefill built for rope_dim 0, 64 or 128");
     if ((long)pos + seq > c->pages.max_tokens())
         return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
                                          " exceeded at " + std::to_string((long)pos + seq));
@@ -495,45 +497,43 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
                          {qnw, D * 4, &c->in_qnw}, {knw, D * 4, &c->in_knw}});
             c->out_o.reserve(qn * 4);
         }
-        const int seq_pad = (seq + 31) / 32 * 32;
-        c->qp.reserve((size_t)c->heads * seq_pad * D * 2);
-
         PrepArgs p;
-        p.q = dev ? q : c->in_q.p;
         p.k = dev ? k : c->in_k.p;
         p.v = dev ? v : c->in_v.p;
-        p.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
         p.knw = !knw ? nullptr : dev ? knw : (const float *)c->in_knw.p;
         p.rope_cos = (const float *)c->rope_cos.p;
         p.rope_sin = (const float *)c->rope_sin.p;
         p.tab = (const int32_t *)c->tab.p;
         p.kpool = c->klayer(layer);
         p.vpool = c->vlayer(layer);
-        p.qp = c->qp.p;
         p.pos0 = pos;
         p.seq = seq;
-        p.seq_pad = seq_pad;
-        p.heads = c->heads;
         p.kv_heads = c->kv_heads;
         p.rope_half = c->rope_dim / 2;
         p.rope_dim = c->rope_dim;
         p.io_bf16 = io_dtype == HYMT_BF16;
         p.eps = c->eps;
-        p.qscale = 1.4426950408889634f / sqrtf((float)D);
         HIP_TRY(launch_prefill_prep(c->kv_dtype, p, c->stream));
 
         FlashArgs f;
-        f.qp = c->qp.p;
+        f.q = dev ? q : c->in_q.p;
+        f.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
+        f.rope_cos = (const float *)c->rope_cos.p;
+        f.rope_sin = (const float *)c->rope_sin.p;
         f.tab = (const int32_t *)c->tab.p;
         f.kpool = c->klayer(layer);
         f.vpool = c->vlayer(layer);
         f.out = dev ? out : (float *)c->out_o.p;
         f.pos0 = pos;
         f.seq = seq;
-        f.seq_pad = seq_pad;
         f.heads = c->heads;
         f.kv_heads = c->kv_heads;
-        f.nqb = seq_pad / 32;
+        f.rope_half = c->rope_dim / 2;
+        f.rope_dim = c->rope_dim;
+        f.io_bf16 = io_dtype == HYMT_BF16;
+        f.eps = c->eps;
+        f.qscale = 1.4426950408889634f / sqrtf((float)D);
+        f.nqb = (seq + 31) / 32;
         // Work items: split the kv range of q blocks only when there are too
         // few (kv head, q block) pairs to fill the GPU.
         int max_tiles = 0;

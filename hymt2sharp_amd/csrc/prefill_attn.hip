@@ -6,15 +6,17 @@
 // (Ops.cs:198-221, 359-455, 535-595), as the Vulkan pf_kvprep + pf_fa32 pair
 // does on other GPUs (pf_kvprep.comp, pf_fa32.comp).
 //
-// Three kernels:
-//  prefill_prep   one workgroup per token: RoPE/norm q and k, write k and v
-//                 into the paged cache (cache dtype), write q in the MFMA
-//                 operand type pre-scaled by log2(e)/sqrt(D).
+// Kernels:
+//  prefill_kv     one workgroup per (16-position block, kv head): RoPE + norm
+//                 of k, k and v rounded into the paged cache (v transposed
+//                 through LDS into the 16-position V^T sub-tiles).
 //  prefill_flash  one workgroup per (kv head, 32-row q block, kv tile range):
-//                 4 waves = the 4 q heads of the GQA group sharing every
-//                 K/V tile staged in LDS.  S^T = K Q^T and O^T += V^T P^T on
-//                 v_mfma_f32_16x16x32_{bf16,f16}, single-pass online
-//                 softmax in base 2 with the reference's -80 floor.
+//                 4 waves = the 4 q heads of the GQA group sharing every K/V
+//                 tile staged in LDS.  The prologue applies RoPE + norm to the
+//                 wave's 32 q rows straight into MFMA operand registers.
+//                 S^T = K Q^T and O^T += V^T P^T on
+//                 v_mfma_f32_16x16x32_{bf16,f16}; single-pass online softmax
+//                 in base 2 with the reference's -80 floor.
 //  prefill_merge  combines the (m, l, O) partials of q blocks whose kv range
 //                 was split over several workgroups (long cached prefixes).
 #include "attn_kernels.hpp"
@@ -26,74 +28,137 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// ------------------------------------------------------------------ prep
+// Cross-row (16-lane) reductions with the gfx950 permlane swaps.
+__device__ __forceinline__ float pf_xrow_sum(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pf_xrow_max(float v) {
+    auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Two floats to the MFMA operand type, packed (v_cvt_pk_{bf16,f16}_f32, RNE).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float x, float y);
+template <> __device__ __forceinline__ uint32_t pack2<BF16>(float x, float y) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    v2 r;
+    r[0] = (__bf16)x;
+    r[1] = (__bf16)y;
+    return __builtin_bit_cast(uint32_t, r);
+}
+template <> __device__ __forceinline__ uint32_t pack2<F16>(float x, float y) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    v2 r;
+    r[0] = (_Float16)x;
+    r[1] = (_Float16)y;
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// Load 8 consecutive input elements (fp32 or bf16 bits) as fp32.
+__device__ __forceinline__ void load8_in(const void *base, size_t i, bool bf16, float *o) {
+    if (bf16) {
+        const uint4 u = *(const uint4 *)((const uint16_t *)base + i);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            o[2 * e] = __uint_as_float(w[e] << 16);
+            o[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 a = *(const float4 *)((const float *)base + i);
+        const float4 b = *(const float4 *)((const float *)base + i + 4);
+        o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+        o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+    }
+}
+
+// ------------------------------------------------------------------ k/v
+// Block (16-position block tb, kv head); thread (row = tid/16, dims 8*(tid%16)..).
 template <typename T>
-__global__ __launch_bounds__(256) void prefill_prep_kernel(PrepArgs a) {
+__global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     constexpr int D = kHeadDim, P = kPage;
     using S = typename T::storage;
-    const int m = blockIdx.x;
-    const int pos = a.pos0 + m;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int Hq = a.heads, Hkv = a.kv_heads;
-    const float *cs = a.rope_cos + (size_t)pos * a.rope_half;
-    const float *sn = a.rope_sin + (size_t)pos * a.rope_half;
-    const int phys = a.tab[pos / P], t = pos % P;
-
-    auto load = [&](const void *base, size_t i) -> float {
-        return a.io_bf16 ? bf16_to_f32(((const uint16_t *)base)[i]) : ((const float *)base)[i];
-    };
-
-    for (int row = wave; row < Hq + 2 * Hkv; row += 4) {
-        if (row < Hq + Hkv) {
-            const bool isq = row < Hq;
-            const int h = isq ? row : row - Hq;
-            const void *src = isq ? a.q : a.k;
-            const size_t off = (size_t)m * (isq ? Hq : Hkv) * D + (size_t)h * D;
-            float y[2];
+    __shared__ float s_x[16][D];
+    __shared__ __attribute__((aligned(16))) S s_v[16][D];
+    const int kvh = blockIdx.y, Hkv = a.kv_heads;
+    const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
+    const int pstart = (a.pos0 & ~15) + 16 * blockIdx.x;  // 16-aligned block start
+    const int pos = pstart + r, m = pos - a.pos0;
+    const bool valid = m >= 0 && m < a.seq;
+    const int phys = a.tab[pstart / P];
+    const size_t page_base = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
+    const int t = pstart % P + r;  // row within the page
+    float x[8], v[8];
+    if (valid) {
+        load8_in(a.k, (size_t)m * Hkv * D + (size_t)kvh * D + 8 * c, a.io_bf16, x);
+        load8_in(a.v, (size_t)m * Hkv * D + (size_t)kvh * D + 8 * c, a.io_bf16, v);
+    } else {
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int d = lane + 64 * e;
-                const float x = load(src, off + d);
-                if (d < a.rope_half) {
-                    y[e] = x * cs[d] - load(src, off + d + a.rope_half) * sn[d];
-                } else if (d < a.rope_dim) {
-                    const int i = d - a.rope_half;
-                    y[e] = load(src, off + i) * sn[i] + x * cs[i];
-                } else {
-                    y[e] = x;
-                }
-            }
-            const float *w = isq ? a.qnw : a.knw;
-            if (w) {
-                float ss = group_sum<64>(y[0] * y[0] + y[1] * y[1]);
-                float r = 1.0f / sqrtf(ss / (float)D + a.eps);
-                y[0] = y[0] * r * w[lane];
-                y[1] = y[1] * r * w[lane + 64];
-            }
-            if (isq) {
-                S *qp = (S *)a.qp + ((size_t)h * a.seq_pad + m) * D;
-                qp[lane] = to_elem<T>(y[0] * a.qscale);
-                qp[lane + 64] = to_elem<T>(y[1] * a.qscale);
-            } else {
-                S *kp = (S *)a.kpool + ((size_t)phys * Hkv + h) * (size_t)(P * D) + (size_t)t * D;
-                kp[lane] = to_elem<T>(y[0]);
-                kp[lane + 64] = to_elem<T>(y[1]);
-            }
+        for (int e = 0; e < 8; e++) x[e] = v[e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) s_x[r][8 * c + e] = x[e];
+    __syncthreads();
+    // RoPE (Ops.RopeRange, Ops.cs:157-165) then RMSNorm of the k row
+    const int half = a.rope_half;
+    const float *cs = a.rope_cos + (size_t)(valid ? pos : 0) * half;
+    const float *sn = a.rope_sin + (size_t)(valid ? pos : 0) * half;
+    float y[8], ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int d = 8 * c + e;
+        if (d < half) y[e] = x[e] * cs[d] - s_x[r][d + half] * sn[d];
+        else if (d < a.rope_dim) y[e] = s_x[r][d - half] * sn[d - half] + x[e] * cs[d - half];
+        else y[e] = x[e];
+        ss += y[e] * y[e];
+    }
+    if (a.knw) {
+        ss = dpp_sum16(ss);
+        const float rr = 1.0f / sqrtf(ss / (float)D + a.eps);
+#pragma unroll
+        for (int e = 0; e < 8; e++) y[e] = y[e] * rr * a.knw[8 * c + e];
+    }
+    if (valid) {
+        S ks[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) ks[e] = to_elem<T>(y[e]);
+        S *dst = (S *)a.kpool + page_base + (size_t)t * D + 8 * c;
+#pragma unroll
+        for (int e = 0; e < 8; e++) dst[e] = ks[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) s_v[r][8 * c + e] = to_elem<T>(v[e]);
+    __syncthreads();
+    // V^T sub-tile [d][16]: thread -> (d = tid/2, positions 8*(tid%2) + [0,8))
+    {
+        const int d = tid >> 1, h8 = (tid & 1) * 8;
+        S *dst = (S *)a.vpool + page_base + v_off(pstart % P, d) + h8;
+        const int m0 = pstart + h8 - a.pos0;
+        if (m0 >= 0 && m0 + 8 <= a.seq) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)s_v[h8 + 2 * e][d] | ((uint32_t)s_v[h8 + 2 * e + 1][d] << 16);
+            *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
-            const int h = row - Hq - Hkv;
-            const size_t off = (size_t)m * Hkv * D + (size_t)h * D;
-            S *vp = (S *)a.vpool + ((size_t)phys * Hkv + h) * (size_t)(P * D);
-            vp[v_off(t, lane)] = to_elem<T>(load(a.v, off + lane));
-            vp[v_off(t, lane + 64)] = to_elem<T>(load(a.v, off + lane + 64));
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (m0 + e >= 0 && m0 + e < a.seq) dst[e] = s_v[h8 + e][d];
         }
     }
 }
 
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
-    dim3 grid(a.seq), block(256);
+    const int first = a.pos0 & ~15, last = a.pos0 + a.seq - 1;
+    dim3 grid((last - first) / 16 + 1, a.kv_heads), block(256);
     switch (kv_dtype) {
-    case 1: hipLaunchKernelGGL(prefill_prep_kernel<F16>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(prefill_prep_kernel<BF16>, grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL(prefill_kv_kernel<F16>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(prefill_kv_kernel<BF16>, grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -157,8 +222,21 @@ __device__ __forceinline__ int krow(int kb, int r) {
     return 32 * (kb >> 1) + 8 * (r >> 2) + 4 * (kb & 1) + (r & 3);
 }
 
+// Zero the 16-bit elements of an 8-position V^T chunk starting at column
+// col0 whose position is >= nvalid (unwritten cache rows may hold any bits).
+__device__ __forceinline__ uint4 vmask(uint4 v, int col0, int nvalid) {
+    const int k = nvalid - col0;  // elements kept
+    if (k >= 8) return v;
+    if (k <= 0) return make_uint4(0, 0, 0, 0);
+    const uint32_t keep[4] = {k >= 2 ? 0xFFFFFFFFu : k == 1 ? 0x0000FFFFu : 0u,
+                              k >= 4 ? 0xFFFFFFFFu : k == 3 ? 0x0000FFFFu : 0u,
+                              k >= 6 ? 0xFFFFFFFFu : k == 5 ? 0x0000FFFFu : 0u,
+                              k == 7 ? 0x0000FFFFu : 0u};
+    return make_uint4(v.x & keep[0], v.y & keep[1], v.z & keep[2], v.w & keep[3]);
+}
+
 template <typename T>
-__global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
+__global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
     constexpr int KLD = D + 8;  // 272-byte K rows
     constexpr int VLD = P + 8;  // 144-byte V^T rows
@@ -180,17 +258,107 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
     const FlashItem it = flash_item(a, item_idx);
     const int h = kvh * G + wave;
     const int q0 = it.qb * 32;
+    const int L = a.pos0 + a.seq;
+    const size_t page_elems = (size_t)P * D;
+    const uint16_t *kpool = (const uint16_t *)a.kpool;
+    const uint16_t *vpool = (const uint16_t *)a.vpool;
 
-    // q fragments: B operand of S^T = K Q^T, lane (grp, c) -> row c, dims 8*grp..
+    // K/V tile staging through registers: thread tid moves 16-byte chunks
+    // idx = tid + 256*j of the K page (row idx/16, chunk idx%16) and of the V
+    // page (sub-tile idx/256, d (idx%256)/2, positions 16*sub + 8*(idx%2) + [0,8))
+    uint4 rk0, rk1, rk2, rk3, rv0, rv1, rv2, rv3;
+#define PF_FETCH(tile)                                                                      \
+    do {                                                                                    \
+        const int phys_ = a.tab[tile];                                                      \
+        const uint16_t *kp_ = kpool + ((size_t)phys_ * Hkv + kvh) * page_elems + tid * 8;   \
+        const uint16_t *vp_ = vpool + ((size_t)phys_ * Hkv + kvh) * page_elems + tid * 8;   \
+        rk0 = *(const uint4 *)(kp_);                                                        \
+        rk1 = *(const uint4 *)(kp_ + 2048);                                                 \
+        rk2 = *(const uint4 *)(kp_ + 4096);                                                 \
+        rk3 = *(const uint4 *)(kp_ + 6144);                                                 \
+        rv0 = *(const uint4 *)(vp_);                                                        \
+        rv1 = *(const uint4 *)(vp_ + 2048);                                                 \
+        rv2 = *(const uint4 *)(vp_ + 4096);                                                 \
+        rv3 = *(const uint4 *)(vp_ + 6144);                                                 \
+        const int nv_ = L - (tile) * P; /* positions >= L hold no data */                   \
+        if (nv_ < P) {                                                                      \
+            rv0 = vmask(rv0, 0 * 16 + (tid & 1) * 8, nv_);                                  \
+            rv1 = vmask(rv1, 1 * 16 + (tid & 1) * 8, nv_);                                  \
+            rv2 = vmask(rv2, 2 * 16 + (tid & 1) * 8, nv_);                                  \
+            rv3 = vmask(rv3, 3 * 16 + (tid & 1) * 8, nv_);                                  \
+        }                                                                                   \
+    } while (0)
+#define PF_STASH(buf)                                                                       \
+    do {                                                                                    \
+        const int kr_ = tid / 16, kc_ = (tid % 16) * 8;                                     \
+        *(uint4 *)(&sK[buf][kswz(kr_) * KLD + kc_]) = rk0;                                  \
+        *(uint4 *)(&sK[buf][kswz(kr_ + 16) * KLD + kc_]) = rk1;                             \
+        *(uint4 *)(&sK[buf][kswz(kr_ + 32) * KLD + kc_]) = rk2;                             \
+        *(uint4 *)(&sK[buf][kswz(kr_ + 48) * KLD + kc_]) = rk3;                             \
+        const int vr_ = tid / 2, vc_ = (tid % 2) * 8;                                       \
+        *(uint4 *)(&sV[buf][vr_ * VLD + vc_]) = rv0;                                        \
+        *(uint4 *)(&sV[buf][vr_ * VLD + 16 + vc_]) = rv1;                                   \
+        *(uint4 *)(&sV[buf][vr_ * VLD + 32 + vc_]) = rv2;                                   \
+        *(uint4 *)(&sV[buf][vr_ * VLD + 48 + vc_]) = rv3;                                   \
+    } while (0)
+
+    // ---- q prologue: RoPE + RMSNorm of rows q0 + 16*qq + c straight into the
+    // S^T B operand (lane (grp, c): dims 32*ks + 8*grp + [0, 8)).  The RoPE
+    // partner of a dim (d +- rope_dim/2, rope_dim in {64, 128}) sits in the
+    // same lane; the row's sum of squares is reduced across the 4 lane groups.
     vec qf[2][4];
+    {
+        const int half = a.rope_half, hk = half / 32;  // partner offset in ks units
+        float gw[4][8];
 #pragma unroll
-    for (int qq = 0; qq < 2; qq++) {
-        const int row = q0 + qq * 16 + c;
-        const uint16_t *qr = (const uint16_t *)a.qp + ((size_t)h * a.seq_pad + row) * D;
+        for (int ks = 0; ks < 4; ks++)
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            uint4 u = row < a.seq ? *(const uint4 *)(qr + ks * 32 + grp * 8) : make_uint4(0, 0, 0, 0);
-            qf[qq][ks] = __builtin_bit_cast(vec, u);
+            for (int e = 0; e < 8; e++) gw[ks][e] = a.qnw ? a.qnw[32 * ks + 8 * grp + e] : 1.0f;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+            const int row = q0 + qq * 16 + c;
+            const bool ok = row < a.seq;
+            const int pos = a.pos0 + (ok ? row : 0);
+            float x[4][8];
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                if (ok) load8_in(a.q, (size_t)row * a.heads * D + (size_t)h * D + 32 * ks + 8 * grp, a.io_bf16, x[ks]);
+                else
+#pragma unroll
+                    for (int e = 0; e < 8; e++) x[ks][e] = 0.0f;
+            }
+            const float *cs = a.rope_cos + (size_t)pos * half;
+            const float *sn = a.rope_sin + (size_t)pos * half;
+            float y[4][8], ss = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int ib = 32 * ks + 8 * grp;  // first dim of this chunk
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int d = ib + e;
+                    float v;
+                    if (ks < hk) {
+                        v = x[ks][e] * cs[d] - x[ks + hk][e] * sn[d];
+                    } else if (ks < 2 * hk) {
+                        v = x[ks - hk][e] * sn[d - half] + x[ks][e] * cs[d - half];
+                    } else {
+                        v = x[ks][e];
+                    }
+                    y[ks][e] = v;
+                    ss += v * v;
+                }
+            }
+            float rr = 1.0f;
+            if (a.qnw) rr = 1.0f / sqrtf(pf_xrow_sum(ss) / (float)D + a.eps);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    w[e] = pack2<T>(y[ks][2 * e] * rr * gw[ks][2 * e] * a.qscale,
+                                    y[ks][2 * e + 1] * rr * gw[ks][2 * e + 1] * a.qscale);
+                qf[qq][ks] = __builtin_bit_cast(vec, make_uint4(w[0], w[1], w[2], w[3]));
+            }
         }
     }
 
@@ -200,56 +368,16 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) o[db][qq] = f32x4{0.f, 0.f, 0.f, 0.f};
     float mrun[2] = {kFloor2, kFloor2}, lrun[2] = {0.f, 0.f};
+    const int qmin = a.pos0 + q0;  // smallest q position of the block
 
-    const int L = a.pos0 + a.seq;
-    const size_t page_elems = (size_t)P * D;
-    const uint16_t *kpool = (const uint16_t *)a.kpool;
-    const uint16_t *vpool = (const uint16_t *)a.vpool;
-
-    uint4 rk[4], rv[4];
-    auto fetch = [&](int tile) {
-        const int phys = a.tab[tile];
-        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems;
-        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems;
-        const int nvalid = L - tile * P;  // positions >= L hold no data
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int idx = tid + 256 * j;
-            rk[j] = *(const uint4 *)(kp + (size_t)idx * 8);
-            uint4 v = *(const uint4 *)(vp + (size_t)idx * 8);
-            // idx -> sub-tile idx/256, d (idx%256)/2, positions 16*sub + 8*(idx%2) + [0,8)
-            const int col0 = (idx / 256) * 16 + (idx % 2) * 8;
-            if (col0 + 8 > nvalid) {  // zero V^T entries of unwritten positions
-                uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    if (col0 + 2 * e >= nvalid) w[e] &= 0xFFFF0000u;
-                    if (col0 + 2 * e + 1 >= nvalid) w[e] &= 0x0000FFFFu;
-                }
-                v = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-            rv[j] = v;
-        }
-    };
-    auto stash = [&](int buf) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int idx = tid + 256 * j;
-            const int kr = idx / 16, kc = idx % 16;
-            *(uint4 *)(&sK[buf][kswz(kr) * KLD + kc * 8]) = rk[j];
-            const int vr = (idx % 256) / 2, vcol = (idx / 256) * 16 + (idx % 2) * 8;
-            *(uint4 *)(&sV[buf][vr * VLD + vcol]) = rv[j];
-        }
-    };
-
-    fetch(it.t0);
-    stash(0);
+    PF_FETCH(it.t0);
+    PF_STASH(0);
     __syncthreads();
 
     for (int t = it.t0; t < it.t1; t++) {
         const int buf = (t - it.t0) & 1;
         const bool more = t + 1 < it.t1;
-        if (more) fetch(t + 1);
+        if (more) PF_FETCH(t + 1);
 
         // ---- S^T = K Q^T (64 kv x 32 q) ----
         f32x4 sacc[4][2];
@@ -268,37 +396,66 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
             }
         }
 
-        // ---- causal mask + online softmax (column c = q row) ----
+        // ---- online softmax (column c = q row); the causal mask only touches
+        // tiles reaching past the block's first row ----
         const int kvbase = t * P;
+        const bool diag = kvbase + P - 1 > qmin;
+        if (diag) {
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int qpos = qmin + qq * 16 + c;
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
+            }
+        }
+        bool rescale = false;
+        float alpha[2];
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
-            const int qpos = a.pos0 + q0 + qq * 16 + c;
             float mx = -INFINITY;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int kv = kvbase + krow(kb, grp * 4 + i);
-                    if (kv <= qpos) mx = fmaxf(mx, sacc[kb][qq][i]);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                for (int i = 0; i < 4; i++) mx = fmaxf(mx, sacc[kb][qq][i]);
+            mx = pf_xrow_max(mx);
             const float mnew = fmaxf(mrun[qq], mx);
-            const float alpha = exp2f(mrun[qq] - mnew);
+            alpha[qq] = __builtin_amdgcn_exp2f(mrun[qq] - mnew);
+            rescale |= mnew != mrun[qq];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    sacc[kb][qq][i] = __builtin_amdgcn_exp2f(fmaxf(sacc[kb][qq][i] - mnew, kFloor2));
+            mrun[qq] = mnew;
+        }
+        if (diag) {  // masked entries contribute exactly 0 (not the floor value)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const int qpos = qmin + qq * 16 + c;
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
             float ps = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int kv = kvbase + krow(kb, grp * 4 + i);
-                    const float p = kv <= qpos ? exp2f(fmaxf(sacc[kb][qq][i] - mnew, kFloor2)) : 0.f;
-                    sacc[kb][qq][i] = p;
-                    ps += p;
-                }
-            lrun[qq] = lrun[qq] * alpha + ps;
-            mrun[qq] = mnew;
+                for (int i = 0; i < 4; i++) ps += sacc[kb][qq][i];
+            lrun[qq] = lrun[qq] * alpha[qq] + ps;
+        }
+        if (__any(rescale)) {
 #pragma unroll
-            for (int db = 0; db < 8; db++) o[db][qq] *= alpha;
+            for (int db = 0; db < 8; db++)
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) o[db][qq] *= alpha[qq];
         }
 
         // ---- O^T += V^T P^T ----
@@ -307,14 +464,9 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
             vec pf[2];
 #pragma unroll
             for (int qq = 0; qq < 2; qq++) {
-                uint16_t e[8];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    e[i] = to_elem<T>(sacc[2 * ks2][qq][i]);
-                    e[4 + i] = to_elem<T>(sacc[2 * ks2 + 1][qq][i]);
-                }
-                uint4 u = make_uint4(e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
-                                     e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16));
+                const f32x4 lo = sacc[2 * ks2][qq], hi = sacc[2 * ks2 + 1][qq];
+                const uint4 u = make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]),
+                                           pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]));
                 pf[qq] = __builtin_bit_cast(vec, u);
             }
 #pragma unroll
@@ -325,18 +477,13 @@ __global__ __launch_bounds__(256) void prefill_flash_kernel(FlashArgs a) {
             }
         }
 
-        if (more) stash(buf ^ 1);
+        if (more) PF_STASH(buf ^ 1);
         __syncthreads();
     }
 
     // ---- finish: row sums across the 4 lane groups ----
 #pragma unroll
-    for (int qq = 0; qq < 2; qq++) {
-        float l = lrun[qq];
-        l += __shfl_xor(l, 16, 64);
-        l += __shfl_xor(l, 32, 64);
-        lrun[qq] = l;
-    }
+    for (int qq = 0; qq < 2; qq++) lrun[qq] = pf_xrow_sum(lrun[qq]);
     const int qdim = a.heads * D;
     if (it.nsplit == 1) {
 #pragma unroll
