@@ -15,11 +15,15 @@ Also measured (secondary): causal prefill of 2048
 tokens through one layer, bf16 inputs, bf16 MFMA with fp32 accumulation,
 K/V written into an empty cache.
 
-Printed: ONE JSON line.  `value` is decode-attention HBM GB/s (algorithmic
-bytes per step / wall time per step); `roofline` prices the decode kernel's
-average duration (HIP events around each launch, second pass) against 8 TB/s;
-`prefill` carries the prefill TFLOP/s with its own MFMA roofline;
-`cpu_baseline` is the C oracle (port of Ops.cs) on this host's cores.
+Printed: ONE JSON line.  `value` is decode-attention HBM GB/s: algorithmic
+bytes per step / GPU time per step, from HIP events recorded on the
+backend's stream around the whole timed region.  `roofline` prices one
+decode call (its split kernel and its merge kernel, back to back) against
+8 TB/s with the same events; `traffic` is read from profiles/traffic.json
+(rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when present.  `prefill`
+carries the prefill TFLOP/s with its own MFMA roofline; `config1`, `config4`
+and `config5` are the other configurations; `cpu_baseline` is the C oracle
+(port of Ops.cs) on this host's cores.
 """
 from __future__ import annotations
 
@@ -35,7 +39,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-from hymt2sharp_amd import BF16, F16, HipBackend  # noqa: E402
+from hymt2sharp_amd import BF16, F16, F32, HipBackend  # noqa: E402
 from hymt2sharp_amd import synth as S  # noqa: E402
 
 HQ, HKV, D = 16, 4, 128
@@ -87,34 +91,51 @@ class HipEvents:
         self.L.hipEventDestroy(e)
 
 
-def bench_decode(steps, warmup):
-    L = CTX + 1
-    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS)
-    be.create_cache(LAYERS * NSETS, L, F16)
+def decode_pool(config, ctx, n=8):
+    """`n` distinct seeded cache contents [ctx][Hkv*D] as bf16 bits."""
     scale = 1.0 / np.sqrt(D)
-    # 8 distinct cache contents spread over the 128 layers (distinct addresses)
-    pool = [(S.f32_to_bf16_bits(S.normal(S.seed(2, S.KCACHE, i), (CTX, HKV * D), scale)),
-             S.f32_to_bf16_bits(S.normal(S.seed(2, S.VCACHE, i), (CTX, HKV * D), scale)))
-            for i in range(8)]
-    for layer in range(LAYERS * NSETS):
-        kb, vb = pool[layer % 8]
-        be.UploadKv(layer, 0, CTX, kb, vb)
-    nl = LAYERS * NSETS
-    q = S.normal(S.seed(2, S.Q), (nl, HQ * D), scale)
-    k = S.normal(S.seed(2, S.KNEW), (nl, HKV * D), scale)
-    v = S.normal(S.seed(2, S.VNEW), (nl, HKV * D), scale)
-    gq = S.uniform(S.seed(2, S.GQ), (nl, D), 0.9, 1.1)
-    gk = S.uniform(S.seed(2, S.GK), (nl, D), 0.9, 1.1)
+    return [(S.f32_to_bf16_bits(S.normal(S.seed(config, S.KCACHE, i), (ctx, HKV * D), scale)),
+             S.f32_to_bf16_bits(S.normal(S.seed(config, S.VCACHE, i), (ctx, HKV * D), scale)))
+            for i in range(n)]
+
+
+def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30):
+    """Decode attention at position `ctx` (L = ctx + 1) over distinct layers.
+
+    A step is `layers_per_step` decode calls, one per layer, in stream order
+    (each call's kernels finish before the next call's start, as in the
+    layer loop of a decode step).  Enough layer caches rotate across steps
+    that the resident set exceeds `min_bytes`, so the 256 MiB MALL cannot
+    serve the KV reads.  Inputs (q, k, v, gammas) are device-resident.
+    Returns per-call and per-step times from HIP events on the backend's
+    stream around the whole timed region."""
+    L = ctx + 1
+    kvb = 4 if kv_dtype == F32 else 2
+    bpl = decode_bytes_per_layer(L, kvb)
+    nsets = max(1, -(-min_bytes // (bpl * layers_per_step)))
+    nl = layers_per_step * nsets
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS)
+    be.create_cache(nl, L, kv_dtype)
+    pool = decode_pool(config, ctx)
+    for layer in range(nl):
+        kb, vb = pool[layer % len(pool)]
+        be.UploadKv(layer, 0, ctx, kb, vb)
+    scale = 1.0 / np.sqrt(D)
+    q = S.normal(S.seed(config, S.Q), (nl, HQ * D), scale)
+    k = S.normal(S.seed(config, S.KNEW), (nl, HKV * D), scale)
+    v = S.normal(S.seed(config, S.VNEW), (nl, HKV * D), scale)
+    gq = S.uniform(S.seed(config, S.GQ), (nl, D), 0.9, 1.1)
+    gk = S.uniform(S.seed(config, S.GK), (nl, D), 0.9, 1.1)
     dq, dk, dv = be.alloc(q.nbytes), be.alloc(k.nbytes), be.alloc(v.nbytes)
     dgq, dgk, dout = be.alloc(gq.nbytes), be.alloc(gk.nbytes), be.alloc(q.nbytes)
     for dptr, arr in ((dq, q), (dk, k), (dv, v), (dgq, gq), (dgk, gk)):
         be.upload(dptr, arr)
 
     def step(s):
-        base_layer = (s % NSETS) * LAYERS
-        for l in range(LAYERS):
+        base_layer = (s % nsets) * layers_per_step
+        for l in range(layers_per_step):
             i = base_layer + l
-            be.decode_dev(i, CTX, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
+            be.decode_dev(i, ctx, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
                           dgq + i * D * 4, dgk + i * D * 4, dout + i * HQ * D * 4)
 
     ev = HipEvents(be.stream())
@@ -123,32 +144,15 @@ def bench_decode(steps, warmup):
     be.sync()
     # timed region: K whole steps between two events, synchronised both sides
     e0, e1 = ev.new(), ev.new()
-    be.sync()
     t0 = time.perf_counter()
     ev.record(e0)
     for s in range(steps):
         step(s)
+    t_submit = time.perf_counter() - t0
     ev.record(e1)
     be.sync()
     wall = time.perf_counter() - t0
     gpu_ms = ev.elapsed_ms(e0, e1)
-
-    # second pass: an event pair around every launch -> per-kernel duration
-    pairs = [(ev.new(), ev.new()) for _ in range(LAYERS)]
-    durs = []
-    for s in range(steps):
-        base_layer = (s % NSETS) * LAYERS
-        for l in range(LAYERS):
-            i = base_layer + l
-            ev.record(pairs[l][0])
-            be.decode_dev(i, CTX, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
-                          dgq + i * D * 4, dgk + i * D * 4, dout + i * HQ * D * 4)
-            ev.record(pairs[l][1])
-        be.sync()
-        durs += [ev.elapsed_ms(a, b) for a, b in pairs]
-    for a, b in pairs:
-        ev.destroy(a)
-        ev.destroy(b)
     ev.destroy(e0)
     ev.destroy(e1)
 
@@ -159,28 +163,36 @@ def bench_decode(steps, warmup):
         be.free(p)
     be.Dispose()
 
-    bpl = decode_bytes_per_layer(L)
-    ms_step = gpu_ms / steps
-    kern_us = float(np.mean(durs)) * 1e3
+    calls = steps * layers_per_step
+    call_us = gpu_ms * 1e3 / calls
     return {
-        "ms_per_step": ms_step,
+        "L": L,
+        "ms_per_step": gpu_ms / steps,
         "wall_ms_per_step": wall * 1e3 / steps,
-        "gbs": bpl * LAYERS / (ms_step * 1e-3) / 1e9,
+        "call_us": call_us,
+        "host_submit_us_per_call": t_submit * 1e6 / calls,
+        "gbs": bpl / (call_us * 1e-6) / 1e9,
         "bytes_per_layer": bpl,
-        "kernel_us": kern_us,
-        "kernel_us_p10": float(np.percentile(durs, 10)) * 1e3,
-        "kernel_us_p90": float(np.percentile(durs, 90)) * 1e3,
-        "kernel_gbs": bpl / (kern_us * 1e-6) / 1e9,
-        "tokens_per_s": 1e3 / ms_step,
+        "layers_resident": nl,
+        "tokens_per_s": 1e3 / (gpu_ms / steps),
     }
 
 
-def bench_prefill(steps, warmup, seq=2048):
-    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, seq, BF16)
+def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
+    """One prefill chunk of `seq` tokens at positions [p0, p0+seq) over a cache
+    holding `p0` seeded positions: the chunk's K/V are appended and every row
+    attends causally over [0, p0+row].  Repeating the call rewrites the same
+    rows with the same values, so each timed call does identical work."""
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, p0 + seq, kv_dtype)
+    if p0:
+        kb, vb = decode_pool(config, p0, 1)[0]
+        be.UploadKv(0, 0, p0, kb, vb)
     scale = 1.0 / np.sqrt(D)
-    q = S.f32_to_bf16_bits(S.normal(S.seed(3, S.Q), (seq, HQ * D), scale))
-    k = S.f32_to_bf16_bits(S.normal(S.seed(3, S.KNEW), (seq, HKV * D), scale))
-    v = S.f32_to_bf16_bits(S.normal(S.seed(3, S.VNEW), (seq, HKV * D), scale))
+    q = S.normal(S.seed(config, S.Q), (seq, HQ * D), scale)
+    k = S.normal(S.seed(config, S.KNEW), (seq, HKV * D), scale)
+    v = S.normal(S.seed(config, S.VNEW), (seq, HKV * D), scale)
+    if io_dtype == BF16:
+        q, k, v = map(S.f32_to_bf16_bits, (q, k, v))
     dq, dk, dv = be.alloc(q.nbytes), be.alloc(k.nbytes), be.alloc(v.nbytes)
     dout = be.alloc(seq * HQ * D * 4)
     for dptr, arr in ((dq, q), (dk, k), (dv, v)):
@@ -188,7 +200,7 @@ def bench_prefill(steps, warmup, seq=2048):
     ev = HipEvents(be.stream())
 
     def run():
-        be.prefill_dev(0, 0, seq, dq, dk, dv, BF16, None, None, dout)
+        be.prefill_dev(0, p0, seq, dq, dk, dv, io_dtype, None, None, dout)
 
     for _ in range(warmup):
         run()
@@ -200,13 +212,15 @@ def bench_prefill(steps, warmup, seq=2048):
     ev.record(e1)
     be.sync()
     ms = ev.elapsed_ms(e0, e1) / steps
+    ev.destroy(e0)
+    ev.destroy(e1)
     out = np.empty((seq, HQ * D), np.float32)
     be.download(out, dout)
     assert np.all(np.isfinite(out))
     for p in (dq, dk, dv, dout):
         be.free(p)
     be.Dispose()
-    fl = prefill_flops(0, seq)
+    fl = prefill_flops(p0, seq)
     return {"ms_per_call": ms, "tflops": fl / (ms * 1e-3) / 1e12, "flops": fl,
             "tokens_per_s": seq / (ms * 1e-3)}
 
@@ -265,13 +279,31 @@ def cpu_baseline_prefill(threads, seq=2048):
     return prefill_flops(0, seq) / sec / 1e12, sec
 
 
+def load_traffic():
+    """HBM bytes per call measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (scaled by the same counters on a copy of known size), kept beside the
+    profiles they come from; None when absent."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def r4(d):
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "configs"], default=None,
+                    help="run one leg: the config-2 decode step, the config-3 prefill, "
+                         "or the other configurations (1, 4, 5)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the attention path has no multi-GPU mode in this "
@@ -279,13 +311,32 @@ def main():
         sys.exit(2)
 
     dec = pre = None
+    extra = {}
     if args.only in (None, "decode"):
-        dec = bench_decode(args.steps, args.warmup)
+        dec = time_decode(2, CTX, F16, args.steps, args.warmup)
     if args.only in (None, "prefill"):
-        pre = bench_prefill(args.steps, args.warmup)
+        pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup)
+    if args.only in (None, "configs"):
+        c1 = time_decode(1, 512, F32, args.steps, args.warmup)
+        extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, no QK norm weights "
+                                        "in the reference config (gammas applied here)",
+                            "unit": "GB/s", "value": round(c1["gbs"], 1), **r4(c1)}
+        c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup)
+        extra["config4"] = {"workload": "prefill chunk 256 at positions 8192..8447 over an "
+                                        "8192-position fp16 cache, fp32 in",
+                            "unit": "TFLOP/s", "value": round(c4["tflops"], 2), **r4(c4)}
+        sweep = {}
+        for ctx in (1024, 4096, 16384, 32768):
+            r = time_decode(5, ctx, F16, max(4, args.steps // 4), args.warmup,
+                            layers_per_step=8)
+            sweep[str(ctx)] = {"gbs": round(r["gbs"], 1), "call_us": round(r["call_us"], 3),
+                               "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                               "bytes": r["bytes_per_layer"]}
+        extra["config5"] = {"workload": "decode context sweep, fp16 KV, one layer per call",
+                            "unit": "GB/s", "by_context": sweep}
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and dec is not None:
         th = cpu_threads()
         gbs, sec = cpu_baseline_decode(th)
         tfl, psec = cpu_baseline_prefill(th)
@@ -298,6 +349,7 @@ def main():
                                      f"C port of AttentionScores/SoftmaxCausal/AttentionCombine "
                                      f"with Forward's 1024 chunking"}}
 
+    traffic = load_traffic() or {}
     rec = {
         "metric": "decode-attn HBM GB/s (% peak) @4k ctx; prefill-attn TFLOP/s (% MFMA peak)",
         "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -310,13 +362,15 @@ def main():
     if dec:
         rec["value"] = round(dec["gbs"], 1)
         rec["ms_per_step"] = round(dec["ms_per_step"], 4)
-        rec["decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec.items()}
-        rec["roofline"] = {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 1),
+        rec["decode"] = r4(dec)
+        rec["roofline"] = {"bound": "hbm", "achieved": round(dec["gbs"], 1),
                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                           "kernel": "decode_attn_kernel<F16>",
+                           "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+                           "traffic": traffic.get("decode_config2"),
+                           "kernel": "decode_attn_mfma_kernel<F16,true> + decode_merge_kernel "
+                                     "(one decode call)",
                            "algorithmic_bytes": dec["bytes_per_layer"],
-                           "avg_us": round(dec["kernel_us"], 3)}
+                           "avg_us": round(dec["call_us"], 3)}
     if pre:
         rec["prefill"] = {"workload": "config 3: causal prefill 2048 tokens, one layer, bf16 in, "
                                       "bf16 MFMA fp32 acc, empty cache",
@@ -326,7 +380,9 @@ def main():
                           "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                                        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                       "traffic": None, "flops": pre["flops"]}}
+                                       "traffic": traffic.get("prefill_config3"),
+                                       "flops": pre["flops"]}}
+    rec.update(extra)
     rec["cpu_baseline"] = cpu
     print(json.dumps(rec))
 

@@ -13,6 +13,7 @@ constexpr int kGroup = 4;       // q heads per kv head (16 / 4)
 constexpr int kPage = 64;       // tokens per KV page
 constexpr int kMaxSplits = 128; // decode KV splits per kv head (merge width)
 constexpr int kArgPages = 256;  // decode page lists passed in kernel arguments
+constexpr int kItemTiles = 1024; // prefill kv tiles per work item (page ids staged in LDS)
 
 // Paged pool addressing, per layer.  A page holds 64 positions of one kv head
 // for K and for V (16 KiB each in f16/bf16):

@@ -11,12 +11,19 @@
 //                 of k, k and v rounded into the paged cache (v transposed
 //                 through LDS into the 16-position V^T sub-tiles).
 //  prefill_flash  one workgroup per (kv head, 32-row q block, kv tile range):
-//                 4 waves = the 4 q heads of the GQA group sharing every K/V
-//                 tile staged in LDS.  The prologue applies RoPE + norm to the
-//                 wave's 32 q rows straight into MFMA operand registers.
-//                 S^T = K Q^T and O^T += V^T P^T on
+//                 8 waves = the 4 q heads of the GQA group x the two parities
+//                 of the range's 64-position tiles, so every SIMD runs two
+//                 waves; each staged K/V tile in LDS serves the 4 heads.  The
+//                 prologue applies RoPE + norm to the wave's 32 q rows
+//                 straight into MFMA operand registers.  S^T - m = K Q^T - m
+//                 (accumulated onto -m) and O^T += V^T P^T on
 //                 v_mfma_f32_16x16x32_{bf16,f16}; single-pass online softmax
-//                 in base 2 with the reference's -80 floor.
+//                 in base 2 with a lazy running maximum that starts at the
+//                 reference's -80; the two parities merge through LDS.
+//                 The reference clamps each exponent at -80 below the row
+//                 maximum; weights that small (< 2e-35 of the largest) are
+//                 below fp32 resolution of the row sum, so the kernel uses
+//                 the exact exponent.
 //  prefill_merge  combines the (m, l, O) partials of q blocks whose kv range
 //                 was split over several workgroups (long cached prefixes).
 #include "attn_kernels.hpp"
@@ -235,17 +242,149 @@ __device__ __forceinline__ uint4 vmask(uint4 v, int col0, int nvalid) {
     return make_uint4(v.x & keep[0], v.y & keep[1], v.z & keep[2], v.w & keep[3]);
 }
 
+// Row sum of a packed pair of softmax weights (v_dot2c_f32_{bf16,f16} with
+// (1, 1)): l accumulates exactly the rounded weights the P*V MFMA uses.
+template <typename T> __device__ __forceinline__ float sum2(uint32_t pair, float acc);
+template <> __device__ __forceinline__ float sum2<BF16>(uint32_t pair, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, pair), __builtin_bit_cast(v2, 0x3F803F80u), acc, false);
+}
+template <> __device__ __forceinline__ float sum2<F16>(uint32_t pair, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, pair), __builtin_bit_cast(v2, 0x3C003C00u), acc, false);
+}
+
+constexpr int kRopeLd = 68;  // LDS row stride (floats) of the staged RoPE rows
+
+// q rows q0 + 16*qq + c of head h after RoPE and RMSNorm, times qscale, as the
+// S^T B operand: lane (grp, c) holds dims 32*ks + 8*grp + [0, 8).  The RoPE
+// partner of dim d (d +- rope_dim/2, rope_dim in {0, 64, 128}) is dim chunk
+// ks ^ (rope_dim/64) of the same lane, so no data crosses lanes except the
+// norm's sum of squares.  Every global load is issued before any math; rows
+// past the chunk use q = 0 (their results are discarded).
+template <typename T, bool IN_BF16>
+__device__ __forceinline__ void q_operand(const FlashArgs &a, int h, int q0, int grp, int c,
+                                          const float *rope_lds, typename Mfma<T>::vec (&qf)[2][4]) {
+    constexpr int D = kHeadDim;
+    typedef typename Mfma<T>::vec vec;
+    const int rh = a.rope_half, hk = rh >> 5;
+    float x[2][4][8], cA[2][8], cB[2][8], sA[2][8], sB[2][8], gw[4][8];
+    bool ok[2];
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++) {
+        const int row0 = q0 + qq * 16 + c;
+        ok[qq] = row0 < a.seq;
+        const int row = ok[qq] ? row0 : a.seq - 1;
+        const size_t base = (size_t)row * a.heads * D + (size_t)h * D + 8 * grp;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            if (IN_BF16) {
+                const uint4 u = *(const uint4 *)((const uint16_t *)a.q + base + 32 * ks);
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[qq][ks][2 * e] = __uint_as_float(w[e] << 16);
+                    x[qq][ks][2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+                }
+            } else {
+                const float4 u0 = *(const float4 *)((const float *)a.q + base + 32 * ks);
+                const float4 u1 = *(const float4 *)((const float *)a.q + base + 32 * ks + 4);
+                x[qq][ks][0] = u0.x; x[qq][ks][1] = u0.y; x[qq][ks][2] = u0.z; x[qq][ks][3] = u0.w;
+                x[qq][ks][4] = u1.x; x[qq][ks][5] = u1.y; x[qq][ks][6] = u1.z; x[qq][ks][7] = u1.w;
+            }
+        }
+        if (rh) {
+            // LDS rope rows [cos|sin][32 rows][kRopeLd]
+            const float *rc = rope_lds + (qq * 16 + c) * kRopeLd, *rs = rc + 32 * kRopeLd;
+            const int fa = (8 * grp) & (rh - 1), fb = (32 + 8 * grp) & (rh - 1);
+#pragma unroll
+            for (int e4 = 0; e4 < 2; e4++) {
+                const float4 ca = *(const float4 *)(rc + fa + 4 * e4);
+                const float4 cb = *(const float4 *)(rc + fb + 4 * e4);
+                const float4 sa = *(const float4 *)(rs + fa + 4 * e4);
+                const float4 sb = *(const float4 *)(rs + fb + 4 * e4);
+                cA[qq][4 * e4] = ca.x; cA[qq][4 * e4 + 1] = ca.y; cA[qq][4 * e4 + 2] = ca.z; cA[qq][4 * e4 + 3] = ca.w;
+                cB[qq][4 * e4] = cb.x; cB[qq][4 * e4 + 1] = cb.y; cB[qq][4 * e4 + 2] = cb.z; cB[qq][4 * e4 + 3] = cb.w;
+                sA[qq][4 * e4] = sa.x; sA[qq][4 * e4 + 1] = sa.y; sA[qq][4 * e4 + 2] = sa.z; sA[qq][4 * e4 + 3] = sa.w;
+                sB[qq][4 * e4] = sb.x; sB[qq][4 * e4 + 1] = sb.y; sB[qq][4 * e4 + 2] = sb.z; sB[qq][4 * e4 + 3] = sb.w;
+            }
+        }
+    }
+    if (a.qnw) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const float4 g0 = *(const float4 *)(a.qnw + 32 * ks + 8 * grp);
+            const float4 g1 = *(const float4 *)(a.qnw + 32 * ks + 8 * grp + 4);
+            gw[ks][0] = g0.x; gw[ks][1] = g0.y; gw[ks][2] = g0.z; gw[ks][3] = g0.w;
+            gw[ks][4] = g1.x; gw[ks][5] = g1.y; gw[ks][6] = g1.z; gw[ks][7] = g1.w;
+        }
+    } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) gw[ks][e] = 1.0f;
+    }
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++) {
+        float y[4][8], ss = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            // RoPE (Ops.RopeRange): first half x*c - x'*s, second half x'*s + x*c
+            const bool rot = ks < 2 * hk, lower = (ks & hk) == 0;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float xv = ok[qq] ? x[qq][ks][e] : 0.0f;
+                float v = xv;
+                if (rot) {
+                    const float xp = ok[qq] ? (hk == 2 ? x[qq][ks ^ 2][e] : x[qq][ks ^ 1][e]) : 0.0f;
+                    const float cv = (ks & 1) ? cB[qq][e] : cA[qq][e];
+                    const float sv = (ks & 1) ? sB[qq][e] : sA[qq][e];
+                    v = lower ? xv * cv - xp * sv : xp * sv + xv * cv;
+                }
+                y[ks][e] = v;
+                ss += v * v;
+            }
+        }
+        float rr = 1.0f;
+        if (a.qnw) rr = 1.0f / sqrtf(pf_xrow_sum(ss) / (float)D + a.eps);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = pack2<T>(y[ks][2 * e] * rr * gw[ks][2 * e] * a.qscale,
+                                y[ks][2 * e + 1] * rr * gw[ks][2 * e + 1] * a.qscale);
+            qf[qq][ks] = __builtin_bit_cast(vec, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+    }
+}
+
+// Lazy running maximum: a row's reference m moves only when a tile holds a
+// score above m + kLazy (log2 units).  Weights p = 2^(s - m) then stay below
+// 2^kLazy and most tiles skip the rescale of O and l entirely.
+constexpr float kLazy = 8.0f;
+
+// 8 waves: wave w computes head (w & 3) of the GQA group over the tiles of
+// parity (w >> 2) in the item's range, so each SIMD runs two waves.  Tile
+// pair j sits in LDS buffer j & 1 (one slot per parity); the two halves'
+// (m, l, O) are combined through LDS at the end.
 template <typename T>
-__global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
+__global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
     constexpr int KLD = D + 8;  // 272-byte K rows
     constexpr int VLD = P + 8;  // 144-byte V^T rows
+    constexpr int KT = P * KLD, VT = D * VLD;  // elements of one staged tile
     typedef typename Mfma<T>::vec vec;
-    __shared__ __attribute__((aligned(16))) uint16_t sK[2][P * KLD];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[2][D * VLD];
+    // slot (buffer, parity) at index 2 * buffer + parity; sK doubles as the
+    // merge area of the epilogue ([head][17][64] float4 = 69632 bytes)
+    __shared__ __attribute__((aligned(16))) uint16_t sK[4 * KT];
+    __shared__ __attribute__((aligned(16))) uint16_t sV[4 * VT];
+    __shared__ int32_t sTab[kItemTiles];  // physical pages of the item's tiles
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int hw = wave & 3, half = wave >> 2;
     const int grp = lane >> 4, c = lane & 15;
+    const int st = tid & 255;  // staging index within the half
     const int Hkv = a.kv_heads;
 
     // XCD-aware placement: workgroup b runs on XCD b % 8; give each XCD one kv
@@ -256,22 +395,24 @@ __global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
     const int item_idx = (b / 8) * R + (b % 8) % R;
     if (item_idx >= a.items_per_kvh) return;
     const FlashItem it = flash_item(a, item_idx);
-    const int h = kvh * G + wave;
+    const int h = kvh * G + hw;
     const int q0 = it.qb * 32;
     const int L = a.pos0 + a.seq;
     const size_t page_elems = (size_t)P * D;
     const uint16_t *kpool = (const uint16_t *)a.kpool;
     const uint16_t *vpool = (const uint16_t *)a.vpool;
 
-    // K/V tile staging through registers: thread tid moves 16-byte chunks
-    // idx = tid + 256*j of the K page (row idx/16, chunk idx%16) and of the V
-    // page (sub-tile idx/256, d (idx%256)/2, positions 16*sub + 8*(idx%2) + [0,8))
+    // K/V tile staging through registers: staging thread st of each half moves
+    // 16-byte chunks idx = st + 256*j of the K page (row idx/16, chunk idx%16)
+    // and of the V page (sub-tile idx/256, d (idx%256)/2, positions
+    // 16*sub + 8*(idx%2) + [0,8)) of the tile of its parity.
     uint4 rk0, rk1, rk2, rk3, rv0, rv1, rv2, rv3;
-#define PF_FETCH(tile)                                                                      \
+#define PF_FETCH(tile) PF_FETCH_P(tile, sTab[(tile) - it.t0])
+#define PF_FETCH_P(tile, phys)                                                              \
     do {                                                                                    \
-        const int phys_ = a.tab[tile];                                                      \
-        const uint16_t *kp_ = kpool + ((size_t)phys_ * Hkv + kvh) * page_elems + tid * 8;   \
-        const uint16_t *vp_ = vpool + ((size_t)phys_ * Hkv + kvh) * page_elems + tid * 8;   \
+        const int phys_ = (phys);                                                           \
+        const uint16_t *kp_ = kpool + ((size_t)phys_ * Hkv + kvh) * page_elems + st * 8;    \
+        const uint16_t *vp_ = vpool + ((size_t)phys_ * Hkv + kvh) * page_elems + st * 8;    \
         rk0 = *(const uint4 *)(kp_);                                                        \
         rk1 = *(const uint4 *)(kp_ + 2048);                                                 \
         rk2 = *(const uint4 *)(kp_ + 4096);                                                 \
@@ -282,203 +423,210 @@ __global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
         rv3 = *(const uint4 *)(vp_ + 6144);                                                 \
         const int nv_ = L - (tile) * P; /* positions >= L hold no data */                   \
         if (nv_ < P) {                                                                      \
-            rv0 = vmask(rv0, 0 * 16 + (tid & 1) * 8, nv_);                                  \
-            rv1 = vmask(rv1, 1 * 16 + (tid & 1) * 8, nv_);                                  \
-            rv2 = vmask(rv2, 2 * 16 + (tid & 1) * 8, nv_);                                  \
-            rv3 = vmask(rv3, 3 * 16 + (tid & 1) * 8, nv_);                                  \
+            rv0 = vmask(rv0, 0 * 16 + (st & 1) * 8, nv_);                                   \
+            rv1 = vmask(rv1, 1 * 16 + (st & 1) * 8, nv_);                                   \
+            rv2 = vmask(rv2, 2 * 16 + (st & 1) * 8, nv_);                                   \
+            rv3 = vmask(rv3, 3 * 16 + (st & 1) * 8, nv_);                                   \
         }                                                                                   \
     } while (0)
 #define PF_STASH(buf)                                                                       \
     do {                                                                                    \
-        const int kr_ = tid / 16, kc_ = (tid % 16) * 8;                                     \
-        *(uint4 *)(&sK[buf][kswz(kr_) * KLD + kc_]) = rk0;                                  \
-        *(uint4 *)(&sK[buf][kswz(kr_ + 16) * KLD + kc_]) = rk1;                             \
-        *(uint4 *)(&sK[buf][kswz(kr_ + 32) * KLD + kc_]) = rk2;                             \
-        *(uint4 *)(&sK[buf][kswz(kr_ + 48) * KLD + kc_]) = rk3;                             \
-        const int vr_ = tid / 2, vc_ = (tid % 2) * 8;                                       \
-        *(uint4 *)(&sV[buf][vr_ * VLD + vc_]) = rv0;                                        \
-        *(uint4 *)(&sV[buf][vr_ * VLD + 16 + vc_]) = rv1;                                   \
-        *(uint4 *)(&sV[buf][vr_ * VLD + 32 + vc_]) = rv2;                                   \
-        *(uint4 *)(&sV[buf][vr_ * VLD + 48 + vc_]) = rv3;                                   \
+        uint16_t *k_ = sK + ((buf) * 2 + half) * KT;                                        \
+        uint16_t *v_ = sV + ((buf) * 2 + half) * VT;                                        \
+        const int kr_ = st / 16, kc_ = (st % 16) * 8;                                       \
+        *(uint4 *)(&k_[kswz(kr_) * KLD + kc_]) = rk0;                                       \
+        *(uint4 *)(&k_[kswz(kr_ + 16) * KLD + kc_]) = rk1;                                  \
+        *(uint4 *)(&k_[kswz(kr_ + 32) * KLD + kc_]) = rk2;                                  \
+        *(uint4 *)(&k_[kswz(kr_ + 48) * KLD + kc_]) = rk3;                                  \
+        const int vr_ = st / 2, vc_ = (st % 2) * 8;                                         \
+        *(uint4 *)(&v_[vr_ * VLD + vc_]) = rv0;                                             \
+        *(uint4 *)(&v_[vr_ * VLD + 16 + vc_]) = rv1;                                        \
+        *(uint4 *)(&v_[vr_ * VLD + 32 + vc_]) = rv2;                                        \
+        *(uint4 *)(&v_[vr_ * VLD + 48 + vc_]) = rv3;                                        \
     } while (0)
 
     // ---- q prologue: RoPE + RMSNorm of rows q0 + 16*qq + c straight into the
-    // S^T B operand (lane (grp, c): dims 32*ks + 8*grp + [0, 8)).  The RoPE
-    // partner of a dim (d +- rope_dim/2, rope_dim in {64, 128}) sits in the
-    // same lane; the row's sum of squares is reduced across the 4 lane groups.
-    vec qf[2][4];
+    // S^T B operand (lane (grp, c): dims 32*ks + 8*grp + [0, 8)) ----
+    // ---- start: the first tile's loads, the page ids and the block's RoPE
+    // rows are all in flight before the q math.  The RoPE rows sit in the
+    // LDS slot of tile pair 1, which is first written after iteration 0.
+    const int nt = it.t1 - it.t0;  // <= kItemTiles (host caps items)
+    const int half_u = __builtin_amdgcn_readfirstlane(half);  // wave-uniform: scalar page-id load
+    if (half_u < nt) PF_FETCH_P(it.t0 + half_u, a.tab[it.t0 + half_u]);
+    for (int i = tid; i < nt; i += 512) sTab[i] = a.tab[it.t0 + i];
+    float *rope_lds = (float *)(sV + 2 * VT);  // [cos|sin][32][kRopeLd]
     {
-        const int half = a.rope_half, hk = half / 32;  // partner offset in ks units
-        float gw[4][8];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) gw[ks][e] = a.qnw ? a.qnw[32 * ks + 8 * grp + e] : 1.0f;
-#pragma unroll
-        for (int qq = 0; qq < 2; qq++) {
-            const int row = q0 + qq * 16 + c;
-            const bool ok = row < a.seq;
-            const int pos = a.pos0 + (ok ? row : 0);
-            float x[4][8];
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                if (ok) load8_in(a.q, (size_t)row * a.heads * D + (size_t)h * D + 32 * ks + 8 * grp, a.io_bf16, x[ks]);
-                else
-#pragma unroll
-                    for (int e = 0; e < 8; e++) x[ks][e] = 0.0f;
-            }
-            const float *cs = a.rope_cos + (size_t)pos * half;
-            const float *sn = a.rope_sin + (size_t)pos * half;
-            float y[4][8], ss = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const int ib = 32 * ks + 8 * grp;  // first dim of this chunk
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const int d = ib + e;
-                    float v;
-                    if (ks < hk) {
-                        v = x[ks][e] * cs[d] - x[ks + hk][e] * sn[d];
-                    } else if (ks < 2 * hk) {
-                        v = x[ks - hk][e] * sn[d - half] + x[ks][e] * cs[d - half];
-                    } else {
-                        v = x[ks][e];
-                    }
-                    y[ks][e] = v;
-                    ss += v * v;
-                }
-            }
-            float rr = 1.0f;
-            if (a.qnw) rr = 1.0f / sqrtf(pf_xrow_sum(ss) / (float)D + a.eps);
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                uint32_t w[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    w[e] = pack2<T>(y[ks][2 * e] * rr * gw[ks][2 * e] * a.qscale,
-                                    y[ks][2 * e + 1] * rr * gw[ks][2 * e + 1] * a.qscale);
-                qf[qq][ks] = __builtin_bit_cast(vec, make_uint4(w[0], w[1], w[2], w[3]));
-            }
+        const int rh = a.rope_half;
+        // thread -> (table, row, 4 dims); 2 * 32 * rh / 4 <= 1024 float4
+        for (int i = tid; i < 16 * rh; i += 512) {
+            const int tbl = i / (8 * rh), rem = i % (8 * rh), r = rem / (rh / 4), f4 = rem % (rh / 4);
+            const int row = min(q0 + r, a.seq - 1);
+            const float *src = (tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * rh + 4 * f4;
+            *(float4 *)(rope_lds + (tbl * 32 + r) * kRopeLd + 4 * f4) = *(const float4 *)src;
         }
     }
+    __syncthreads();
+
+    vec qf[2][4];
+    if (a.io_bf16) q_operand<T, true>(a, h, q0, grp, c, rope_lds, qf);
+    else q_operand<T, false>(a, h, q0, grp, c, rope_lds, qf);
 
     f32x4 o[8][2];
 #pragma unroll
     for (int db = 0; db < 8; db++)
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) o[db][qq] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // m starts at the reference's -80 (natural log units); l is this lane's
+    // partial row sum (its 16 positions of each tile)
     float mrun[2] = {kFloor2, kFloor2}, lrun[2] = {0.f, 0.f};
     const int qmin = a.pos0 + q0;  // smallest q position of the block
 
-    PF_FETCH(it.t0);
-    PF_STASH(0);
+    if (half < nt) PF_STASH(0);
     __syncthreads();
 
-    for (int t = it.t0; t < it.t1; t++) {
-        const int buf = (t - it.t0) & 1;
-        const bool more = t + 1 < it.t1;
-        if (more) PF_FETCH(t + 1);
+    for (int j = 0; 2 * j < nt; j++) {
+        const int buf = j & 1;
+        const int t = it.t0 + 2 * j + half;  // this wave's tile
+        const bool more = t + 2 < it.t1;     // this thread stages tile t + 2
+        if (more) PF_FETCH(t + 2);
 
-        // ---- S^T = K Q^T (64 kv x 32 q) ----
-        f32x4 sacc[4][2];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++) sacc[kb][qq] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const int r = kswz(krow(kb, c));
-                vec kf = __builtin_bit_cast(vec, *(const uint4 *)(&sK[buf][r * KLD + ks * 32 + grp * 8]));
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
-            }
-        }
-
-        // ---- online softmax (column c = q row); the causal mask only touches
-        // tiles reaching past the block's first row ----
-        const int kvbase = t * P;
-        const bool diag = kvbase + P - 1 > qmin;
-        if (diag) {
+        if (t < it.t1) {
+            const uint16_t *kt = sK + (buf * 2 + half) * KT;
+            const uint16_t *vt = sV + (buf * 2 + half) * VT;
+            // ---- S^T - m = K Q^T - m (64 kv x 32 q), accumulated onto -m; the
+            // half's first tile starts from 0 and sets m from its scores ----
+            const bool first = j == 0;
+            f32x4 sacc[4][2];
 #pragma unroll
             for (int qq = 0; qq < 2; qq++) {
-                const int qpos = qmin + qq * 16 + c;
+                const float nm = first ? 0.0f : -mrun[qq];
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) sacc[kb][qq] = f32x4{nm, nm, nm, nm};
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const int r = kswz(krow(kb, c));
+                    vec kf = __builtin_bit_cast(vec, *(const uint4 *)(&kt[r * KLD + ks * 32 + grp * 8]));
+#pragma unroll
+                    for (int qq = 0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
+                }
+            }
+
+            // ---- online softmax (column c = q row); the causal mask only
+            // touches tiles reaching past the block's first row ----
+            const int kvbase = t * P;
+            if (kvbase + P - 1 > qmin) {
+#pragma unroll
+                for (int qq = 0; qq < 2; qq++) {
+                    const int qpos = qmin + qq * 16 + c;
+#pragma unroll
+                    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
+                }
+            }
+            float mx[2];
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                float v = -INFINITY;
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
+                    for (int i = 0; i < 4; i++) v = fmaxf(v, sacc[kb][qq][i]);
+                mx[qq] = v;
             }
-        }
-        bool rescale = false;
-        float alpha[2];
+            if (first) {
 #pragma unroll
-        for (int qq = 0; qq < 2; qq++) {
-            float mx = -INFINITY;
+                for (int qq = 0; qq < 2; qq++) {
+                    mrun[qq] = fmaxf(pf_xrow_max(mx[qq]), kFloor2);
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+                    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) mx = fmaxf(mx, sacc[kb][qq][i]);
-            mx = pf_xrow_max(mx);
-            const float mnew = fmaxf(mrun[qq], mx);
-            alpha[qq] = __builtin_amdgcn_exp2f(mrun[qq] - mnew);
-            rescale |= mnew != mrun[qq];
+                        for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= mrun[qq];
+                }
+            } else if (__any(fmaxf(mx[0], mx[1]) > kLazy)) {
+                // move m of every row to its maximum when that is higher
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+                for (int qq = 0; qq < 2; qq++) {
+                    const float d = fmaxf(pf_xrow_max(mx[qq]), 0.0f);
+                    const float al = __builtin_amdgcn_exp2f(-d);
+                    mrun[qq] += d;
+                    lrun[qq] *= al;
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-                    sacc[kb][qq][i] = __builtin_amdgcn_exp2f(fmaxf(sacc[kb][qq][i] - mnew, kFloor2));
-            mrun[qq] = mnew;
-        }
-        if (diag) {  // masked entries contribute exactly 0 (not the floor value)
+                    for (int db = 0; db < 8; db++) o[db][qq] *= al;
 #pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                const int qpos = qmin + qq * 16 + c;
+                    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = 0.0f;
+                        for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= d;
+                }
             }
-        }
-#pragma unroll
-        for (int qq = 0; qq < 2; qq++) {
-            float ps = 0.f;
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) ps += sacc[kb][qq][i];
-            lrun[qq] = lrun[qq] * alpha[qq] + ps;
-        }
-        if (__any(rescale)) {
+                for (int qq = 0; qq < 2; qq++)
 #pragma unroll
-            for (int db = 0; db < 8; db++)
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) o[db][qq] *= alpha[qq];
-        }
+                    for (int i = 0; i < 4; i++) sacc[kb][qq][i] = __builtin_amdgcn_exp2f(sacc[kb][qq][i]);
 
-        // ---- O^T += V^T P^T ----
+            // ---- O^T += V^T P^T ----
 #pragma unroll
-        for (int ks2 = 0; ks2 < 2; ks2++) {
-            vec pf[2];
+            for (int ks2 = 0; ks2 < 2; ks2++) {
+                vec pf[2];
 #pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                const f32x4 lo = sacc[2 * ks2][qq], hi = sacc[2 * ks2 + 1][qq];
-                const uint4 u = make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]),
-                                           pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]));
-                pf[qq] = __builtin_bit_cast(vec, u);
-            }
+                for (int qq = 0; qq < 2; qq++) {
+                    const f32x4 lo = sacc[2 * ks2][qq], hi = sacc[2 * ks2 + 1][qq];
+                    const uint4 u = make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]),
+                                               pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]));
+                    lrun[qq] = sum2<T>(u.w, sum2<T>(u.z, sum2<T>(u.y, sum2<T>(u.x, lrun[qq]))));
+                    pf[qq] = __builtin_bit_cast(vec, u);
+                }
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                vec vf = __builtin_bit_cast(vec, *(const uint4 *)(&sV[buf][(db * 16 + c) * VLD + ks2 * 32 + grp * 8]));
+                for (int db = 0; db < 8; db++) {
+                    vec vf = __builtin_bit_cast(vec, *(const uint4 *)(&vt[(db * 16 + c) * VLD + ks2 * 32 + grp * 8]));
 #pragma unroll
-                for (int qq = 0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
+                    for (int qq = 0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
+                }
             }
         }
 
         if (more) PF_STASH(buf ^ 1);
         __syncthreads();
+    }
+#undef PF_FETCH
+#undef PF_FETCH_P
+#undef PF_STASH
+
+    // ---- combine the two parities: half 1 hands (m, l, O) to half 0 ----
+    float4 *xo = (float4 *)sK + hw * 17 * 64 + lane;
+    if (half) {
+#pragma unroll
+        for (int db = 0; db < 8; db++)
+#pragma unroll
+            for (int qq = 0; qq < 2; qq++) {
+                const f32x4 v = o[db][qq];
+                xo[(db * 2 + qq) * 64] = make_float4(v[0], v[1], v[2], v[3]);
+            }
+        xo[16 * 64] = make_float4(mrun[0], mrun[1], lrun[0], lrun[1]);
+    }
+    __syncthreads();
+    if (half) return;
+    {
+        const float4 ml = xo[16 * 64];
+        const float m1[2] = {ml.x, ml.y}, l1[2] = {ml.z, ml.w};
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+            const float M = fmaxf(mrun[qq], m1[qq]);
+            const float a0 = exp2f(mrun[qq] - M), a1 = exp2f(m1[qq] - M);
+            mrun[qq] = M;
+            lrun[qq] = lrun[qq] * a0 + l1[qq] * a1;
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                const float4 v = xo[(db * 2 + qq) * 64];
+                o[db][qq] = o[db][qq] * a0 + f32x4{v.x, v.y, v.z, v.w} * a1;
+            }
+        }
     }
 
     // ---- finish: row sums across the 4 lane groups ----
@@ -503,14 +651,14 @@ __global__ __launch_bounds__(256, 2) void prefill_flash_kernel(FlashArgs a) {
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
             const int r = qq * 16 + c;
-            float *po = a.part_o + ((slot * G + wave) * 32 + r) * D + grp * 4;
+            float *po = a.part_o + ((slot * G + hw) * 32 + r) * D + grp * 4;
 #pragma unroll
             for (int db = 0; db < 8; db++) {
                 f32x4 v = o[db][qq];
                 *(float4 *)(po + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
             }
             if (grp == 0) {
-                float *pm = a.part_ml + ((slot * G + wave) * 32 + r) * 2;
+                float *pm = a.part_ml + ((slot * G + hw) * 32 + r) * 2;
                 pm[0] = mrun[qq];
                 pm[1] = lrun[qq];
             }
@@ -522,7 +670,7 @@ hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_item
     (void)total_items;
     const int R = 8 / a.kv_heads;
     const int per_xcd = (a.items_per_kvh + R - 1) / R;
-    dim3 grid(per_xcd * 8), block(256);
+    dim3 grid(per_xcd * 8), block(512);
     switch (kv_dtype) {
     case 1: hipLaunchKernelGGL(prefill_flash_kernel<F16>, grid, block, 0, s, a); break;
     case 2: hipLaunchKernelGGL(prefill_flash_kernel<BF16>, grid, block, 0, s, a); break;
@@ -532,43 +680,58 @@ hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_item
 }
 
 // ------------------------------------------------------------------ merge
+// Combine the split items of a q block: one workgroup per (q block, kv head,
+// head in group, 8-row quarter); thread -> (row, 4 dims).  All (m, l) of the
+// row are read first, then the partial O rows stream with up to 8 loads in
+// flight per thread.
 __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, G = kGroup;
-    const int kvh = blockIdx.x % a.kv_heads;
-    const int qb = blockIdx.x / a.kv_heads;
-    // locate q block qb's items
+    int b = blockIdx.x;
+    const int quarter = b & 3;
+    b >>= 2;
+    const int g = b % G;
+    b /= G;
+    const int kvh = b % a.kv_heads;
+    const int qb = b / a.kv_heads;
     int first = 0, ns = 0;
-    for (int b = a.nqb - 1; b >= 0; b--) {
-        const int n = flash_splits(flash_tiles(a.pos0, b, a.seq), a.cap);
-        if (b == qb) { ns = n; break; }
+    for (int q = a.nqb - 1; q >= 0; q--) {
+        const int n = flash_splits(flash_tiles(a.pos0, q, a.seq), a.cap);
+        if (q == qb) {
+            ns = n;
+            break;
+        }
         first += n;
     }
     if (ns <= 1) return;
-    const int qdim = a.heads * D;
-    const int d = threadIdx.x % D;
-    for (int rr = threadIdx.x / D; rr < G * 32; rr += 256 / D) {
-        const int g = rr / 32, r = rr % 32;
-        const int row = qb * 32 + r;
-        if (row >= a.seq) continue;
-        float M = -INFINITY;
-        for (int s = 0; s < ns; s++) {
-            const size_t slot = (size_t)kvh * a.items_per_kvh + first + s;
-            M = fmaxf(M, a.part_ml[((slot * G + g) * 32 + r) * 2]);
-        }
-        float Ls = 0.f, acc = 0.f;
-        for (int s = 0; s < ns; s++) {
-            const size_t slot = (size_t)kvh * a.items_per_kvh + first + s;
-            const float *pm = a.part_ml + ((slot * G + g) * 32 + r) * 2;
-            const float w = exp2f(pm[0] - M);
-            Ls += w * pm[1];
-            acc = fmaf(w, a.part_o[((slot * G + g) * 32 + r) * D + d], acc);
-        }
-        a.out[(size_t)row * qdim + (size_t)(kvh * G + g) * D + d] = Ls > 0.f ? acc / Ls : 0.f;
+    const int r = quarter * 8 + threadIdx.x / 32;
+    const int row = qb * 32 + r;
+    if (row >= a.seq) return;
+    const int d = (threadIdx.x % 32) * 4;
+    const size_t slot0 = (size_t)kvh * a.items_per_kvh + first;
+    const float *pm = a.part_ml + ((slot0 * G + g) * 32 + r) * 2;
+    const float *po = a.part_o + ((slot0 * G + g) * 32 + r) * D + d;
+    const size_t ml_stride = (size_t)G * 32 * 2, o_stride = (size_t)G * 32 * D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, pm[s * ml_stride]);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    float Ls = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < ns; s++) {
+        const float w = exp2f(pm[s * ml_stride] - M);
+        Ls = fmaf(w, pm[s * ml_stride + 1], Ls);
+        const float4 v = *(const float4 *)(po + s * o_stride);
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
     }
+    const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
+    *(float4 *)(a.out + (size_t)row * a.heads * D + (size_t)(kvh * G + g) * D + d) =
+        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.nqb * a.kv_heads), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.nqb * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -1,16 +1,24 @@
 """fp64 model of the prefill kernel's rounding points.
 
 The MFMA prefill (hymt2sharp_amd/csrc/prefill_attn.hip) differs from the
-fp32 reference in two roundings only: q after RoPE/norm, scaled by
-log2(e)/sqrt(D), is rounded to the MFMA operand type, and each softmax
-weight p = 2^(s - m) is rounded to that type before P*V, where m is the
-running row maximum after the current 64-position kv tile (online softmax).
-The row sum l accumulates the unrounded p.  Work items that split a q
-block's kv range keep their own (m, l, O) and are merged with weights
-2^(m_i - max m).
+fp32 reference in its roundings and its order of accumulation only:
 
-This model reproduces those roundings in fp64 so the GPU result can be
-checked far tighter than against the fp32 oracle.  Test infrastructure only.
+* q after RoPE/norm, scaled by log2(e)/sqrt(D), is rounded to the MFMA
+  operand type;
+* each softmax weight p = 2^(s - m) is rounded to that type before P*V and
+  the row sum l adds the rounded weights;
+* m is a lazy running reference: it starts at the reference's -80 (natural
+  log units) and moves up to the row's tile maximum (if higher) on a wave
+  half's first 64-position tile and on any later tile where some row of the
+  wave's 32 rows has s - m > 8 (then for every row); otherwise m stays, so p
+  may reach 2^8;
+* the tiles of a work item alternate between two wave halves (even and odd
+  tile offsets), each with its own (m, l, O), combined with weights
+  2^(m_i - max m); work items that split a q block's kv range are combined
+  the same way.
+
+This model reproduces those steps in fp64 so the GPU result can be checked
+far tighter than against the fp32 oracle.  Test infrastructure only.
 """
 from __future__ import annotations
 
@@ -20,6 +28,7 @@ from hymt2sharp_amd import BF16, F16
 from hymt2sharp_amd import synth as S
 
 LOG2E = 1.4426950408889634
+ITEM_TILES = 1024  # kItemTiles: kv tiles per work item
 FLOOR2 = np.float32(-80.0 * LOG2E)
 
 
@@ -47,12 +56,48 @@ def split_ranges(pos0, seq, kv_heads, cap=None):
         if pairs < 256:
             per = (256 + pairs - 1) // pairs
             cap = max(4, (max_tiles + per - 1) // per)
+    cap = min(cap, ITEM_TILES)
     out = []
     for qb in range(nqb):
         nt = tiles_of(pos0, qb, seq)
         ns = (nt + cap - 1) // cap
         out.append([(s * nt // ns, (s + 1) * nt // ns) for s in range(ns)])
     return out
+
+
+LAZY = 8.0
+
+
+def _half_softmax(s_rows, vis_rows, tiles, L, V, dtype):
+    """One wave half: online softmax over `tiles` for the q rows given.
+    Returns (m, l, O) with l the sum of the rounded weights."""
+    n, D = s_rows.shape[0], V.shape[1]
+    m = np.full(n, float(FLOOR2))
+    l = np.zeros(n)
+    o = np.zeros((n, D))
+    for k, t in enumerate(tiles):
+        cols = np.arange(t * 64, min(t * 64 + 64, L))
+        sm = np.where(vis_rows[:, cols], s_rows[:, cols] - m[:, None], -np.inf)
+        mt = sm.max(axis=1)
+        if k == 0 or np.any(mt > LAZY):
+            d = np.maximum(mt, 0.0)
+            m = m + d
+            al = np.exp2(-d)
+            l = l * al
+            o = o * al[:, None]
+            sm = sm - d[:, None]
+        p = round_to(np.exp2(sm), dtype)
+        l = l + p.sum(axis=1)
+        o = o + p @ V[cols]
+    return m, l, o
+
+
+def _combine(parts):
+    M = np.max([p[0] for p in parts], axis=0)
+    w = [np.exp2(p[0] - M) for p in parts]
+    lt = sum(wi * p[1] for wi, p in zip(w, parts))
+    ot = sum(wi[:, None] * p[2] for wi, p in zip(w, parts))
+    return M, lt, ot
 
 
 def prefill_model(q_hat, cache_k, cache_v, heads, kv_heads, head_dim, pos0, seq, dtype, cap=None):
@@ -67,36 +112,18 @@ def prefill_model(q_hat, cache_k, cache_v, heads, kv_heads, head_dim, pos0, seq,
     V = np.asarray(cache_v, np.float64)[:L].reshape(L, kv_heads, D)
     out = np.zeros((seq, heads, D))
     ranges = split_ranges(pos0, seq, kv_heads, cap)
+    qpos = pos0 + np.arange(seq)
+    vis = np.arange(L)[None, :] <= qpos[:, None]
     for h in range(heads):
         kvh = h // G
         s_all = qm[:, h, :] @ K[:, kvh, :].T                 # [seq][L]
-        qpos = pos0 + np.arange(seq)
-        vis = np.arange(L)[None, :] <= qpos[:, None]
         for qb, splits in enumerate(ranges):
             rows = np.arange(qb * 32, min(qb * 32 + 32, seq))
-            parts = []
+            items = []
             for (t0, t1) in splits:
-                m = np.full(len(rows), float(FLOOR2))
-                l = np.zeros(len(rows))
-                o = np.zeros((len(rows), D))
-                for t in range(t0, t1):
-                    cols = np.arange(t * 64, min(t * 64 + 64, L))
-                    st = s_all[np.ix_(rows, cols)]
-                    vv = vis[np.ix_(rows, cols)]
-                    mt = np.where(vv, st, -np.inf).max(axis=1)
-                    mnew = np.maximum(m, mt)
-                    alpha = np.exp2(m - mnew)
-                    p = np.where(vv, np.exp2(np.maximum(st - mnew[:, None], float(FLOOR2))), 0.0)
-                    l = l * alpha + p.sum(axis=1)
-                    o = o * alpha[:, None] + round_to(p, dtype) @ V[cols, kvh, :]
-                    m = mnew
-                parts.append((m, l, o))
-            if len(parts) == 1:
-                m, l, o = parts[0]
-                out[rows, h, :] = np.where(l[:, None] > 0, o / np.where(l > 0, l, 1)[:, None], 0)
-            else:
-                M = np.max([p[0] for p in parts], axis=0)
-                lt = sum(np.exp2(p[0] - M) * p[1] for p in parts)
-                ot = sum(np.exp2(p[0] - M)[:, None] * p[2] for p in parts)
-                out[rows, h, :] = ot / lt[:, None]
+                halves = [_half_softmax(s_all[rows], vis[rows], range(t0 + hp, t1, 2), L,
+                                        V[:, kvh, :], dtype) for hp in (0, 1)]
+                items.append(_combine(halves))
+            m, l, o = items[0] if len(items) == 1 else _combine(items)
+            out[rows, h, :] = np.where(l[:, None] > 0, o / np.where(l > 0, l, 1)[:, None], 0)
     return out.reshape(seq, heads * D)
