@@ -279,6 +279,19 @@ def cpu_baseline_prefill(threads, seq=2048):
     return prefill_flops(0, seq) / sec / 1e12, sec
 
 
+def copy_calibration(nbytes=64 << 20, reps=3):
+    """Device-to-device copies of a known size: the reference point for the
+    FETCH_SIZE / WRITE_SIZE counters (each copy reads and writes `nbytes`)."""
+    from hymt2sharp_amd import _native as N
+    be = HipBackend(0)
+    src, dst = be.alloc(nbytes), be.alloc(nbytes)
+    for _ in range(reps):
+        N.check(be._lib.hymt_memcpy(be.handle, ctypes.c_void_p(dst), ctypes.c_void_p(src), nbytes, 2))
+    be.free(src)
+    be.free(dst)
+    be.Dispose()
+
+
 def load_traffic():
     """HBM bytes per call measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (scaled by the same counters on a copy of known size), kept beside the
@@ -304,12 +317,16 @@ def main():
     ap.add_argument("--only", choices=["decode", "prefill", "configs"], default=None,
                     help="run one leg: the config-2 decode step, the config-3 prefill, "
                          "or the other configurations (1, 4, 5)")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run 64 MiB device copies (counter calibration for profiles)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the attention path has no multi-GPU mode in this "
               f"build (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
 
+    if args.calibrate:
+        copy_calibration()
     dec = pre = None
     extra = {}
     if args.only in (None, "decode"):
