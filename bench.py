@@ -99,7 +99,8 @@ def decode_pool(config, ctx, n=8):
             for i in range(n)]
 
 
-def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30):
+def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30,
+                norm=True):
     """Decode attention at position `ctx` (L = ctx + 1) over distinct layers.
 
     A step is `layers_per_step` decode calls, one per layer, in stream order
@@ -108,7 +109,8 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     that the resident set exceeds `min_bytes`, so the 256 MiB MALL cannot
     serve the KV reads.  Inputs (q, k, v, gammas) are device-resident.
     Returns per-call and per-step times from HIP events on the backend's
-    stream around the whole timed region."""
+    stream around the whole timed region.  norm=False passes no gamma
+    vectors (the QK norm step is skipped)."""
     L = ctx + 1
     kvb = 4 if kv_dtype == F32 else 2
     bpl = decode_bytes_per_layer(L, kvb)
@@ -136,7 +138,8 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         for l in range(layers_per_step):
             i = base_layer + l
             be.decode_dev(i, ctx, dq + i * HQ * D * 4, dk + i * HKV * D * 4, dv + i * HKV * D * 4,
-                          dgq + i * D * 4, dgk + i * D * 4, dout + i * HQ * D * 4)
+                          dgq + i * D * 4 if norm else None, dgk + i * D * 4 if norm else None,
+                          dout + i * HQ * D * 4)
 
     ev = HipEvents(be.stream())
     for s in range(warmup):
@@ -334,9 +337,9 @@ def main():
     if args.only in (None, "prefill"):
         pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup)
     if args.only in (None, "configs"):
-        c1 = time_decode(1, 512, F32, args.steps, args.warmup)
-        extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, no QK norm weights "
-                                        "in the reference config (gammas applied here)",
+        c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False)
+        extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, QK norm off "
+                                        "(the configuration names none)",
                             "unit": "GB/s", "value": round(c1["gbs"], 1), **r4(c1)}
         c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup)
         extra["config4"] = {"workload": "prefill chunk 256 at positions 8192..8447 over an "

@@ -140,7 +140,10 @@ int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const fl
  * Causal prefill attention for one layer: `seq` tokens at positions
  * [pos, pos+seq), attending over [0, pos+row].  Same steps as decode; K/V of
  * the chunk are written into the cache.  q/k/v are fp32 or bf16 as io_dtype;
- * out is fp32.  Cache dtype f16 or bf16 (MFMA operand type); f32 caches
+ * out is fp32.  The row maximum starts at -80 as in Ops.SoftmaxRow; the
+ * per-weight clamp at -80 below the maximum is not applied (such weights are
+ * below 2e-35 of the largest, under fp32 resolution of the row sum).
+ * Cache dtype f16 or bf16 (MFMA operand type); f32 caches
  * return HYMT_E_UNSUPPORTED.  Replaces HunyuanDenseModel.PrefillAttention
  * lines 53-83 (HunyuanDenseModel.Prefill.cs), the pf_kvprep + pf_fa32 pair
  * of the Vulkan backend (VulkanBackend.cs:786-802).
