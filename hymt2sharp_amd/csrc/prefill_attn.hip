@@ -85,61 +85,78 @@ __device__ __forceinline__ void load8_in(const void *base, size_t i, bool bf16, 
 }
 
 // ------------------------------------------------------------------ k/v
-// Block (16-position block tb, kv head); thread (row = tid/16, dims 8*(tid%16)..).
+// Block (16-position block, kv head); thread (row = tid/16, dims 8*(tid%16)..).
+// Every global load (k, v, the row's cos/sin, gamma) is issued before any
+// math.  The RoPE partner of dim d (d +- rope_dim/2) lives in lane
+// c ^ (rope_dim/16) of the same 16-lane row and is fetched by a lane shuffle;
+// the norm's sum of squares is a DPP reduction over the row.  K is written as
+// one 16-byte store per thread; V is transposed through LDS into the page's
+// 16-position V^T sub-tile.
 template <typename T>
 __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     constexpr int D = kHeadDim, P = kPage;
     using S = typename T::storage;
-    __shared__ float s_x[16][D];
+    static_assert(sizeof(S) == 2, "prefill caches are 16-bit");
     __shared__ __attribute__((aligned(16))) S s_v[16][D];
     const int kvh = blockIdx.y, Hkv = a.kv_heads;
     const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
     const int pstart = (a.pos0 & ~15) + 16 * blockIdx.x;  // 16-aligned block start
-    const int pos = pstart + r, m = pos - a.pos0;
+    const int m = pstart + r - a.pos0;                    // row within the chunk
     const bool valid = m >= 0 && m < a.seq;
+    const int mc = m < 0 ? 0 : (m < a.seq ? m : a.seq - 1);  // clamped for loads
     const int phys = a.tab[pstart / P];
     const size_t page_base = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
-    const int t = pstart % P + r;  // row within the page
-    float x[8], v[8];
-    if (valid) {
-        load8_in(a.k, (size_t)m * Hkv * D + (size_t)kvh * D + 8 * c, a.io_bf16, x);
-        load8_in(a.v, (size_t)m * Hkv * D + (size_t)kvh * D + 8 * c, a.io_bf16, v);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = v[e] = 0.0f;
+    const int d0 = 8 * c, rh = a.rope_half;
+    const size_t src = (size_t)mc * Hkv * D + (size_t)kvh * D + d0;
+
+    float x[8], v[8], cs[8], sn[8], gw[8];
+    load8_in(a.k, src, a.io_bf16, x);
+    load8_in(a.v, src, a.io_bf16, v);
+    const bool rot = d0 < a.rope_dim;
+    if (rot) {
+        const size_t rb = (size_t)(a.pos0 + mc) * rh + (d0 & (rh - 1));
+        const float4 c0 = *(const float4 *)(a.rope_cos + rb), c1 = *(const float4 *)(a.rope_cos + rb + 4);
+        const float4 s0 = *(const float4 *)(a.rope_sin + rb), s1 = *(const float4 *)(a.rope_sin + rb + 4);
+        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
     }
+    if (a.knw) {
+        const float4 g0 = *(const float4 *)(a.knw + d0), g1 = *(const float4 *)(a.knw + d0 + 4);
+        gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w; gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
+    }
+
+    // V: round into LDS now, transpose after the barrier below
+    {
+        uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 8; e++) s_x[r][8 * c + e] = x[e];
-    __syncthreads();
+        for (int e = 0; e < 4; e++)
+            w[e] = (uint32_t)to_elem<T>(v[2 * e]) | ((uint32_t)to_elem<T>(v[2 * e + 1]) << 16);
+        *(uint4 *)&s_v[r][d0] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+
     // RoPE (Ops.RopeRange, Ops.cs:157-165) then RMSNorm of the k row
-    const int half = a.rope_half;
-    const float *cs = a.rope_cos + (size_t)(valid ? pos : 0) * half;
-    const float *sn = a.rope_sin + (size_t)(valid ? pos : 0) * half;
+    const int pl = rh >> 3;  // partner lane distance: 8 (rope 128) or 4 (rope 64)
+    const bool lower = (d0 & rh) == 0;
     float y[8], ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const int d = 8 * c + e;
-        if (d < half) y[e] = x[e] * cs[d] - s_x[r][d + half] * sn[d];
-        else if (d < a.rope_dim) y[e] = s_x[r][d - half] * sn[d - half] + x[e] * cs[d - half];
-        else y[e] = x[e];
+        const float xp = pl ? __shfl_xor(x[e], pl, 16) : 0.0f;
+        y[e] = !rot ? x[e] : lower ? x[e] * cs[e] - xp * sn[e] : xp * sn[e] + x[e] * cs[e];
         ss += y[e] * y[e];
     }
     if (a.knw) {
         ss = dpp_sum16(ss);
         const float rr = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
-        for (int e = 0; e < 8; e++) y[e] = y[e] * rr * a.knw[8 * c + e];
+        for (int e = 0; e < 8; e++) y[e] = y[e] * rr * gw[e];
     }
     if (valid) {
-        S ks[8];
+        uint32_t w[4];
 #pragma unroll
-        for (int e = 0; e < 8; e++) ks[e] = to_elem<T>(y[e]);
-        S *dst = (S *)a.kpool + page_base + (size_t)t * D + 8 * c;
-#pragma unroll
-        for (int e = 0; e < 8; e++) dst[e] = ks[e];
+        for (int e = 0; e < 4; e++)
+            w[e] = (uint32_t)to_elem<T>(y[2 * e]) | ((uint32_t)to_elem<T>(y[2 * e + 1]) << 16);
+        *(uint4 *)((S *)a.kpool + page_base + (size_t)(pstart % P + r) * D + d0) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-#pragma unroll
-    for (int e = 0; e < 8; e++) s_v[r][8 * c + e] = to_elem<T>(v[e]);
     __syncthreads();
     // V^T sub-tile [d][16]: thread -> (d = tid/2, positions 8*(tid%2) + [0,8))
     {
