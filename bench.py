@@ -100,7 +100,7 @@ def decode_pool(config, ctx, n=8):
 
 
 def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30,
-                norm=True):
+                norm=True, graph=True):
     """Decode attention at position `ctx` (L = ctx + 1) over distinct layers.
 
     A step is `layers_per_step` decode calls, one per layer, in stream order
@@ -133,7 +133,7 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     for dptr, arr in ((dq, q), (dk, k), (dv, v), (dgq, gq), (dgk, gk)):
         be.upload(dptr, arr)
 
-    def step(s):
+    def record(s):
         base_layer = (s % nsets) * layers_per_step
         for l in range(layers_per_step):
             i = base_layer + l
@@ -142,6 +142,18 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
                           dout + i * HQ * D * 4)
 
     ev = HipEvents(be.stream())
+    for s in range(max(warmup, nsets)):  # every layer set once eagerly before recording
+        record(s)
+    be.sync()
+    graphs = []
+    if graph:
+        for s in range(nsets):
+            be.graph_begin()
+            record(s)
+            graphs.append(be.graph_end())
+        step = lambda s: be.graph_launch(graphs[s % nsets])  # noqa: E731
+    else:
+        step = record
     for s in range(warmup):
         step(s)
     be.sync()
@@ -158,6 +170,8 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     gpu_ms = ev.elapsed_ms(e0, e1)
     ev.destroy(e0)
     ev.destroy(e1)
+    for g in graphs:
+        be.graph_destroy(g)
 
     out = np.empty((nl, HQ * D), np.float32)
     be.download(out, dout)
@@ -174,6 +188,7 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         "wall_ms_per_step": wall * 1e3 / steps,
         "call_us": call_us,
         "host_submit_us_per_call": t_submit * 1e6 / calls,
+        "submission": "recorded step (hymt_graph_launch)" if graph else "one hymt_attn_decode per layer",
         "gbs": bpl / (call_us * 1e-6) / 1e9,
         "bytes_per_layer": bpl,
         "layers_resident": nl,
@@ -334,6 +349,7 @@ def main():
     extra = {}
     if args.only in (None, "decode"):
         dec = time_decode(2, CTX, F16, args.steps, args.warmup)
+        eager = time_decode(2, CTX, F16, args.steps, args.warmup, graph=False)
     if args.only in (None, "prefill"):
         pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup)
     if args.only in (None, "configs"):
@@ -383,12 +399,15 @@ def main():
         rec["value"] = round(dec["gbs"], 1)
         rec["ms_per_step"] = round(dec["ms_per_step"], 4)
         rec["decode"] = r4(dec)
+        rec["decode_eager"] = {"call_us": round(eager["call_us"], 3), "gbs": round(eager["gbs"], 1),
+                               "host_submit_us_per_call": round(eager["host_submit_us_per_call"], 3),
+                               "submission": eager["submission"]}
         rec["roofline"] = {"bound": "hbm", "achieved": round(dec["gbs"], 1),
                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                            "traffic": traffic.get("decode_config2"),
-                           "kernel": "decode_attn_mfma_kernel<F16,true> + decode_merge_kernel "
-                                     "(one decode call)",
+                           "kernel": "decode_attn_mfma_kernel<F16> + decode_merge_kernel "
+                                     "(one decode call, both launches)",
                            "algorithmic_bytes": dec["bytes_per_layer"],
                            "avg_us": round(dec["call_us"], 3)}
     if pre:

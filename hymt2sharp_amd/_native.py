@@ -86,6 +86,10 @@ SIGNATURES = {
     "hymt_dev_alloc": [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)],
     "hymt_dev_free": [_vp, _vp],
     "hymt_memcpy": [_vp, _vp, _vp, ctypes.c_size_t, _i],
+    "hymt_graph_begin": [_vp],
+    "hymt_graph_end": [_vp, ctypes.POINTER(_vp)],
+    "hymt_graph_launch": [_vp, _vp],
+    "hymt_graph_destroy": [_vp, _vp],
 }
 
 _lib = None

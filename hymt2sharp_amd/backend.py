@@ -160,6 +160,23 @@ class HipBackend:
         N.check(self._lib.hymt_get_stream(self._h, ctypes.byref(s)))
         return s.value
 
+    # -- recorded call sequences (HIP graphs) ----------------------------
+    def graph_begin(self):
+        """Start recording device-pointer calls on the context's stream
+        (the recorded decode command buffer of VulkanBackend.cs:400-568)."""
+        N.check(self._lib.hymt_graph_begin(self._h))
+
+    def graph_end(self) -> int:
+        g = ctypes.c_void_p()
+        N.check(self._lib.hymt_graph_end(self._h, ctypes.byref(g)))
+        return g.value
+
+    def graph_launch(self, g: int):
+        N.check(self._lib.hymt_graph_launch(self._h, g))
+
+    def graph_destroy(self, g: int):
+        N.check(self._lib.hymt_graph_destroy(self._h, g))
+
     # -- IDisposable ------------------------------------------------------
     def Dispose(self):
         if self._h:

@@ -41,7 +41,6 @@ struct DecodeArgs {
     void *vpool;        // this layer's V pool
     float *part_ml;     // [Hq][kMaxSplits][2]
     float *part_acc;    // [Hq][kMaxSplits][D]
-    uint32_t *counters; // [Hkv], zero between launches
     float *out;         // [Hq*D]
     int L;              // positions attended = pos + 1
     int kv_heads;
@@ -51,7 +50,6 @@ struct DecodeArgs {
     int ppw;            // pages per split
     float eps;
     float qscale;       // log2(e) / sqrt(D)
-    int merge_inline;   // 1: last workgroup merges splits; 0: decode_merge_kernel
     int pages_in_args;  // 1: pages[] below holds tab[0, npages) (npages <= kArgPages)
     int32_t pages[kArgPages];  // physical page of each logical block, saving a
                                // dependent table load before the K/V stream

@@ -10,15 +10,17 @@
 // Work split (flash-decoding, as the reference's Metal attn_split/attn_merge,
 // MslDecodeKernels.cs:172-300, but over KV heads so that each K/V byte is read
 // from HBM once for all 4 q heads of its GQA group):
-//   workgroup = (split, kv head), 4 waves, `ppw` 64-position pages per split.
-//   Wave w owns positions [16w, 16w+16) of every page of its split and runs
-//   its own online softmax over them: no workgroup barrier on the streaming
-//   path.  A wave's 16 K rows and its 16x128 V^T sub-tile are each one
-//   contiguous 4 KiB block; every load is a 16-byte vector.
-//   The 4 wave partials are combined through LDS into one (m, l, acc[128])
-//   per q head and split; splits are merged either by a second small kernel
-//   or, with merge_inline, by the last workgroup of each kv head to finish
-//   (device-coherent sc1 stores/loads and an atomic ticket; no cache flush).
+//   workgroup = (split, kv head), 4 waves, `ppw` 64-position pages per split
+//   (one page per split until the split count reaches kMaxSplits, so a
+//   4k-context layer spreads over 260 workgroups, every CU).
+//   Wave w owns positions [16w, 16w+16) of every page of its split.  A wave's
+//   16 K rows and its 16x128 V^T sub-tile are each one contiguous 4 KiB block.
+//   The kernel is latency-bound at decode sizes, so the prologue is ordered
+//   for the shortest dependent chain: page ids (scalar loads) first, then the
+//   q rows, then the K/V stream; no workgroup barrier before the final
+//   combine of the 4 wave partials.  Splits are merged by a second launch.
+#include <algorithm>
+
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
 
@@ -36,15 +38,6 @@ template <typename T> struct DecodeShape {
     static constexpr int VDPI = 64 / VCPD;    // V^T rows per wave load (32 or 16)
     static constexpr int VLD = D / VDPI;      // V loads per lane per sub-tile
 };
-
-// Device-coherent (agent scope) accesses: sc1 on gfx950, visible across XCDs
-// without writing back or invalidating whole L2 caches.
-__device__ __forceinline__ void store_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_coherent(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // RoPE (Ops.RopeRange, Ops.cs:157-165) of element d of one head row whose
 // values at d and at its rotation partner are x and xp.
@@ -102,27 +95,12 @@ struct RowIn {
 };
 
 // Combine the 4 wave partials of one split (s_m, s_l, s_acc in LDS, after a
-// workgroup barrier) and either finish the output (single split), store the
-// split partial for decode_merge_kernel, or merge inline when this is the
-// last split of its kv head.
-struct SplitLds {
-    float (*m)[kGroup];
-    float (*l)[kGroup];
-    float (*acc)[kGroup][kHeadDim];
-    float (*w)[kMaxSplits];
-    float *L;
-    uint32_t *ticket;
-};
-
+// workgroup barrier) and either finish the output (single split) or store
+// the split partial for decode_merge_kernel.
 __device__ __forceinline__ void split_epilogue(const DecodeArgs &a, int kvh, int split, int tid,
-                                               const SplitLds &sl) {
+                                               const float (&s_m)[4][kGroup], const float (&s_l)[4][kGroup],
+                                               const float (&s_acc)[4][kGroup][kHeadDim]) {
     constexpr int D = kHeadDim, G = kGroup;
-    auto &s_m = sl.m;
-    auto &s_l = sl.l;
-    auto &s_acc = sl.acc;
-    auto &s_w = sl.w;
-    float *s_L = sl.L;
-    uint32_t &s_ticket = *sl.ticket;
     const int g = tid >> 6, d0 = (tid & 63) * 2;  // thread -> head g, dims d0, d0+1
     const int h = kvh * G + g;
     float M = s_m[0][g];
@@ -136,76 +114,13 @@ __device__ __forceinline__ void split_epilogue(const DecodeArgs &a, int kvh, int
         o0 = fmaf(sc, s_acc[w][g][d0], o0);
         o1 = fmaf(sc, s_acc[w][g][d0 + 1], o1);
     }
-
     if (a.nsplit == 1) {
         const float inv = Lw > 0.0f ? 1.0f / Lw : 0.0f;
         *(float2 *)(a.out + (size_t)h * D + d0) = make_float2(o0 * inv, o1 * inv);
         return;
     }
-
-    float *pacc = a.part_acc + ((size_t)h * kMaxSplits + split) * D + d0;
-    float *pml = a.part_ml + ((size_t)h * kMaxSplits + split) * 2;
-    if (!a.merge_inline) {
-        *(float2 *)pacc = make_float2(o0, o1);
-        if (d0 == 0) *(float2 *)pml = make_float2(M, Lw);
-        return;
-    }
-
-    // ---- inline merge: the last split of this kv head combines all splits ---
-    store_coherent(pacc, o0);
-    store_coherent(pacc + 1, o1);
-    if (d0 == 0) {
-        store_coherent(pml, M);
-        store_coherent(pml + 1, Lw);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
-    __syncthreads();
-    if (tid == 0)
-        s_ticket = __hip_atomic_fetch_add(&a.counters[kvh], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s_ticket != (uint32_t)(a.nsplit - 1)) return;
-
-    {
-        const float *ml = a.part_ml + (size_t)h * kMaxSplits * 2;
-        float mloc = -INFINITY;
-        for (int s = tid & 63; s < a.nsplit; s += 64) mloc = fmaxf(mloc, load_coherent(ml + 2 * s));
-        const float Mg = group_max<64>(mloc);
-        float lsum = 0.0f;
-        for (int s = tid & 63; s < a.nsplit; s += 64) {
-            const float w = exp2f(load_coherent(ml + 2 * s) - Mg);
-            s_w[g][s] = w;
-            lsum = fmaf(w, load_coherent(ml + 2 * s + 1), lsum);
-        }
-        lsum = group_sum<64>(lsum);
-        if ((tid & 63) == 0) s_L[g] = lsum;
-    }
-    __syncthreads();
-    {
-        const float *pa = a.part_acc + (size_t)h * kMaxSplits * D + d0;
-        float r0 = 0.0f, r1 = 0.0f;
-        int s = 0;
-        for (; s + 16 <= a.nsplit; s += 16) {
-            float x0[16], x1[16];
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                x0[i] = load_coherent(pa + (size_t)(s + i) * D);
-                x1[i] = load_coherent(pa + (size_t)(s + i) * D + 1);
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                r0 = fmaf(s_w[g][s + i], x0[i], r0);
-                r1 = fmaf(s_w[g][s + i], x1[i], r1);
-            }
-        }
-        for (; s < a.nsplit; s++) {
-            r0 = fmaf(s_w[g][s], load_coherent(pa + (size_t)s * D), r0);
-            r1 = fmaf(s_w[g][s], load_coherent(pa + (size_t)s * D + 1), r1);
-        }
-        const float l = s_L[g];
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        *(float2 *)(a.out + (size_t)h * D + d0) = make_float2(r0 * inv, r1 * inv);
-    }
-    if (tid == 0) a.counters[kvh] = 0u;
+    *(float2 *)(a.part_acc + ((size_t)h * kMaxSplits + split) * D + d0) = make_float2(o0, o1);
+    if (d0 == 0) *(float2 *)(a.part_ml + ((size_t)h * kMaxSplits + split) * 2) = make_float2(M, Lw);
 }
 
 template <typename T, bool MULTI>
@@ -231,9 +146,6 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
     __shared__ float s_p[4][G][SUB];
     __shared__ float s_acc[4][G][D];
     __shared__ float s_m[4][G], s_l[4][G];
-    __shared__ float s_w[G][kMaxSplits];
-    __shared__ float s_L[G];
-    __shared__ uint32_t s_ticket;
 
     const size_t page_elems = (size_t)P * D;
     const S *kpool = (const S *)a.kpool;
@@ -437,7 +349,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
         }
     }
     __syncthreads();
-    split_epilogue(a, kvh, split, tid, SplitLds{s_m, s_l, s_acc, s_w, s_L, &s_ticket});
+    split_epilogue(a, kvh, split, tid, s_m, s_l, s_acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -503,7 +415,83 @@ __device__ __forceinline__ uint32_t dpp_from_minus4(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);
 }
 
-template <typename T, bool MULTI>
+// Sum over all 64 lanes on the VALU: DPP within 16-lane rows, then the
+// row swaps (no LDS round trip).
+__device__ __forceinline__ float wave_sum64(float v) { return xrow32_sum(xrow16_sum(dpp_sum16(v))); }
+
+// NR consecutive head rows (q heads of one GQA group, or one k row) held as
+// lanes (d, d+64).  All loads -- rows, rotation partners, cos/sin, gamma --
+// are issued by load() before any use, in straight-line code, so they share
+// one memory round trip and can be issued ahead of the K/V stream; finish()
+// applies RoPE then RMSNorm (HunyuanDenseModel.Decode.cs:80-85).
+// FULL: rotary width 128 (half 64), the partner of d is d^64 in the same
+// lane and no partner loads are needed.
+template <int NR, bool FULL> struct RowsIn {
+    float x[NR][2], xp[NR][2], c[2], s[2], w[2];
+    __device__ __forceinline__ void load(const float *rows, const float *cosr, const float *sinr,
+                                         const float *gamma, int lane, int half, int rdim) {
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            x[r][0] = rows[r * kHeadDim + lane];
+            x[r][1] = rows[r * kHeadDim + lane + 64];
+        }
+        w[0] = gamma ? gamma[lane] : 1.0f;
+        w[1] = gamma ? gamma[lane + 64] : 1.0f;
+        if constexpr (FULL) {
+            c[0] = c[1] = cosr[lane];
+            s[0] = s[1] = sinr[lane];
+        } else {
+            // partner index d when d is not rotated; table index 0 then (the
+            // table has at least one column whenever rdim > 0)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int d = lane + 64 * e;
+#pragma unroll
+                for (int r = 0; r < NR; r++) xp[r][e] = rows[r * kHeadDim + rope_partner(d, half, rdim)];
+                c[e] = rdim > 0 ? cosr[rope_index(d, half, rdim)] : 1.0f;
+                s[e] = rdim > 0 ? sinr[rope_index(d, half, rdim)] : 0.0f;
+            }
+        }
+    }
+    // Row r: RoPE (Ops.cs:157-165) then y = x * (1/sqrt(sum x^2/D + eps)) * gamma
+    // (Ops.cs:62-88), times `scale`.
+    __device__ __forceinline__ void finish(int r, float (&y)[2], int lane, int half, int rdim, bool norm,
+                                           float eps, float scale) const {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float p = FULL ? x[r][1 - e] : xp[r][e];
+            y[e] = FULL ? (e == 0 ? x[r][0] * c[0] - p * s[0] : p * s[1] + x[r][1] * c[1])
+                        : rope_elem(lane + 64 * e, x[r][e], p, c[e], s[e], half, rdim);
+        }
+        if (norm) {
+            const float ss = wave_sum64(y[0] * y[0] + y[1] * y[1]);
+            const float rr = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
+            y[0] = y[0] * rr * w[0];
+            y[1] = y[1] * rr * w[1];
+        }
+        y[0] *= scale;
+        y[1] *= scale;
+    }
+};
+
+// f16 / bf16 decode.
+//   The cached positions [0, pos) are split by pages: workgroup (split, kv
+//   head), 4 waves; wave w streams the 16-position sub-tile [16w, 16w+16) of
+//   each of the split's pages.
+//     S = K_sub . Qcat^T, lane (grp, c<4) gets head c at positions 4*grp + i
+//     (its hi part; lanes c+4 hold the lo part).
+//     O += Pcat . V_sub, lane (grp, c) gets rows 4*grp + i of dims 16*db + c,
+//     rows 0-3 = hi(P) of the 4 heads, rows 4-7 = lo(P).
+//   The new token (position pos) is one more position.  Wave 3 of the last
+//   split computes it on the VALU from registers -- its K after RoPE + norm,
+//   both rows rounded to the cache type as the reference reads them back from
+//   its cache -- and adds it to the split's combine as a fifth partial; the
+//   same wave appends the row to the cache at the end.  So no workgroup is
+//   spent on a page that holds only the new token (L = 4097 runs exactly 256
+//   workgroups), and no MFMA operand needs patching.
+// PAGES_ARG: page ids come from the kernel arguments, else from the device
+// page table; both are scalar loads issued first.
+template <typename T, bool MULTI, bool PAGES_ARG, bool FULL>
 __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     constexpr int D = kHeadDim, G = kGroup, P = kPage, SUB = 16;
     using M = DecMfma<T>;
@@ -513,102 +501,117 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     const int Hkv = a.kv_heads;
     const int kvh = blockIdx.x % Hkv;
     const int split = blockIdx.x / Hkv;
-    const int npages = (a.L + P - 1) / P;
+    const int newpos = a.L - 1;                // cached positions [0, newpos)
+    const int ncp = (newpos + P - 1) / P;      // cached pages
     const int page0 = split * a.ppw;
-    const int page_end = MULTI ? min(page0 + a.ppw, npages) : page0 + 1;
-    const int newpos = a.L - 1;
-    const bool owner = page_end == npages;
+    const int page_end = min(page0 + (MULTI ? a.ppw : 1), ncp);
+    const bool last = split == a.nsplit - 1;
+    const bool extra = last && wave == 3;      // the wave that adds the new token
 
-    __shared__ float s_q[G][D];
-    __shared__ __attribute__((aligned(16))) uint16_t s_knew[D];
-    __shared__ uint16_t s_vnew[D];
-    __shared__ float s_acc[4][G][D];
-    __shared__ float s_m[4][G], s_l[4][G];
-    __shared__ float s_w[G][kMaxSplits];
-    __shared__ float s_L[G];
-    __shared__ uint32_t s_ticket;
+    __shared__ __attribute__((aligned(16))) uint16_t s_qop[4][2][G][D];  // per wave: hi/lo q
+    __shared__ __attribute__((aligned(16))) float s_o[4][2][D][G];       // per wave: hi/lo rows
+    __shared__ __attribute__((aligned(16))) float s_xo[D][G];            // the new token
+    __shared__ float s_m[5][G], s_l[5][G];                                // [4]: the new token
 
     const size_t page_elems = (size_t)P * D;
     const uint16_t *kpool = (const uint16_t *)a.kpool;
     const uint16_t *vpool = (const uint16_t *)a.vpool;
     const int half = a.rope_half, rdim = a.rope_dim;
 
-    RowIn qin, nin;
-    qin.load(a.q + (size_t)(kvh * G + wave) * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
-    if (owner && wave == 0)
-        nin.load(a.knew + (size_t)kvh * D, a.rope_cos, a.rope_sin, a.knw, lane, half, rdim);
-    if (owner && wave == 1)
-        nin.load(a.vnew + (size_t)kvh * D, a.rope_cos, a.rope_sin, nullptr, lane, half, rdim);
+    // ---- 1. page ids: the K/V addresses hang on them -----------------------
+    // Loads are never skipped by a branch: after a conditional block of loads
+    // the wait counts must cover the path without them, which makes every
+    // later wait drain the K/V stream.  Look-ahead pages past the split clamp
+    // to its last page (a re-read from L2); with no cached page (pos = 0) the
+    // page of pos is read and ignored.
+    auto page_id = [&](int p) { return PAGES_ARG ? a.pages[p] : a.tab[p]; };
+    const int plast = max(page_end - 1, page0);
+    const int phys0 = page_id(page0);
+    const int phys1 = MULTI ? page_id(min(page0 + 1, plast)) : 0;
 
+    // ---- 2. q rows and the new k, v rows ------------------------------------
+    // vmcnt retires in order: these small rows are issued ahead of the K/V
+    // stream so the q operand is built while it is in flight.  Every wave
+    // loads the new rows (1.5 KiB, cached) so that all loads sit in one
+    // straight-line block.
+    RowsIn<G, FULL> qin;
+    RowsIn<1, FULL> kin;
+    qin.load(a.q + (size_t)kvh * G * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
+    kin.load(a.knew + (size_t)kvh * D, a.rope_cos, a.rope_sin, a.knw, lane, half, rdim);
+    const float vnew0 = a.vnew[(size_t)kvh * D + lane];
+    const float vnew1 = a.vnew[(size_t)kvh * D + lane + 64];
+
+    // ---- 3. the K/V stream --------------------------------------------------
     // K A-operand: lane (grp, c) = K row c, dims 32*ks + 8*grp + [0, 8)
     // V B-operand: lane (grp, c) = V^T row 16*db + c, positions 4*grp + [0, 4)
+    // Whole sub-tiles are loaded (pages are fully allocated); rows at or past
+    // pos are masked out of the scores and zeroed in V before use.
     uint4 ka[4], kn[4];
     uint2 vb[8], vn[8];
-    auto load_sub = [&](int page, uint4 *kk, uint2 *vv) {
-        const int base = page * P + SUB * wave;
-        const int inmem = newpos - base;  // rows < inmem are resident
-        const int phys = a.pages_in_args ? a.pages[page] : a.tab[page];
+    auto load_sub = [&](int phys, uint4 *kk, uint2 *vv) {
         const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)(SUB * wave) * D;
         const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)wave * D * SUB;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-            kk[ks] = c < inmem ? *(const uint4 *)(kp + (size_t)c * D + 32 * ks + 8 * grp) : make_uint4(0, 0, 0, 0);
+        for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + (size_t)c * D + 32 * ks + 8 * grp);
 #pragma unroll
-        for (int db = 0; db < 8; db++)
-            vv[db] = 4 * grp < inmem ? *(const uint2 *)(vp + (size_t)(16 * db + c) * SUB + 4 * grp) : make_uint2(0, 0);
+        for (int db = 0; db < 8; db++) vv[db] = *(const uint2 *)(vp + (size_t)(16 * db + c) * SUB + 4 * grp);
     };
-    load_sub(page0, ka, vb);
-    if (MULTI && page0 + 1 < page_end) load_sub(page0 + 1, kn, vn);  // two pages in flight
+    load_sub(phys0, ka, vb);
+    if (MULTI) load_sub(phys1, kn, vn);  // two pages in flight
 
-    {
-        float y[2];
-        qin.finish(y, lane, half, rdim, a.qnw != nullptr, a.eps);
-        s_q[wave][lane] = y[0] * a.qscale;
-        s_q[wave][lane + 64] = y[1] * a.qscale;
-    }
-    if (owner && wave < 2) {
-        const int t = newpos % P;
-        const int phys = a.pages_in_args ? a.pages[newpos / P] : a.tab[newpos / P];
-        if (wave == 0) {
-            float y[2];
-            nin.finish(y, lane, half, rdim, a.knw != nullptr, a.eps);
-            uint16_t *kp = (uint16_t *)kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)t * D;
+    // ---- 4. q operand: RoPE + norm, hi/lo split, through this wave's LDS ----
+    uint16_t(&sq)[2][G][D] = s_qop[wave];
+    float qy[G][2];  // fp32 q (scaled), kept for the new token
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const uint16_t st = to_elem<T>(y[e]);
-                kp[lane + 64 * e] = st;
-                s_knew[lane + 64 * e] = st;
-            }
-        } else {
-            uint16_t *vp = (uint16_t *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
+    for (int g = 0; g < G; g++) {
+        qin.finish(g, qy[g], lane, half, rdim, a.qnw != nullptr, a.eps, a.qscale);
 #pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int d = lane + 64 * e;
-                const uint16_t st = to_elem<T>(nin.x[e]);
-                vp[v_off(t, d)] = st;
-                s_vnew[d] = st;
-            }
+        for (int e = 0; e < 2; e++) {
+            const uint32_t pr = split_pair<T>(qy[g][e]);
+            sq[0][g][lane + 64 * e] = (uint16_t)pr;
+            sq[1][g][lane + 64 * e] = (uint16_t)(pr >> 16);
         }
     }
-    __syncthreads();
-
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // Qcat B-operand: lane (grp, c), dims 32*ks + 8*grp + [0, 8):
     // c < 4 -> hi(q_c), 4 <= c < 8 -> lo(q_{c-4}), else 0
     uint4 qb[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-        uint32_t w[4] = {0u, 0u, 0u, 0u};
-        if (c < 8) {
-            const float *qrow = s_q[c & 3] + 32 * ks + 8 * grp;
+    for (int ks = 0; ks < 4; ks++)
+        qb[ks] = c < 8 ? *(const uint4 *)&sq[c >> 2][c & 3][32 * ks + 8 * grp] : make_uint4(0, 0, 0, 0);
+
+    // ---- 5. the new token: K after RoPE + norm and V, rounded to the cache
+    // type (Ops.ConvertToBf16, Ops.cs:658-680), then its weight for each head
+    // in the softmax's base-2 units: m = max(s, floor), l = exp2(max(s-m, floor)).
+    // Its cache stores are issued at the end: vmcnt retires in order, so
+    // stores issued here would hold up every later wait on the K/V stream.
+    uint16_t knew_st[2] = {0, 0}, vnew_st[2] = {0, 0};
+    if (extra) {
+        float ky[2];
+        kin.finish(0, ky, lane, half, rdim, a.knw != nullptr, a.eps, 1.0f);
+        knew_st[0] = to_elem<T>(ky[0]);
+        knew_st[1] = to_elem<T>(ky[1]);
+        vnew_st[0] = to_elem<T>(vnew0);
+        vnew_st[1] = to_elem<T>(vnew1);
+        const float k0 = from_elem<T>(knew_st[0]), k1 = from_elem<T>(knew_st[1]);
+        const float v0 = from_elem<T>(vnew_st[0]), v1 = from_elem<T>(vnew_st[1]);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t p0 = split_pair<T>(qrow[2 * e]), p1 = split_pair<T>(qrow[2 * e + 1]);
-                w[e] = c < 4 ? (p0 & 0xFFFFu) | (p1 << 16) : (p0 >> 16) | (p1 & 0xFFFF0000u);
+        for (int g = 0; g < G; g++) {
+            const float sc = wave_sum64(qy[g][0] * k0 + qy[g][1] * k1);
+            const float m = fmaxf(sc, kFloor2);
+            const float l = exp2f(fmaxf(sc - m, kFloor2));
+            s_xo[lane][g] = l * v0;
+            s_xo[lane + 64][g] = l * v1;
+            if (lane == 0) {
+                s_m[4][g] = m;
+                s_l[4][g] = l;
             }
         }
-        qb[ks] = make_uint4(w[0], w[1], w[2], w[3]);
     }
 
+    // ---- 6. attention over the split's cached sub-tiles ---------------------
     f32x4 acc[8];
 #pragma unroll
     for (int db = 0; db < 8; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -616,35 +619,28 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 
     for (int page = page0; page < page_end; page++) {
         const int base = page * P + SUB * wave;
-        if (base < a.L) {
-            const int rel = newpos - base;  // row of the new token in this sub-tile
-            if (c == rel) {                 // new K row: the rounded value just appended
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) ka[ks] = *(const uint4 *)(s_knew + 32 * ks + 8 * grp);
-            }
-            // ---- scores: lane (grp, c<4) <- head c, positions 4*grp + i ----
+        const int nv = newpos - base;  // valid rows of this sub-tile (>= 16: all)
+        if (nv > 0) {
+            // scores: lane (grp, c<4) <- head c, positions 4*grp + i
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) sacc = M::qk(ka[ks], qb[ks], sacc);
-            float sc[4], mt = -INFINITY;
+            float sc[4], mt = kFloor2;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 sc[i] = sacc[i] + dpp_from_plus4(sacc[i]);
-                if (4 * grp + i <= rel) mt = fmaxf(mt, sc[i]);
+                if (4 * grp + i < nv) mt = fmaxf(mt, sc[i]);
             }
             mt = xrow32_max(xrow16_max(mt));
             const float mnew = fmaxf(m_run, mt);
-            const float alpha = exp2f(m_run - mnew);
             float p[4], ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[i] = 4 * grp + i <= rel ? exp2f(fmaxf(sc[i] - mnew, kFloor2)) : 0.0f;
+                p[i] = 4 * grp + i < nv ? exp2f(fmaxf(sc[i] - mnew, kFloor2)) : 0.0f;
                 ps += p[i];
             }
             ps = xrow32_sum(xrow16_sum(ps));
-            l_run = l_run * alpha + ps;
-            m_run = mnew;
-            // ---- Pcat A-operand: lane (grp, r): r<4 hi(p_r), 4<=r<8 lo(p_{r-4}) ----
+            // Pcat A-operand: lane (grp, r): r<4 hi(p_r), 4<=r<8 lo(p_{r-4})
             uint32_t hp[2], lp[2];
 #pragma unroll
             for (int e = 0; e < 2; e++) {
@@ -653,55 +649,106 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
                 lp[e] = dpp_from_minus4((p0 >> 16) | (p1 & 0xFFFF0000u));
             }
             const uint2 pa = c < 4 ? make_uint2(hp[0], hp[1]) : c < 8 ? make_uint2(lp[0], lp[1]) : make_uint2(0u, 0u);
-            // ---- V: zero positions past the new token, substitute the new row ----
-            float al[4];
+            if (MULTI) {  // rescale the running sums (a single sub-tile starts from zero)
+                const float alpha = exp2f(m_run - mnew);
+                l_run = l_run * alpha + ps;
+                float al[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) al[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), i));  // head i
+                for (int i = 0; i < 4; i++) al[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), i));  // head i
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                uint2 v = vb[db];
-                if (4 * grp + 3 >= rel) {
-                    uint16_t e4[4] = {(uint16_t)(v.x & 0xFFFFu), (uint16_t)(v.x >> 16), (uint16_t)(v.y & 0xFFFFu), (uint16_t)(v.y >> 16)};
+                for (int db = 0; db < 8; db++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int r = 4 * grp + j;
-                        if (r == rel) e4[j] = s_vnew[16 * db + c];
-                        else if (r > rel) e4[j] = 0;
-                    }
-                    v = make_uint2(e4[0] | ((uint32_t)e4[1] << 16), e4[2] | ((uint32_t)e4[3] << 16));
-                }
-                f32x4 o = acc[db];
-#pragma unroll
-                for (int i = 0; i < 4; i++) o[i] *= al[i];
-                acc[db] = M::pv(pa, v, o);
+                    for (int i = 0; i < 4; i++) acc[db][i] *= al[i];
+            } else {
+                l_run = ps;
             }
+            m_run = mnew;
+            // V: zero the positions at or past pos (halfword masks of this
+            // lane's 4 positions); they may hold stale data
+            uint32_t keep[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
+            if (nv < SUB) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (4 * grp + j >= nv) keep[j >> 1] &= ~(0xFFFFu << (16 * (j & 1)));
+            }
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+                acc[db] = M::pv(pa, make_uint2(vb[db].x & keep[0], vb[db].y & keep[1]), acc[db]);
         }
-        if (MULTI && page + 1 < page_end) {
+        if (MULTI) {
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) ka[ks] = kn[ks];
 #pragma unroll
             for (int db = 0; db < 8; db++) vb[db] = vn[db];
-            if (page + 2 < page_end) load_sub(page + 2, kn, vn);
+            load_sub(page_id(min(page + 2, plast)), kn, vn);
         }
     }
 
-    // ---- wave partial: O[head i][16*db + c] = rows i (hi) + rows 4+i (lo) ----
+    // ---- 7. combine the wave partials (and the new token) ------------------
+    // rows 0-3 (grp 0, hi) and 4-7 (grp 1, lo) of every dim go to LDS as
+    // 16-byte vectors [wave][part][dim][head]; (m, l) of head c from lane c.
+    if (grp < 2) {
 #pragma unroll
-    for (int db = 0; db < 8; db++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float o = xrow16_sum(acc[db][i]);
-            if (grp == 0) s_acc[wave][i][16 * db + c] = o;
-        }
+        for (int db = 0; db < 8; db++) *(f32x4 *)&s_o[wave][grp][16 * db + c][0] = acc[db];
+    }
     if (lane < G) {
         s_m[wave][lane] = m_run;
         s_l[wave][lane] = l_run;
     }
     __syncthreads();
-    split_epilogue(a, kvh, split, tid, SplitLds{s_m, s_l, s_acc, s_w, s_L, &s_ticket});
+    {
+        const int d = tid & 127, gp = 2 * (tid >> 7);  // thread -> dim d, heads gp, gp+1
+        const int nw = last ? 5 : 4;
+        float Mx[2], Lx[2] = {0.f, 0.f}, O[2] = {0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            Mx[j] = s_m[0][gp + j];
+#pragma unroll
+            for (int w = 1; w < 5; w++)
+                if (w < nw) Mx[j] = fmaxf(Mx[j], s_m[w][gp + j]);
+        }
+#pragma unroll
+        for (int w = 0; w < 5; w++) {
+            if (w >= nw) break;
+            float2 o;
+            if (w < 4) {
+                const float2 hi = *(const float2 *)&s_o[w][0][d][gp];
+                const float2 lo = *(const float2 *)&s_o[w][1][d][gp];
+                o = make_float2(hi.x + lo.x, hi.y + lo.y);
+            } else {
+                o = *(const float2 *)&s_xo[d][gp];
+            }
+            const float sc0 = exp2f(s_m[w][gp] - Mx[0]), sc1 = exp2f(s_m[w][gp + 1] - Mx[1]);
+            Lx[0] = fmaf(sc0, s_l[w][gp], Lx[0]);
+            Lx[1] = fmaf(sc1, s_l[w][gp + 1], Lx[1]);
+            O[0] = fmaf(sc0, o.x, O[0]);
+            O[1] = fmaf(sc1, o.y, O[1]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int h = kvh * G + gp + j;
+            if (a.nsplit == 1) {
+                a.out[(size_t)h * D + d] = Lx[j] > 0.0f ? O[j] / Lx[j] : 0.0f;
+            } else {
+                a.part_acc[((size_t)h * kMaxSplits + split) * D + d] = O[j];
+                if (d == 0) *(float2 *)(a.part_ml + ((size_t)h * kMaxSplits + split) * 2) = make_float2(Mx[j], Lx[j]);
+            }
+        }
+    }
+    // ---- 8. append the new row to the cache ---------------------------------
+    if (extra) {
+        const int phys = page_id(newpos / P), t = newpos % P;
+        uint16_t *kp = (uint16_t *)kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)t * D;
+        uint16_t *vp = (uint16_t *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            kp[lane + 64 * e] = knew_st[e];
+            vp[v_off(t, lane + 64 * e)] = vnew_st[e];
+        }
+    }
 }
 
-// Merge of the split partials (second launch when merge_inline is off).
+// Merge of the split partials (the second launch of a multi-split call).
 // Block (head h, 32-dim slice); thread (split group sg of 8, dim).  Every
 // thread issues all its (m, l, acc) loads at once, reduces its splits with a
 // local maximum, and the 8 split groups are combined through LDS.
@@ -754,20 +801,40 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     }
 }
 
-hipError_t launch_decode(int kv_dtype, const DecodeArgs &a, hipStream_t s) {
+using DecodeKernel = void (*)(DecodeArgs);
+
+template <typename T> DecodeKernel pick_mfma(bool multi, bool args, bool full) {
+    const int i = multi * 4 + args * 2 + full;
+    static const DecodeKernel k[8] = {
+        decode_attn_mfma_kernel<T, false, false, false>, decode_attn_mfma_kernel<T, false, false, true>,
+        decode_attn_mfma_kernel<T, false, true, false>,  decode_attn_mfma_kernel<T, false, true, true>,
+        decode_attn_mfma_kernel<T, true, false, false>,  decode_attn_mfma_kernel<T, true, false, true>,
+        decode_attn_mfma_kernel<T, true, true, false>,   decode_attn_mfma_kernel<T, true, true, true>};
+    return k[i];
+}
+
+hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
+    DecodeArgs a = args;
+    // Work split.  VALU kernel (f32 cache): pages of all L positions.  MFMA
+    // kernels: pages of the cached positions [0, L-1), the new token riding
+    // with the last split.  One page per split until the split count reaches
+    // kMaxSplits (the merge width).
+    const int pages = kv_dtype == 0 ? (a.L + kPage - 1) / kPage : (a.L - 1 + kPage - 1) / kPage;
+    a.ppw = std::max(1, (pages + kMaxSplits - 1) / kMaxSplits);
+    a.nsplit = std::max(1, (pages + a.ppw - 1) / a.ppw);
     dim3 grid(a.nsplit * a.kv_heads), block(256);
-    const bool multi = a.ppw > 1;
-    switch (kv_dtype * 2 + multi) {
-    case 0: hipLaunchKernelGGL((decode_attn_kernel<F32, false>), grid, block, 0, s, a); break;
-    case 1: hipLaunchKernelGGL((decode_attn_kernel<F32, true>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((decode_attn_mfma_kernel<F16, false>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((decode_attn_mfma_kernel<F16, true>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((decode_attn_mfma_kernel<BF16, false>), grid, block, 0, s, a); break;
-    case 5: hipLaunchKernelGGL((decode_attn_mfma_kernel<BF16, true>), grid, block, 0, s, a); break;
+    const bool multi = a.ppw > 1, in_args = a.pages_in_args != 0;
+    const bool full = a.rope_dim == kHeadDim;
+    DecodeKernel k;
+    switch (kv_dtype) {
+    case 0: k = multi ? decode_attn_kernel<F32, true> : decode_attn_kernel<F32, false>; break;
+    case 1: k = pick_mfma<F16>(multi, in_args, full); break;
+    case 2: k = pick_mfma<BF16>(multi, in_args, full); break;
     default: return hipErrorInvalidValue;
     }
+    hipLaunchKernelGGL(k, grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.nsplit == 1 || a.merge_inline) return e;
+    if (e != hipSuccess || a.nsplit == 1) return e;
     hipLaunchKernelGGL(decode_merge_kernel, dim3(a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }

@@ -104,18 +104,26 @@ struct hymt_ctx {
     int rope_cap = 0;
     DevBuf rope_cos, rope_sin;
 
-    // decode workspace; splits merged in-kernel (1) or by a second launch (0)
-    DevBuf dec_ml, dec_acc, dec_cnt;
-    int decode_merge_inline = 0;
+    // decode workspace: split partials (m, l) and acc
+    DevBuf dec_ml, dec_acc;
     // prefill workspace
     DevBuf part_o, part_ml;
     // staging for host-pointer calls
     DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
     HostBuf h_in, h_out;
 
+    // stream capture (hymt_graph_begin .. hymt_graph_end)
+    bool capturing = false;
+    bool capture_failed = false;
+
     bool has_device() const { return device >= 0; }
     void *klayer(int l) const { return (char *)kpool.p + (size_t)l * layer_elems * dtype_bytes(kv_dtype); }
     void *vlayer(int l) const { return (char *)vpool.p + (size_t)l * layer_elems * dtype_bytes(kv_dtype); }
+};
+
+struct hymt_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
 };
 
 namespace {
@@ -186,11 +194,31 @@ void stage_out(hymt_ctx *c, const void *dsrc, void *hdst, size_t bytes) {
     std::memcpy(hdst, c->h_out.p, bytes);
 }
 
+// The kernels read q/k/v/gamma rows and write outputs as 16-byte vectors.
+bool aligned16(std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (((uintptr_t)p & 15u) != 0) return false;
+    return true;
+}
+
 int check_ctx(hymt_ctx *c, bool need_kv, bool need_dev) {
     if (!c) return fail(HYMT_E_ARG, "null context");
     if (need_kv && !c->kv_ready) return fail(HYMT_E_STATE, "KV cache not created (hymt_kv_create)");
     if (need_dev && !c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     return HYMT_OK;
+}
+
+// Calls that synchronise or copy host memory cannot be recorded.
+int refuse_in_capture(hymt_ctx *c, const char *what) {
+    if (!c->capturing) return HYMT_OK;
+    c->capture_failed = true;
+    return fail(HYMT_E_STATE, std::string(what) + " cannot run while the stream is being recorded");
+}
+
+// A device-pointer call being recorded fails if it would have to allocate.
+int fail_capture(hymt_ctx *c, const std::string &msg) {
+    c->capture_failed = true;
+    return fail(HYMT_E_STATE, msg + " during recording; run the call once before hymt_graph_begin");
 }
 
 }  // namespace
@@ -234,8 +262,6 @@ int hymt_create(int device, hymt_ctx **out) {
         }
         HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
         c->device = device;
-        if (const char *m = std::getenv("HYMT_HIP_DECODE_MERGE"))
-            c->decode_merge_inline = std::strcmp(m, "inline") == 0;
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -248,9 +274,15 @@ int hymt_destroy(hymt_ctx *c) {
     if (!c) return HYMT_OK;
     if (c->has_device()) {
         (void)hipSetDevice(c->device);
+        if (c->capturing) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(c->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            c->capturing = false;
+        }
         (void)hipStreamSynchronize(c->stream);
         for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->dec_ml,
-                          &c->dec_acc, &c->dec_cnt, &c->part_o, &c->part_ml, &c->in_q,
+                          &c->dec_acc, &c->part_o, &c->part_ml, &c->in_q,
                           &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v})
             b->release();
         c->h_in.release();
@@ -284,6 +316,7 @@ int hymt_kv_create(hymt_ctx *c, int layers, int max_tokens, int kv_dtype) {
     if (int r = check_ctx(c, false, false)) return r;
     if (!c->configured) return fail(HYMT_E_STATE, "hymt_set_attn_config first");
     if (c->kv_ready) return fail(HYMT_E_STATE, "KV cache already created");
+    if (int r = refuse_in_capture(c, "hymt_kv_create")) return r;
     if (layers <= 0 || max_tokens <= 0 || kv_dtype < HYMT_F32 || kv_dtype > HYMT_BF16)
         return fail(HYMT_E_ARG, "invalid KV cache arguments");
     c->layers = layers;
@@ -301,8 +334,6 @@ int hymt_kv_create(hymt_ctx *c, int layers, int max_tokens, int kv_dtype) {
             HIP_TRY(hipMemset(c->tab.p, 0xFF, (size_t)P * 4));
             c->dec_ml.reserve((size_t)c->heads * kMaxSplits * 2 * 4);
             c->dec_acc.reserve((size_t)c->heads * kMaxSplits * kHeadDim * 4);
-            c->dec_cnt.reserve((size_t)c->kv_heads * 4);
-            HIP_TRY(hipMemset(c->dec_cnt.p, 0, (size_t)c->kv_heads * 4));
         } catch (const HipError &e) {
             c->kpool.release();
             c->vpool.release();
@@ -362,6 +393,7 @@ int hymt_kv_upload(hymt_ctx *c, int layer, int pos, int len, const uint16_t *k_b
                                          " exceeded at " + std::to_string((long)pos + len));
     if (len == 0) return HYMT_OK;
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    if (int r = refuse_in_capture(c, "hymt_kv_upload")) return r;
     try {
         HIP_TRY(hipSetDevice(c->device));
         c->pages.ensure_written(pos, len);
@@ -388,6 +420,7 @@ int hymt_kv_read(hymt_ctx *c, int layer, int pos, int len, float *k_out, float *
         return fail(HYMT_E_ARG, "invalid read arguments");
     if (!c->pages.resident(pos + len)) return fail(HYMT_E_STATE, "rows not resident");
     if (len == 0) return HYMT_OK;
+    if (int r = refuse_in_capture(c, "hymt_kv_read")) return r;
     try {
         HIP_TRY(hipSetDevice(c->device));
         const size_t n = (size_t)len * c->kv_heads * c->head_dim;
@@ -415,6 +448,11 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
     if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before decode");
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
+    if (dev && !aligned16({q, k, v, qnw, knw, out}))
+        return fail(HYMT_E_ARG, "device tensors must be 16-byte aligned");
+    if (!dev)
+        if (int r = refuse_in_capture(c, "a host-pointer decode")) return r;
+    if (c->capturing && pos + 1 > c->rope_cap) return fail_capture(c, "RoPE table growth");
     try {
         HIP_TRY(hipSetDevice(c->device));
         c->pages.ensure_written(pos, 1);
@@ -440,21 +478,15 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         a.vpool = c->vlayer(layer);
         a.part_ml = (float *)c->dec_ml.p;
         a.part_acc = (float *)c->dec_acc.p;
-        a.counters = (uint32_t *)c->dec_cnt.p;
         a.out = dev ? out : (float *)c->out_o.p;
         a.L = pos + 1;
         a.kv_heads = c->kv_heads;
         a.rope_half = half;
         a.rope_dim = c->rope_dim;
         const int npages = (a.L + kPage - 1) / kPage;
-        // two pages per split once there are enough pages: half the partials
-        // to merge at the same streaming time (both pages' loads issue at once)
-        a.ppw = std::max(npages >= 32 ? 2 : 1, (npages + kMaxSplits - 1) / kMaxSplits);
-        if (const char *s = std::getenv("HYMT_HIP_DECODE_PPW")) a.ppw = std::max(a.ppw, atoi(s));
-        a.nsplit = (npages + a.ppw - 1) / a.ppw;
+        a.ppw = a.nsplit = 0;  // the work split is chosen by launch_decode
         a.eps = c->eps;
         a.qscale = 1.4426950408889634f / sqrtf((float)D);
-        a.merge_inline = c->decode_merge_inline;
         a.pages_in_args = npages <= kArgPages;
         if (a.pages_in_args)
             for (int b = 0; b < npages; b++) a.pages[b] = c->pages.phys(b);
@@ -485,6 +517,9 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
     if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before prefill");
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
+    if (!dev)
+        if (int r = refuse_in_capture(c, "a host-pointer prefill")) return r;
+    if (c->capturing && pos + seq > c->rope_cap) return fail_capture(c, "RoPE table growth");
     try {
         HIP_TRY(hipSetDevice(c->device));
         c->pages.ensure_written(pos, seq);
@@ -557,6 +592,8 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         f.items_per_kvh = items;
         if (split) {
             const size_t slots = (size_t)c->kv_heads * items;
+            if (c->capturing && slots * kGroup * 32 * D * 4 > c->part_o.bytes)
+                return fail_capture(c, "prefill workspace growth");
             c->part_o.reserve(slots * kGroup * 32 * D * 4);
             c->part_ml.reserve(slots * kGroup * 32 * 2 * 4);
         }
@@ -575,6 +612,7 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
 
 int hymt_sync(hymt_ctx *c) {
     if (int r = check_ctx(c, false, true)) return r;
+    if (int r = refuse_in_capture(c, "hymt_sync")) return r;
     hipError_t e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
     return HYMT_OK;
@@ -590,6 +628,7 @@ int hymt_get_stream(hymt_ctx *c, void **stream) {
 int hymt_dev_alloc(hymt_ctx *c, size_t bytes, void **dptr) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!dptr || bytes == 0) return fail(HYMT_E_ARG, "invalid allocation request");
+    if (int r = refuse_in_capture(c, "hymt_dev_alloc")) return r;
     (void)hipSetDevice(c->device);
     hipError_t e = hipMalloc(dptr, bytes);
     if (e != hipSuccess) return fail(HYMT_E_OOM, std::string("hipMalloc: ") + hipGetErrorString(e));
@@ -599,6 +638,7 @@ int hymt_dev_alloc(hymt_ctx *c, size_t bytes, void **dptr) {
 int hymt_dev_free(hymt_ctx *c, void *dptr) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!dptr) return HYMT_OK;
+    if (int r = refuse_in_capture(c, "hymt_dev_free")) return r;
     (void)hipStreamSynchronize(c->stream);
     hipError_t e = hipFree(dptr);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipFree: ") + hipGetErrorString(e));
@@ -609,12 +649,77 @@ int hymt_memcpy(hymt_ctx *c, void *dst, const void *src, size_t bytes, int kind)
     if (int r = check_ctx(c, false, true)) return r;
     if (!dst || !src || kind < 0 || kind > 2) return fail(HYMT_E_ARG, "invalid copy arguments");
     if (bytes == 0) return HYMT_OK;
+    if (int r = refuse_in_capture(c, "hymt_memcpy")) return r;
     const hipMemcpyKind k = kind == 0 ? hipMemcpyHostToDevice
                             : kind == 1 ? hipMemcpyDeviceToHost
                                         : hipMemcpyDeviceToDevice;
     hipError_t e = hipMemcpyAsync(dst, src, bytes, k, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipMemcpy: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_graph_begin(hymt_ctx *c) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (c->capturing) return fail(HYMT_E_STATE, "a recording is already open");
+    (void)hipSetDevice(c->device);
+    // this thread's stream-unsafe HIP calls fail instead of joining the graph
+    hipError_t e = hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipStreamBeginCapture: ") + hipGetErrorString(e));
+    c->capturing = true;
+    c->capture_failed = false;
+    return HYMT_OK;
+}
+
+int hymt_graph_end(hymt_ctx *c, hymt_graph **out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!out) return fail(HYMT_E_ARG, "null graph out");
+    *out = nullptr;
+    if (!c->capturing) return fail(HYMT_E_STATE, "no recording is open");
+    (void)hipSetDevice(c->device);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    c->capturing = false;
+    if (c->capture_failed || e != hipSuccess || !g) {
+        if (g) (void)hipGraphDestroy(g);
+        if (e != hipSuccess)
+            return fail(HYMT_E_DEVICE, std::string("hipStreamEndCapture: ") + hipGetErrorString(e));
+        return fail(HYMT_E_STATE, "a call failed during recording; the recording is discarded");
+    }
+    hymt_graph *hg = new (std::nothrow) hymt_graph();
+    if (!hg) {
+        (void)hipGraphDestroy(g);
+        return fail(HYMT_E_OOM, "host allocation failed");
+    }
+    hg->graph = g;
+    e = hipGraphInstantiate(&hg->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete hg;
+        return fail(HYMT_E_DEVICE, std::string("hipGraphInstantiate: ") + hipGetErrorString(e));
+    }
+    *out = hg;
+    return HYMT_OK;
+}
+
+int hymt_graph_launch(hymt_ctx *c, hymt_graph *g) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!g || !g->exec) return fail(HYMT_E_ARG, "null graph");
+    if (c->capturing) return fail(HYMT_E_STATE, "cannot replay while recording");
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipGraphLaunch(g->exec, c->stream);
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipGraphLaunch: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_graph_destroy(hymt_ctx *c, hymt_graph *g) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!g) return HYMT_OK;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);  // a replay may still be running
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
     return HYMT_OK;
 }
 

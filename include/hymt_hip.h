@@ -155,6 +155,27 @@ int hymt_attn_prefill(hymt_ctx *ctx, int layer, int pos, int seq, const void *q,
 /* Wait for all work on the context's stream. */
 int hymt_sync(hymt_ctx *ctx);
 
+/*
+ * Recorded call sequences (HIP graphs).  Between hymt_graph_begin and
+ * hymt_graph_end the context's stream is captured: device-pointer
+ * (HYMT_FLAG_DEVICE_PTRS) attention calls are recorded instead of run, and
+ * hymt_graph_launch replays the whole sequence with one submission.  This is
+ * the HIP form of the reference's recorded decode command buffer: the Vulkan
+ * backend records the decode graph once (VulkanBackend.cs:326, RecordDecodeGraph
+ * :400-568) and submits it per token (:677).  Replays repeat the recorded
+ * arguments (positions included).  During capture, calls that synchronise,
+ * copy host memory or would grow a device workspace return HYMT_E_STATE, so a
+ * sequence is warmed up once eagerly before it is recorded.  Such a refusal
+ * spoils the recording: it stays open, and hymt_graph_end discards it and
+ * reports the failure.  A call rejected for its arguments records nothing
+ * and leaves the recording intact.
+ */
+typedef struct hymt_graph hymt_graph;
+int hymt_graph_begin(hymt_ctx *ctx);
+int hymt_graph_end(hymt_ctx *ctx, hymt_graph **graph);
+int hymt_graph_launch(hymt_ctx *ctx, hymt_graph *graph);
+int hymt_graph_destroy(hymt_ctx *ctx, hymt_graph *graph);
+
 /* The context's hipStream_t, for callers that time or order work around it. */
 int hymt_get_stream(hymt_ctx *ctx, void **stream);
 

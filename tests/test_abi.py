@@ -153,6 +153,18 @@ def test_decode_requires_resident_prefix_and_device():
         L.hymt_destroy(h)
 
 
+def test_graph_calls_need_a_device():
+    L, h = host_ctx(64)
+    try:
+        g = ctypes.c_void_p()
+        assert L.hymt_graph_begin(h) == N.HYMT_E_NO_DEVICE
+        assert L.hymt_graph_end(h, ctypes.byref(g)) == N.HYMT_E_NO_DEVICE
+        assert L.hymt_graph_launch(h, None) == N.HYMT_E_NO_DEVICE
+        assert L.hymt_graph_begin(None) == N.HYMT_E_ARG
+    finally:
+        L.hymt_destroy(h)
+
+
 def test_f32_cache_has_no_prefill():
     L, h = host_ctx(128, N.F32)
     try:

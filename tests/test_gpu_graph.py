@@ -1,0 +1,144 @@
+"""Recorded call sequences (hymt_graph_*) on the GPU: a recorded decode step
+and a recorded prefill replay to the same bits as the eager calls, replays
+interleaved with eager work stay correct, and calls that cannot be recorded
+are refused with the recording discarded.
+
+The recorded form is what a HipBackend.ForwardStep would submit per token,
+as the Vulkan backend records its decode command buffer once and replays it
+(VulkanBackend.cs:326, :400-568, :677)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from hymt2sharp_amd import BF16, F16, HipBackend
+from hymt2sharp_amd import _native as N
+from hymt2sharp_amd import synth as S
+from tests.attn_cases import BASE, D, EPS, HKV, HQ, cache_rows, new_token
+
+pytestmark = pytest.mark.gpu
+
+
+def backend(layers, cap, dtype):
+    return HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, cap, dtype)
+
+
+def dev_inputs(be, arrays):
+    ptrs = []
+    for a in arrays:
+        p = be.alloc(max(a.nbytes, 16))
+        be.upload(p, a)
+        ptrs.append(p)
+    return ptrs
+
+
+def test_recorded_decode_step_replays_exactly(hip_available):
+    layers, pos = 3, 700
+    be = backend(layers, pos + 1, F16)
+    try:
+        kb, vb = cache_rows(11, pos)
+        for l in range(layers):
+            be.UploadKv(l, 0, pos, kb, vb)
+        q, k, v, qnw, knw = new_token(11, 0, "gamma", seq=layers)
+        dq, dk, dv, dqn, dkn = dev_inputs(be, [q, k, v, qnw, knw])
+        dout = be.alloc(q.nbytes)
+        qs, ks = HQ * D * 4, HKV * D * 4
+
+        def step():
+            for l in range(layers):
+                be.decode_dev(l, pos, dq + l * qs, dk + l * ks, dv + l * ks, dqn, dkn, dout + l * qs)
+
+        step()  # eager warm-up
+        eager = be.download(np.empty((layers, HQ * D), np.float32), dout)
+        be.graph_begin()
+        step()
+        g = be.graph_end()
+        try:
+            for rep in range(3):
+                be.upload(dout, np.zeros_like(q))  # eager work between replays
+                be.graph_launch(g)
+                be.sync()
+                got = be.download(np.empty((layers, HQ * D), np.float32), dout)
+                assert np.array_equal(got, eager), rep
+        finally:
+            be.graph_destroy(g)
+        for p in (dq, dk, dv, dqn, dkn, dout):
+            be.free(p)
+    finally:
+        be.Dispose()
+
+
+def test_recorded_prefill_replays_exactly(hip_available):
+    pos, seq = 130, 96
+    be = backend(1, pos + seq, BF16)
+    try:
+        kb, vb = cache_rows(12, pos)
+        be.UploadKv(0, 0, pos, kb, vb)
+        q, k, v, qnw, knw = new_token(12, 0, "gamma", seq=seq)
+        qb, kb16, vb16 = (S.f32_to_bf16_bits(x) for x in (q, k, v))
+        dq, dk, dv, dqn, dkn = dev_inputs(be, [qb, kb16, vb16, qnw, knw])
+        dout = be.alloc(q.nbytes)
+        be.prefill_dev(0, pos, seq, dq, dk, dv, BF16, dqn, dkn, dout)
+        eager = be.download(np.empty((seq, HQ * D), np.float32), dout)
+        be.graph_begin()
+        be.prefill_dev(0, pos, seq, dq, dk, dv, BF16, dqn, dkn, dout)
+        g = be.graph_end()
+        try:
+            for rep in range(3):
+                be.upload(dout, np.zeros_like(q))
+                be.graph_launch(g)
+                be.sync()
+                got = be.download(np.empty((seq, HQ * D), np.float32), dout)
+                assert np.array_equal(got, eager), rep
+        finally:
+            be.graph_destroy(g)
+        for p in (dq, dk, dv, dqn, dkn, dout):
+            be.free(p)
+    finally:
+        be.Dispose()
+
+
+def test_unrecordable_calls_are_refused(hip_available):
+    pos = 64
+    be = backend(1, 5000, F16)
+    L = N.lib()
+    try:
+        kb, vb = cache_rows(13, pos)
+        be.UploadKv(0, 0, pos, kb, vb)
+        q, k, v, qnw, knw = new_token(13, 0, "gamma")
+        be.graph_begin()
+        # host pointers synchronise: refused, and the recording is spoiled
+        with pytest.raises(N.InvalidOperationError):
+            be.DecodeAttention(0, pos, q[0], k[0], v[0], qnw, knw)
+        assert L.hymt_sync(be.handle) == N.HYMT_E_STATE
+        assert L.hymt_graph_begin(be.handle) == N.HYMT_E_STATE  # already open
+        with pytest.raises(N.InvalidOperationError):
+            be.graph_end()
+        # a device-pointer call whose RoPE table would grow is refused too
+        dq, dk, dv = dev_inputs(be, [q, k, v])
+        dout = be.alloc(q.nbytes)
+        be.MapRange(0, 5000)
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)  # table of 4096 rows
+        be.sync()
+        be.graph_begin()
+        with pytest.raises(N.InvalidOperationError) as e:
+            be.decode_dev(0, 4999, dq, dk, dv, None, None, dout)
+        assert "RoPE table growth" in str(e.value)
+        with pytest.raises(N.InvalidOperationError):
+            be.graph_end()
+        # an argument error records nothing and leaves the recording usable
+        be.graph_begin()
+        with pytest.raises(N.ArgumentError):
+            be.decode_dev(7, pos, dq, dk, dv, None, None, dout)
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
+        g = be.graph_end()
+        be.graph_launch(g)
+        be.sync()
+        be.graph_destroy(g)
+        # misaligned device tensors are rejected before any work
+        with pytest.raises(N.ArgumentError):
+            be.decode_dev(0, pos, dq + 4, dk, dv, None, None, dout)
+        for p in (dq, dk, dv, dout):
+            be.free(p)
+    finally:
+        be.Dispose()
