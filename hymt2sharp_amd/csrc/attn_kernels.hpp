@@ -29,28 +29,31 @@ __host__ __device__ inline size_t v_off(int t, int d) {
 }
 
 struct DecodeArgs {
+    // Ordered by first use in the kernels: the scalars that place a
+    // workgroup, then the pointers its first loads need.
+    int L;              // positions attended = pos + 1
+    int kv_heads;
+    int kv_shift;       // log2(kv_heads)
+    int ppw;            // pages per split (set by launch_decode)
+    int nsplit;         // splits per kv head (set by launch_decode)
+    int rope_half;
+    int rope_dim;
+    int pages_in_args;  // 1: pages[] below holds tab[0, npages) (npages <= kArgPages)
     const float *q;     // [Hq*D]
-    const float *knew;  // [Hkv*D]
-    const float *vnew;  // [Hkv*D]
     const float *qnw;   // [D] or null
-    const float *knw;   // [D] or null
     const float *rope_cos;  // row `pos` of the cos table, [rope_half]
     const float *rope_sin;
+    const float *knew;  // [Hkv*D]
+    const float *knw;   // [D] or null
+    const float *vnew;  // [Hkv*D]
     const int32_t *tab; // logical block -> physical page
     void *kpool;        // this layer's K pool
     void *vpool;        // this layer's V pool
-    float *part_ml;     // [Hq][kMaxSplits][2]
-    float *part_acc;    // [Hq][kMaxSplits][D]
-    float *out;         // [Hq*D]
-    int L;              // positions attended = pos + 1
-    int kv_heads;
-    int rope_half;
-    int rope_dim;
-    int nsplit;
-    int ppw;            // pages per split
     float eps;
     float qscale;       // log2(e) / sqrt(D)
-    int pages_in_args;  // 1: pages[] below holds tab[0, npages) (npages <= kArgPages)
+    float *out;         // [Hq*D]
+    float *part_ml;     // [Hq][kMaxSplits][2]
+    float *part_acc;    // [Hq][kMaxSplits][D]
     int32_t pages[kArgPages];  // physical page of each logical block, saving a
                                // dependent table load before the K/V stream
 };

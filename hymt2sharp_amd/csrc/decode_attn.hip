@@ -499,16 +499,18 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, c = lane & 15;  // MFMA lane group / row-col index
     const int Hkv = a.kv_heads;
-    const int kvh = blockIdx.x % Hkv;
-    const int split = blockIdx.x / Hkv;
+    const int split = blockIdx.x, kvh = blockIdx.y;  // grid (nsplit, kv heads)
     const int newpos = a.L - 1;                // cached positions [0, newpos)
     const int ncp = (newpos + P - 1) / P;      // cached pages
-    const int page0 = split * a.ppw;
+    // one page per split unless MULTI: the first page id's address then
+    // depends on blockIdx alone and is loaded with the kernel arguments
+    const int page0 = MULTI ? split * a.ppw : split;
     const int page_end = min(page0 + (MULTI ? a.ppw : 1), ncp);
     const bool last = split == a.nsplit - 1;
     const bool extra = last && wave == 3;      // the wave that adds the new token
 
-    __shared__ __attribute__((aligned(16))) uint16_t s_qop[4][2][G][D];  // per wave: hi/lo q
+    __shared__ __attribute__((aligned(16))) uint16_t s_qop[2][G][D];  // hi/lo q of the 4 heads
+    __shared__ float s_qf[G][D];                                      // fp32 q, for the new token
     __shared__ __attribute__((aligned(16))) float s_o[4][2][D][G];       // per wave: hi/lo rows
     __shared__ __attribute__((aligned(16))) float s_xo[D][G];            // the new token
     __shared__ float s_m[5][G], s_l[5][G];                                // [4]: the new token
@@ -531,12 +533,12 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 
     // ---- 2. q rows and the new k, v rows ------------------------------------
     // vmcnt retires in order: these small rows are issued ahead of the K/V
-    // stream so the q operand is built while it is in flight.  Every wave
-    // loads the new rows (1.5 KiB, cached) so that all loads sit in one
-    // straight-line block.
-    RowsIn<G, FULL> qin;
+    // stream so the q operand is built while it is in flight.  Wave w loads
+    // q head w of the group; every wave loads the new rows (1.5 KiB, cached)
+    // so that all loads sit in one straight-line block.
+    RowsIn<1, FULL> qin;
     RowsIn<1, FULL> kin;
-    qin.load(a.q + (size_t)kvh * G * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
+    qin.load(a.q + (size_t)(kvh * G + wave) * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
     kin.load(a.knew + (size_t)kvh * D, a.rope_cos, a.rope_sin, a.knw, lane, half, rdim);
     const float vnew0 = a.vnew[(size_t)kvh * D + lane];
     const float vnew1 = a.vnew[(size_t)kvh * D + lane + 64];
@@ -559,28 +561,26 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     load_sub(phys0, ka, vb);
     if (MULTI) load_sub(phys1, kn, vn);  // two pages in flight
 
-    // ---- 4. q operand: RoPE + norm, hi/lo split, through this wave's LDS ----
-    uint16_t(&sq)[2][G][D] = s_qop[wave];
-    float qy[G][2];  // fp32 q (scaled), kept for the new token
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        qin.finish(g, qy[g], lane, half, rdim, a.qnw != nullptr, a.eps, a.qscale);
+    // ---- 4. q operand: wave w applies RoPE + norm to head w and stores its
+    // hi/lo split (and the fp32 row) in LDS; one barrier shares the 4 heads --
+    {
+        float y[2];
+        qin.finish(0, y, lane, half, rdim, a.qnw != nullptr, a.eps, a.qscale);
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            const uint32_t pr = split_pair<T>(qy[g][e]);
-            sq[0][g][lane + 64 * e] = (uint16_t)pr;
-            sq[1][g][lane + 64 * e] = (uint16_t)(pr >> 16);
+            const uint32_t pr = split_pair<T>(y[e]);
+            s_qop[0][wave][lane + 64 * e] = (uint16_t)pr;
+            s_qop[1][wave][lane + 64 * e] = (uint16_t)(pr >> 16);
+            s_qf[wave][lane + 64 * e] = y[e];
         }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __syncthreads();
     // Qcat B-operand: lane (grp, c), dims 32*ks + 8*grp + [0, 8):
     // c < 4 -> hi(q_c), 4 <= c < 8 -> lo(q_{c-4}), else 0
     uint4 qb[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
-        qb[ks] = c < 8 ? *(const uint4 *)&sq[c >> 2][c & 3][32 * ks + 8 * grp] : make_uint4(0, 0, 0, 0);
+        qb[ks] = c < 8 ? *(const uint4 *)&s_qop[c >> 2][c & 3][32 * ks + 8 * grp] : make_uint4(0, 0, 0, 0);
 
     // ---- 5. the new token: K after RoPE + norm and V, rounded to the cache
     // type (Ops.ConvertToBf16, Ops.cs:658-680), then its weight for each head
@@ -599,7 +599,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
         const float v0 = from_elem<T>(vnew_st[0]), v1 = from_elem<T>(vnew_st[1]);
 #pragma unroll
         for (int g = 0; g < G; g++) {
-            const float sc = wave_sum64(qy[g][0] * k0 + qy[g][1] * k1);
+            const float sc = wave_sum64(s_qf[g][lane] * k0 + s_qf[g][lane + 64] * k1);
             const float m = fmaxf(sc, kFloor2);
             const float l = exp2f(fmaxf(sc - m, kFloor2));
             s_xo[lane][g] = l * v0;
@@ -748,56 +748,68 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     }
 }
 
-// Merge of the split partials (the second launch of a multi-split call).
-// Block (head h, 32-dim slice); thread (split group sg of 8, dim).  Every
-// thread issues all its (m, l, acc) loads at once, reduces its splits with a
-// local maximum, and the 8 split groups are combined through LDS.
+// Merge of the split partials (the second launch of a multi-split call):
+// out[h] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
+// Workgroup = q head; thread = (split group sg of 8, 4 dims).  Every thread
+// issues all its loads (float2 (m, l) and float4 acc per split) at once; the
+// 8 split groups are combined through LDS.
 __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
     constexpr int D = kHeadDim, NG = 8, PER = kMaxSplits / NG;
-    const int h = blockIdx.x >> 2, d = (blockIdx.x & 3) * 32 + (threadIdx.x & 31);
-    const int sg = threadIdx.x >> 5;
-    __shared__ float s_m[NG][32], s_l[NG][32], s_o[NG][32];
-    const float *ml = a.part_ml + (size_t)h * kMaxSplits * 2;
-    const float *pa = a.part_acc + (size_t)h * kMaxSplits * D + d;
-    float m[PER], l[PER], x[PER];
+    const int h = blockIdx.x, d4 = threadIdx.x & 31, sg = threadIdx.x >> 5;
+    __shared__ float s_m[NG], s_l[NG];
+    __shared__ float4 s_o[NG][32];
+    const float2 *ml = (const float2 *)(a.part_ml + (size_t)h * kMaxSplits * 2);
+    const float4 *pa = (const float4 *)(a.part_acc + (size_t)h * kMaxSplits * D) + d4;
+    float2 mlv[PER];
+    float4 x[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int s = sg + NG * k;
         const bool ok = s < a.nsplit;
-        m[k] = ok ? ml[2 * s] : -INFINITY;
-        l[k] = ok ? ml[2 * s + 1] : 0.0f;
-        x[k] = ok ? pa[(size_t)s * D] : 0.0f;
+        mlv[k] = ok ? ml[s] : make_float2(-INFINITY, 0.0f);
+        x[k] = ok ? pa[(size_t)s * (D / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < PER; k++) M = fmaxf(M, m[k]);
-    float L = 0.0f, O = 0.0f;
+    for (int k = 0; k < PER; k++) M = fmaxf(M, mlv[k].x);
+    float L = 0.0f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
     if (M != -INFINITY) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
-            const float w = exp2f(m[k] - M);
-            L = fmaf(w, l[k], L);
-            O = fmaf(w, x[k], O);
+            const float w = exp2f(mlv[k].x - M);
+            L = fmaf(w, mlv[k].y, L);
+            O.x = fmaf(w, x[k].x, O.x);
+            O.y = fmaf(w, x[k].y, O.y);
+            O.z = fmaf(w, x[k].z, O.z);
+            O.w = fmaf(w, x[k].w, O.w);
         }
     }
-    s_m[sg][threadIdx.x & 31] = M;
-    s_l[sg][threadIdx.x & 31] = L;
-    s_o[sg][threadIdx.x & 31] = O;
+    if (d4 == 0) {
+        s_m[sg] = M;
+        s_l[sg] = L;
+    }
+    s_o[sg][d4] = O;
     __syncthreads();
     if (sg == 0) {
-        const int i = threadIdx.x & 31;
-        float Mt = s_m[0][i];
+        float Mt = s_m[0];
 #pragma unroll
-        for (int g = 1; g < NG; g++) Mt = fmaxf(Mt, s_m[g][i]);
-        float Lt = 0.0f, Ot = 0.0f;
+        for (int g = 1; g < NG; g++) Mt = fmaxf(Mt, s_m[g]);
+        float Lt = 0.0f;
+        float4 Ot = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (int g = 0; g < NG; g++) {
-            if (s_m[g][i] == -INFINITY) continue;
-            const float w = exp2f(s_m[g][i] - Mt);
-            Lt = fmaf(w, s_l[g][i], Lt);
-            Ot = fmaf(w, s_o[g][i], Ot);
+            if (s_m[g] == -INFINITY) continue;
+            const float w = exp2f(s_m[g] - Mt);
+            const float4 o = s_o[g][d4];
+            Lt = fmaf(w, s_l[g], Lt);
+            Ot.x = fmaf(w, o.x, Ot.x);
+            Ot.y = fmaf(w, o.y, Ot.y);
+            Ot.z = fmaf(w, o.z, Ot.z);
+            Ot.w = fmaf(w, o.w, Ot.w);
         }
-        a.out[(size_t)h * D + d] = Lt > 0.0f ? Ot / Lt : 0.0f;
+        const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+        ((float4 *)(a.out + (size_t)h * D))[d4] = make_float4(Ot.x * inv, Ot.y * inv, Ot.z * inv, Ot.w * inv);
     }
 }
 
@@ -832,10 +844,13 @@ hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     case 2: k = pick_mfma<BF16>(multi, in_args, full); break;
     default: return hipErrorInvalidValue;
     }
+    // the VALU kernel indexes (split, kv head) linearly, the MFMA kernels by
+    // a 2D grid
+    if (kv_dtype != 0) grid = dim3(a.nsplit, a.kv_heads);
     hipLaunchKernelGGL(k, grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(decode_merge_kernel, dim3(a.kv_heads * kGroup), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -481,6 +481,7 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         a.out = dev ? out : (float *)c->out_o.p;
         a.L = pos + 1;
         a.kv_heads = c->kv_heads;
+        a.kv_shift = __builtin_ctz((unsigned)c->kv_heads);
         a.rope_half = half;
         a.rope_dim = c->rope_dim;
         const int npages = (a.L + kPage - 1) / kPage;
