@@ -87,17 +87,26 @@ struct FlashArgs {
     int rope_half, rope_dim;  // rope_dim in {0, 64, 128}
     int io_bf16;
     float eps, qscale;  // qscale = log2(e) / sqrt(D)
-    int nqb;            // q blocks of 32 rows
+    int nb16;           // q blocks of 16 rows
+    int npairs;         // block pairs (b, nb16-1-b), b < npairs
     int cap;            // max kv tiles per work item
     int items_per_kvh;  // work items per kv head
 };
 
-// Number of kv tiles (pages) q block qb attends to.
-__host__ __device__ inline int flash_tiles(int pos0, int qb, int seq) {
-    int last = pos0 + qb * 32 + 31;
+// Number of kv tiles (pages) the 16-row q block b attends to.
+__host__ __device__ inline int block_tiles(int pos0, int b, int seq) {
+    int last = pos0 + b * 16 + 15;
     int lim = pos0 + seq - 1;
     if (last > lim) last = lim;
     return last / 64 + 1;
+}
+
+// Causal prefill pairs the short block b with the long block nb16-1-b, so
+// every pair carries about the same work.  The long block sets the pair's
+// kv range; the short one (absent for the middle block of an odd count)
+// joins for the tiles it attends to.
+__host__ __device__ inline int pair_tiles(int pos0, int pair, int nb16, int seq) {
+    return block_tiles(pos0, nb16 - 1 - pair, seq);
 }
 
 // kv dtype codes as in hymt_dtype.

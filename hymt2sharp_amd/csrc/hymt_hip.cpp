@@ -569,13 +569,14 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         f.io_bf16 = io_dtype == HYMT_BF16;
         f.eps = c->eps;
         f.qscale = 1.4426950408889634f / sqrtf((float)D);
-        f.nqb = (seq + 31) / 32;
-        // Work items: split the kv range of q blocks only when there are too
-        // few (kv head, q block) pairs to fill the GPU.
+        f.nb16 = (seq + 15) / 16;
+        f.npairs = (f.nb16 + 1) / 2;
+        // Work items: split the kv range of block pairs only when there are
+        // too few (kv head, pair) combinations to fill the GPU.
         int max_tiles = 0;
-        for (int qb = 0; qb < f.nqb; qb++) max_tiles = std::max(max_tiles, flash_tiles(pos, qb, seq));
+        for (int pr = 0; pr < f.npairs; pr++) max_tiles = std::max(max_tiles, pair_tiles(pos, pr, f.nb16, seq));
         int cap = max_tiles;
-        const int pairs = f.nqb * c->kv_heads;
+        const int pairs = f.npairs * c->kv_heads;
         if (pairs < 256) {
             const int per = (256 + pairs - 1) / pairs;
             cap = std::max(4, (max_tiles + per - 1) / per);
@@ -585,8 +586,8 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         f.cap = cap;
         int items = 0;
         bool split = false;
-        for (int qb = 0; qb < f.nqb; qb++) {
-            const int ns = (flash_tiles(pos, qb, seq) + cap - 1) / cap;
+        for (int pr = 0; pr < f.npairs; pr++) {
+            const int ns = (pair_tiles(pos, pr, f.nb16, seq) + cap - 1) / cap;
             items += ns;
             split |= ns > 1;
         }

@@ -26,6 +26,8 @@
 //                 the exact exponent.
 //  prefill_merge  combines the (m, l, O) partials of q blocks whose kv range
 //                 was split over several workgroups (long cached prefixes).
+#include <type_traits>
+
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
 
@@ -189,23 +191,24 @@ hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
 }
 
 // ------------------------------------------------------------------ work items
-// Items are enumerated heaviest q block first; a q block with more than
-// `cap` kv tiles is split into ceil(tiles/cap) consecutive items.
+// A work item is (block pair, kv tile range).  Pairs are enumerated longest
+// first; a pair whose range exceeds `cap` tiles is split into
+// ceil(tiles/cap) consecutive items.
 __host__ __device__ inline int flash_splits(int tiles, int cap) { return (tiles + cap - 1) / cap; }
 
 struct FlashItem {
-    int qb, split, nsplit, t0, t1, first;  // `first`: item index of split 0
+    int pair, split, nsplit, t0, t1, first;  // `first`: item index of split 0
 };
 
 __device__ inline FlashItem flash_item(const FlashArgs &a, int item) {
     FlashItem it;
     int first = 0;
-    for (int qb = a.nqb - 1; qb >= 0; qb--) {
-        const int nt = flash_tiles(a.pos0, qb, a.seq);
+    for (int pr = 0; pr < a.npairs; pr++) {
+        const int nt = pair_tiles(a.pos0, pr, a.nb16, a.seq);
         const int ns = flash_splits(nt, a.cap);
         if (item < first + ns) {
             const int s = item - first;
-            it.qb = qb;
+            it.pair = pr;
             it.split = s;
             it.nsplit = ns;
             it.t0 = s * nt / ns;
@@ -215,7 +218,7 @@ __device__ inline FlashItem flash_item(const FlashArgs &a, int item) {
         }
         first += ns;
     }
-    it.qb = -1;
+    it.pair = -1;
     return it;
 }
 
@@ -273,60 +276,48 @@ template <> __device__ __forceinline__ float sum2<F16>(uint32_t pair, float acc)
 
 constexpr int kRopeLd = 68;  // LDS row stride (floats) of the staged RoPE rows
 
-// q rows q0 + 16*qq + c of head h after RoPE and RMSNorm, times qscale, as the
+// q rows rowq[qq] + c of head h after RoPE and RMSNorm, times qscale, as the
 // S^T B operand: lane (grp, c) holds dims 32*ks + 8*grp + [0, 8).  The RoPE
 // partner of dim d (d +- rope_dim/2, rope_dim in {0, 64, 128}) is dim chunk
 // ks ^ (rope_dim/64) of the same lane, so no data crosses lanes except the
-// norm's sum of squares.  Every global load is issued before any math; rows
-// past the chunk use q = 0 (their results are discarded).
-template <typename T, bool IN_BF16>
-__device__ __forceinline__ void q_operand(const FlashArgs &a, int h, int q0, int grp, int c,
-                                          const float *rope_lds, typename Mfma<T>::vec (&qf)[2][4]) {
+// norm's sum of squares.  q_load issues the row loads (before the prologue's
+// barrier, so they overlap the staging of the first tile); q_finish reads the
+// RoPE rows from LDS and builds the operand.  Rows past the chunk or of an
+// absent block use q = 0 (their results are discarded).
+template <bool IN_BF16> struct QRaw {
+    uint4 u[2][4][IN_BF16 ? 1 : 2];
+};
+
+template <bool IN_BF16>
+__device__ __forceinline__ void q_load(const FlashArgs &a, int h, const int (&rowq)[2], const bool (&okq)[2],
+                                       int grp, int c, QRaw<IN_BF16> &raw, bool (&ok)[2]) {
     constexpr int D = kHeadDim;
-    typedef typename Mfma<T>::vec vec;
-    const int rh = a.rope_half, hk = rh >> 5;
-    float x[2][4][8], cA[2][8], cB[2][8], sA[2][8], sB[2][8], gw[4][8];
-    bool ok[2];
 #pragma unroll
     for (int qq = 0; qq < 2; qq++) {
-        const int row0 = q0 + qq * 16 + c;
-        ok[qq] = row0 < a.seq;
-        const int row = ok[qq] ? row0 : a.seq - 1;
+        const int row0 = rowq[qq] + c;
+        ok[qq] = okq[qq] && row0 < a.seq;
+        const int row = min(row0, a.seq - 1);
         const size_t base = (size_t)row * a.heads * D + (size_t)h * D + 8 * grp;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             if (IN_BF16) {
-                const uint4 u = *(const uint4 *)((const uint16_t *)a.q + base + 32 * ks);
-                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    x[qq][ks][2 * e] = __uint_as_float(w[e] << 16);
-                    x[qq][ks][2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
-                }
+                raw.u[qq][ks][0] = *(const uint4 *)((const uint16_t *)a.q + base + 32 * ks);
             } else {
-                const float4 u0 = *(const float4 *)((const float *)a.q + base + 32 * ks);
-                const float4 u1 = *(const float4 *)((const float *)a.q + base + 32 * ks + 4);
-                x[qq][ks][0] = u0.x; x[qq][ks][1] = u0.y; x[qq][ks][2] = u0.z; x[qq][ks][3] = u0.w;
-                x[qq][ks][4] = u1.x; x[qq][ks][5] = u1.y; x[qq][ks][6] = u1.z; x[qq][ks][7] = u1.w;
-            }
-        }
-        if (rh) {
-            // LDS rope rows [cos|sin][32 rows][kRopeLd]
-            const float *rc = rope_lds + (qq * 16 + c) * kRopeLd, *rs = rc + 32 * kRopeLd;
-            const int fa = (8 * grp) & (rh - 1), fb = (32 + 8 * grp) & (rh - 1);
-#pragma unroll
-            for (int e4 = 0; e4 < 2; e4++) {
-                const float4 ca = *(const float4 *)(rc + fa + 4 * e4);
-                const float4 cb = *(const float4 *)(rc + fb + 4 * e4);
-                const float4 sa = *(const float4 *)(rs + fa + 4 * e4);
-                const float4 sb = *(const float4 *)(rs + fb + 4 * e4);
-                cA[qq][4 * e4] = ca.x; cA[qq][4 * e4 + 1] = ca.y; cA[qq][4 * e4 + 2] = ca.z; cA[qq][4 * e4 + 3] = ca.w;
-                cB[qq][4 * e4] = cb.x; cB[qq][4 * e4 + 1] = cb.y; cB[qq][4 * e4 + 2] = cb.z; cB[qq][4 * e4 + 3] = cb.w;
-                sA[qq][4 * e4] = sa.x; sA[qq][4 * e4 + 1] = sa.y; sA[qq][4 * e4 + 2] = sa.z; sA[qq][4 * e4 + 3] = sa.w;
-                sB[qq][4 * e4] = sb.x; sB[qq][4 * e4 + 1] = sb.y; sB[qq][4 * e4 + 2] = sb.z; sB[qq][4 * e4 + 3] = sb.w;
+                raw.u[qq][ks][0] = *(const uint4 *)((const float *)a.q + base + 32 * ks);
+                raw.u[qq][ks][IN_BF16 ? 0 : 1] = *(const uint4 *)((const float *)a.q + base + 32 * ks + 4);
             }
         }
     }
+}
+
+// HK = rope_dim / 64: dim chunk ks rotates with chunk ks ^ HK (HK 0: no RoPE).
+template <typename T, bool IN_BF16, int HK>
+__device__ __forceinline__ void q_finish(const FlashArgs &a, const QRaw<IN_BF16> &raw, const bool (&ok)[2],
+                                         int grp, int c, const float *rope_lds, typename Mfma<T>::vec (&qf)[2][4]) {
+    constexpr int D = kHeadDim;
+    typedef typename Mfma<T>::vec vec;
+    const int rh = a.rope_half;
+    float gw[4][8];
     if (a.qnw) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
@@ -343,19 +334,54 @@ __device__ __forceinline__ void q_operand(const FlashArgs &a, int h, int q0, int
     }
 #pragma unroll
     for (int qq = 0; qq < 2; qq++) {
+        float x[4][8];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            if (IN_BF16) {
+                const uint4 u = raw.u[qq][ks][0];
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[ks][2 * e] = ok[qq] ? __uint_as_float(w[e] << 16) : 0.0f;
+                    x[ks][2 * e + 1] = ok[qq] ? __uint_as_float(w[e] & 0xFFFF0000u) : 0.0f;
+                }
+            } else {
+                const uint4 u0 = raw.u[qq][ks][0], u1 = raw.u[qq][ks][IN_BF16 ? 0 : 1];
+                const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) x[ks][e] = ok[qq] ? __uint_as_float(w[e]) : 0.0f;
+            }
+        }
+        float cA[8], cB[8], sA[8], sB[8];
+        if (HK) {
+            // LDS rope rows [cos|sin][32 rows][kRopeLd]
+            const float *rc = rope_lds + (qq * 16 + c) * kRopeLd, *rs = rc + 32 * kRopeLd;
+            const int fa = (8 * grp) & (rh - 1), fb = (32 + 8 * grp) & (rh - 1);
+#pragma unroll
+            for (int e4 = 0; e4 < 2; e4++) {
+                const float4 ca = *(const float4 *)(rc + fa + 4 * e4);
+                const float4 cb = *(const float4 *)(rc + fb + 4 * e4);
+                const float4 sa = *(const float4 *)(rs + fa + 4 * e4);
+                const float4 sb = *(const float4 *)(rs + fb + 4 * e4);
+                cA[4 * e4] = ca.x; cA[4 * e4 + 1] = ca.y; cA[4 * e4 + 2] = ca.z; cA[4 * e4 + 3] = ca.w;
+                cB[4 * e4] = cb.x; cB[4 * e4 + 1] = cb.y; cB[4 * e4 + 2] = cb.z; cB[4 * e4 + 3] = cb.w;
+                sA[4 * e4] = sa.x; sA[4 * e4 + 1] = sa.y; sA[4 * e4 + 2] = sa.z; sA[4 * e4 + 3] = sa.w;
+                sB[4 * e4] = sb.x; sB[4 * e4 + 1] = sb.y; sB[4 * e4 + 2] = sb.z; sB[4 * e4 + 3] = sb.w;
+            }
+        }
         float y[4][8], ss = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             // RoPE (Ops.RopeRange): first half x*c - x'*s, second half x'*s + x*c
-            const bool rot = ks < 2 * hk, lower = (ks & hk) == 0;
+            const bool rot = ks < 2 * HK, lower = (ks & HK) == 0;
 #pragma unroll
             for (int e = 0; e < 8; e++) {
-                const float xv = ok[qq] ? x[qq][ks][e] : 0.0f;
+                const float xv = x[ks][e];
                 float v = xv;
                 if (rot) {
-                    const float xp = ok[qq] ? (hk == 2 ? x[qq][ks ^ 2][e] : x[qq][ks ^ 1][e]) : 0.0f;
-                    const float cv = (ks & 1) ? cB[qq][e] : cA[qq][e];
-                    const float sv = (ks & 1) ? sB[qq][e] : sA[qq][e];
+                    const float xp = x[ks ^ HK][e];
+                    const float cv = (ks & 1) ? cB[e] : cA[e];
+                    const float sv = (ks & 1) ? sB[e] : sA[e];
                     v = lower ? xv * cv - xp * sv : xp * sv + xv * cv;
                 }
                 y[ks][e] = v;
@@ -382,9 +408,11 @@ __device__ __forceinline__ void q_operand(const FlashArgs &a, int h, int q0, int
 constexpr float kLazy = 8.0f;
 
 // 8 waves: wave w computes head (w & 3) of the GQA group over the tiles of
-// parity (w >> 2) in the item's range, so each SIMD runs two waves.  Tile
-// pair j sits in LDS buffer j & 1 (one slot per parity); the two halves'
-// (m, l, O) are combined through LDS at the end.
+// parity (w >> 2) in the item's range, so each SIMD runs two waves.  The
+// wave's 32 q rows are the 16 rows of the pair's short block A (qq = 0) and
+// the 16 of its long block B (qq = 1); tiles past A's causal range run B
+// alone.  Tile pair j sits in LDS buffer j & 1 (one slot per parity); the
+// two halves' (m, l, O) are combined through LDS at the end.
 template <typename T>
 __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
@@ -413,7 +441,12 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     if (item_idx >= a.items_per_kvh) return;
     const FlashItem it = flash_item(a, item_idx);
     const int h = kvh * G + hw;
-    const int q0 = it.qb * 32;
+    // the pair's blocks: qq = 0 -> short block A, qq = 1 -> long block B
+    const int blkA = it.pair, blkB = a.nb16 - 1 - it.pair;
+    const bool hasA = blkA < blkB;
+    const int lenA = hasA ? block_tiles(a.pos0, blkA, a.seq) : 0;  // A attends to tiles [0, lenA)
+    const int rowq[2] = {16 * blkA, 16 * blkB};
+    const bool okq[2] = {hasA, true};
     const int L = a.pos0 + a.seq;
     const size_t page_elems = (size_t)P * D;
     const uint16_t *kpool = (const uint16_t *)a.kpool;
@@ -462,11 +495,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
         *(uint4 *)(&v_[vr_ * VLD + 48 + vc_]) = rv3;                                        \
     } while (0)
 
-    // ---- q prologue: RoPE + RMSNorm of rows q0 + 16*qq + c straight into the
-    // S^T B operand (lane (grp, c): dims 32*ks + 8*grp + [0, 8)) ----
-    // ---- start: the first tile's loads, the page ids and the block's RoPE
-    // rows are all in flight before the q math.  The RoPE rows sit in the
-    // LDS slot of tile pair 1, which is first written after iteration 0.
+    // ---- start: the first tile's loads, the page ids, the pair's RoPE rows
+    // and the q rows are all in flight before the first barrier.  The RoPE
+    // rows sit in the LDS slot of tile pair 1, which is first written after
+    // iteration 0.
     const int nt = it.t1 - it.t0;  // <= kItemTiles (host caps items)
     const int half_u = __builtin_amdgcn_readfirstlane(half);  // wave-uniform: scalar page-id load
     if (half_u < nt) PF_FETCH_P(it.t0 + half_u, a.tab[it.t0 + half_u]);
@@ -477,16 +509,29 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
         // thread -> (table, row, 4 dims); 2 * 32 * rh / 4 <= 1024 float4
         for (int i = tid; i < 16 * rh; i += 512) {
             const int tbl = i / (8 * rh), rem = i % (8 * rh), r = rem / (rh / 4), f4 = rem % (rh / 4);
-            const int row = min(q0 + r, a.seq - 1);
+            const int row = min((r < 16 ? rowq[0] : rowq[1]) + (r & 15), a.seq - 1);
             const float *src = (tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * rh + 4 * f4;
             *(float4 *)(rope_lds + (tbl * 32 + r) * kRopeLd + 4 * f4) = *(const float4 *)src;
         }
     }
-    __syncthreads();
-
     vec qf[2][4];
-    if (a.io_bf16) q_operand<T, true>(a, h, q0, grp, c, rope_lds, qf);
-    else q_operand<T, false>(a, h, q0, grp, c, rope_lds, qf);
+    bool qok[2];
+    const int hk = a.rope_half >> 5;  // rope_dim / 64
+    if (a.io_bf16) {
+        QRaw<true> raw;
+        q_load<true>(a, h, rowq, okq, grp, c, raw, qok);
+        __syncthreads();
+        if (hk == 2) q_finish<T, true, 2>(a, raw, qok, grp, c, rope_lds, qf);
+        else if (hk == 1) q_finish<T, true, 1>(a, raw, qok, grp, c, rope_lds, qf);
+        else q_finish<T, true, 0>(a, raw, qok, grp, c, rope_lds, qf);
+    } else {
+        QRaw<false> raw;
+        q_load<false>(a, h, rowq, okq, grp, c, raw, qok);
+        __syncthreads();
+        if (hk == 2) q_finish<T, false, 2>(a, raw, qok, grp, c, rope_lds, qf);
+        else if (hk == 1) q_finish<T, false, 1>(a, raw, qok, grp, c, rope_lds, qf);
+        else q_finish<T, false, 0>(a, raw, qok, grp, c, rope_lds, qf);
+    }
 
     f32x4 o[8][2];
 #pragma unroll
@@ -496,118 +541,124 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     // m starts at the reference's -80 (natural log units); l is this lane's
     // partial row sum (its 16 positions of each tile)
     float mrun[2] = {kFloor2, kFloor2}, lrun[2] = {0.f, 0.f};
-    const int qmin = a.pos0 + q0;  // smallest q position of the block
+    const int qmin[2] = {a.pos0 + rowq[0], a.pos0 + rowq[1]};  // first q position of each block
 
     if (half < nt) PF_STASH(0);
     __syncthreads();
+
+    // One tile of this wave's parity for q blocks QQ0..1 (QQ0 = 0: both
+    // blocks; QQ0 = 1: the long block alone).
+    auto tile_body = [&](auto qq0_tag, int t, int j, int buf) {
+        constexpr int QQ0 = decltype(qq0_tag)::value;
+        const uint16_t *kt = sK + (buf * 2 + half) * KT;
+        const uint16_t *vt = sV + (buf * 2 + half) * VT;
+        // ---- S^T - m = K Q^T - m (64 kv x 16 q per block), accumulated onto
+        // -m; the half's first tile starts from 0 and sets m from its scores
+        const bool first = j == 0;
+        f32x4 sacc[4][2];
+#pragma unroll
+        for (int qq = QQ0; qq < 2; qq++) {
+            const float nm = first ? 0.0f : -mrun[qq];
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) sacc[kb][qq] = f32x4{nm, nm, nm, nm};
+        }
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++) {
+                const int r = kswz(krow(kb, c));
+                vec kf = __builtin_bit_cast(vec, *(const uint4 *)(&kt[r * KLD + ks * 32 + grp * 8]));
+#pragma unroll
+                for (int qq = QQ0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
+            }
+        }
+
+        // ---- online softmax (column c = q row); the causal mask only
+        // touches tiles reaching past a block's first row ----
+        const int kvbase = t * P;
+#pragma unroll
+        for (int qq = QQ0; qq < 2; qq++) {
+            if (kvbase + P - 1 > qmin[qq]) {
+                const int qpos = qmin[qq] + c;
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
+            }
+        }
+        float mx[2] = {-INFINITY, -INFINITY};
+#pragma unroll
+        for (int qq = QQ0; qq < 2; qq++) {
+            float v = -INFINITY;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) v = fmaxf(v, sacc[kb][qq][i]);
+            mx[qq] = v;
+        }
+        if (first) {
+#pragma unroll
+            for (int qq = QQ0; qq < 2; qq++) {
+                mrun[qq] = fmaxf(pf_xrow_max(mx[qq]), kFloor2);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= mrun[qq];
+            }
+        } else if (__any(fmaxf(mx[0], mx[1]) > kLazy)) {
+            // move m of every row to its maximum when that is higher
+#pragma unroll
+            for (int qq = QQ0; qq < 2; qq++) {
+                const float d = fmaxf(pf_xrow_max(mx[qq]), 0.0f);
+                const float al = __builtin_amdgcn_exp2f(-d);
+                mrun[qq] += d;
+                lrun[qq] *= al;
+#pragma unroll
+                for (int db = 0; db < 8; db++) o[db][qq] *= al;
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= d;
+            }
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int qq = QQ0; qq < 2; qq++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) sacc[kb][qq][i] = __builtin_amdgcn_exp2f(sacc[kb][qq][i]);
+
+        // ---- O^T += V^T P^T ----
+#pragma unroll
+        for (int ks2 = 0; ks2 < 2; ks2++) {
+            vec pf[2];
+#pragma unroll
+            for (int qq = QQ0; qq < 2; qq++) {
+                const f32x4 lo = sacc[2 * ks2][qq], hi = sacc[2 * ks2 + 1][qq];
+                const uint4 u = make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]),
+                                           pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]));
+                lrun[qq] = sum2<T>(u.w, sum2<T>(u.z, sum2<T>(u.y, sum2<T>(u.x, lrun[qq]))));
+                pf[qq] = __builtin_bit_cast(vec, u);
+            }
+#pragma unroll
+            for (int db = 0; db < 8; db++) {
+                vec vf = __builtin_bit_cast(vec, *(const uint4 *)(&vt[(db * 16 + c) * VLD + ks2 * 32 + grp * 8]));
+#pragma unroll
+                for (int qq = QQ0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
+            }
+        }
+    };
 
     for (int j = 0; 2 * j < nt; j++) {
         const int buf = j & 1;
         const int t = it.t0 + 2 * j + half;  // this wave's tile
         const bool more = t + 2 < it.t1;     // this thread stages tile t + 2
         if (more) PF_FETCH(t + 2);
-
         if (t < it.t1) {
-            const uint16_t *kt = sK + (buf * 2 + half) * KT;
-            const uint16_t *vt = sV + (buf * 2 + half) * VT;
-            // ---- S^T - m = K Q^T - m (64 kv x 32 q), accumulated onto -m; the
-            // half's first tile starts from 0 and sets m from its scores ----
-            const bool first = j == 0;
-            f32x4 sacc[4][2];
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                const float nm = first ? 0.0f : -mrun[qq];
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++) sacc[kb][qq] = f32x4{nm, nm, nm, nm};
-            }
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++) {
-                    const int r = kswz(krow(kb, c));
-                    vec kf = __builtin_bit_cast(vec, *(const uint4 *)(&kt[r * KLD + ks * 32 + grp * 8]));
-#pragma unroll
-                    for (int qq = 0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
-                }
-            }
-
-            // ---- online softmax (column c = q row); the causal mask only
-            // touches tiles reaching past the block's first row ----
-            const int kvbase = t * P;
-            if (kvbase + P - 1 > qmin) {
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) {
-                    const int qpos = qmin + qq * 16 + c;
-#pragma unroll
-                    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
-                }
-            }
-            float mx[2];
-#pragma unroll
-            for (int qq = 0; qq < 2; qq++) {
-                float v = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) v = fmaxf(v, sacc[kb][qq][i]);
-                mx[qq] = v;
-            }
-            if (first) {
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) {
-                    mrun[qq] = fmaxf(pf_xrow_max(mx[qq]), kFloor2);
-#pragma unroll
-                    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= mrun[qq];
-                }
-            } else if (__any(fmaxf(mx[0], mx[1]) > kLazy)) {
-                // move m of every row to its maximum when that is higher
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) {
-                    const float d = fmaxf(pf_xrow_max(mx[qq]), 0.0f);
-                    const float al = __builtin_amdgcn_exp2f(-d);
-                    mrun[qq] += d;
-                    lrun[qq] *= al;
-#pragma unroll
-                    for (int db = 0; db < 8; db++) o[db][qq] *= al;
-#pragma unroll
-                    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) sacc[kb][qq][i] -= d;
-                }
-            }
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) sacc[kb][qq][i] = __builtin_amdgcn_exp2f(sacc[kb][qq][i]);
-
-            // ---- O^T += V^T P^T ----
-#pragma unroll
-            for (int ks2 = 0; ks2 < 2; ks2++) {
-                vec pf[2];
-#pragma unroll
-                for (int qq = 0; qq < 2; qq++) {
-                    const f32x4 lo = sacc[2 * ks2][qq], hi = sacc[2 * ks2 + 1][qq];
-                    const uint4 u = make_uint4(pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]),
-                                               pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3]));
-                    lrun[qq] = sum2<T>(u.w, sum2<T>(u.z, sum2<T>(u.y, sum2<T>(u.x, lrun[qq]))));
-                    pf[qq] = __builtin_bit_cast(vec, u);
-                }
-#pragma unroll
-                for (int db = 0; db < 8; db++) {
-                    vec vf = __builtin_bit_cast(vec, *(const uint4 *)(&vt[(db * 16 + c) * VLD + ks2 * 32 + grp * 8]));
-#pragma unroll
-                    for (int qq = 0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
-                }
-            }
+            if (t < lenA) tile_body(std::integral_constant<int, 0>{}, t, j, buf);
+            else tile_body(std::integral_constant<int, 1>{}, t, j, buf);
         }
-
         if (more) PF_STASH(buf ^ 1);
         __syncthreads();
     }
@@ -653,8 +704,8 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     if (it.nsplit == 1) {
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
-            const int row = q0 + qq * 16 + c;
-            if (row >= a.seq) continue;
+            const int row = rowq[qq] + c;
+            if (!okq[qq] || row >= a.seq) continue;
             const float inv = lrun[qq] > 0.f ? 1.0f / lrun[qq] : 0.f;
             float *orow = a.out + (size_t)row * qdim + (size_t)h * D + grp * 4;
 #pragma unroll
@@ -697,10 +748,10 @@ hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_item
 }
 
 // ------------------------------------------------------------------ merge
-// Combine the split items of a q block: one workgroup per (q block, kv head,
-// head in group, 8-row quarter); thread -> (row, 4 dims).  All (m, l) of the
-// row are read first, then the partial O rows stream with up to 8 loads in
-// flight per thread.
+// Combine the split items of a block pair: one workgroup per (pair, kv head,
+// head in group, 8-row quarter of the pair's 32 rows); thread -> (row, 4
+// dims).  All (m, l) of the row are read first, then the partial O rows
+// stream with up to 8 loads in flight per thread.
 __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, G = kGroup;
     int b = blockIdx.x;
@@ -709,19 +760,15 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     const int g = b % G;
     b /= G;
     const int kvh = b % a.kv_heads;
-    const int qb = b / a.kv_heads;
-    int first = 0, ns = 0;
-    for (int q = a.nqb - 1; q >= 0; q--) {
-        const int n = flash_splits(flash_tiles(a.pos0, q, a.seq), a.cap);
-        if (q == qb) {
-            ns = n;
-            break;
-        }
-        first += n;
-    }
+    const int pr = b / a.kv_heads;
+    int first = 0;
+    for (int q = 0; q < pr; q++) first += flash_splits(pair_tiles(a.pos0, q, a.nb16, a.seq), a.cap);
+    const int ns = flash_splits(pair_tiles(a.pos0, pr, a.nb16, a.seq), a.cap);
     if (ns <= 1) return;
-    const int r = quarter * 8 + threadIdx.x / 32;
-    const int row = qb * 32 + r;
+    const int r = quarter * 8 + threadIdx.x / 32;  // row of the pair: r < 16 block A, else B
+    const int blk = r < 16 ? pr : a.nb16 - 1 - pr;
+    if (r < 16 && blk >= a.nb16 - 1 - pr) return;  // the middle block has no A rows
+    const int row = blk * 16 + (r & 15);
     if (row >= a.seq) return;
     const int d = (threadIdx.x % 32) * 4;
     const size_t slot0 = (size_t)kvh * a.items_per_kvh + first;
@@ -748,7 +795,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
 }
 
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.nqb * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.npairs * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

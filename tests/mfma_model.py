@@ -12,9 +12,13 @@ fp32 reference in its roundings and its order of accumulation only:
   half's first 64-position tile and on any later tile where some row of the
   wave's 32 rows has s - m > 8 (then for every row); otherwise m stays, so p
   may reach 2^8;
+* a wave's 32 rows are the 16-row q blocks b and nb-1-b of a block pair
+  (the causal work of every pair is then about equal); the pair's kv range
+  is that of its long block, the short block taking part in the tiles it
+  attends to;
 * the tiles of a work item alternate between two wave halves (even and odd
   tile offsets), each with its own (m, l, O), combined with weights
-  2^(m_i - max m); work items that split a q block's kv range are combined
+  2^(m_i - max m); work items that split a pair's kv range are combined
   the same way.
 
 This model reproduces those steps in fp64 so the GPU result can be checked
@@ -41,27 +45,35 @@ def round_to(x, dtype):
     raise ValueError(dtype)
 
 
-def tiles_of(pos0, qb, seq):
-    last = min(pos0 + qb * 32 + 31, pos0 + seq - 1)
+def block_tiles(pos0, b, seq):
+    """kv tiles the 16-row q block b attends to."""
+    last = min(pos0 + b * 16 + 15, pos0 + seq - 1)
     return last // 64 + 1
 
 
-def split_ranges(pos0, seq, kv_heads, cap=None):
-    """Tile ranges per q block, mirroring hymt_attn_prefill's work items."""
-    nqb = (seq + 31) // 32
-    max_tiles = max(tiles_of(pos0, qb, seq) for qb in range(nqb))
+def pair_items(pos0, seq, kv_heads, cap=None):
+    """Per block pair: (rows of the pair, its tile ranges), mirroring
+    hymt_attn_prefill's work items.  Pair p holds the short block p and the
+    long block nb-1-p (the middle block of an odd count alone)."""
+    nb = (seq + 15) // 16
+    npairs = (nb + 1) // 2
+    max_tiles = max(block_tiles(pos0, nb - 1 - p, seq) for p in range(npairs))
     if cap is None:
         cap = max_tiles
-        pairs = nqb * kv_heads
+        pairs = npairs * kv_heads
         if pairs < 256:
             per = (256 + pairs - 1) // pairs
             cap = max(4, (max_tiles + per - 1) // per)
     cap = min(cap, ITEM_TILES)
     out = []
-    for qb in range(nqb):
-        nt = tiles_of(pos0, qb, seq)
+    for p in range(npairs):
+        a, b = p, nb - 1 - p
+        rows = list(range(b * 16, min(b * 16 + 16, seq)))
+        if a < b:
+            rows += list(range(a * 16, a * 16 + 16))
+        nt = block_tiles(pos0, b, seq)
         ns = (nt + cap - 1) // cap
-        out.append([(s * nt // ns, (s + 1) * nt // ns) for s in range(ns)])
+        out.append((np.array(rows), [(s * nt // ns, (s + 1) * nt // ns) for s in range(ns)]))
     return out
 
 
@@ -111,14 +123,13 @@ def prefill_model(q_hat, cache_k, cache_v, heads, kv_heads, head_dim, pos0, seq,
     K = np.asarray(cache_k, np.float64)[:L].reshape(L, kv_heads, D)
     V = np.asarray(cache_v, np.float64)[:L].reshape(L, kv_heads, D)
     out = np.zeros((seq, heads, D))
-    ranges = split_ranges(pos0, seq, kv_heads, cap)
+    pairs = pair_items(pos0, seq, kv_heads, cap)
     qpos = pos0 + np.arange(seq)
     vis = np.arange(L)[None, :] <= qpos[:, None]
     for h in range(heads):
         kvh = h // G
         s_all = qm[:, h, :] @ K[:, kvh, :].T                 # [seq][L]
-        for qb, splits in enumerate(ranges):
-            rows = np.arange(qb * 32, min(qb * 32 + 32, seq))
+        for rows, splits in pairs:
             items = []
             for (t0, t1) in splits:
                 halves = [_half_softmax(s_all[rows], vis[rows], range(t0 + hp, t1, 2), L,
