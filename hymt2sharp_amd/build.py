@@ -17,13 +17,20 @@ CSRC = os.path.join(PKG, "csrc")
 HIP_LIB = os.path.join(PKG, "libhymt_hip.so")
 SYNTH_LIB = os.path.join(PKG, "libhymt_synth.so")
 
-HIP_SOURCES = ["hymt_hip.cpp", "decode_attn.hip", "prefill_attn.hip", "kv_ops.hip"]
+# Sources of libhymt_hip.so and the extra compiler flags of each.
+HIP_SOURCES = {
+    "hymt_hip.cpp": [],
+    "decode_attn.hip": [],
+    "prefill_attn.hip": [],
+    "kv_ops.hip": [],
+}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+BUILD_DIR = os.path.join(PKG, "_build")
 
 # Packed fp32 VALU ops are kept off: hipcc -O3 would otherwise form
 # v_pk_{add,mul,fma}_f32 from scalar float code.
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
 ]
@@ -38,9 +45,24 @@ def _run(cmd, cwd=None):
 
 
 def build_hip(extra=()):
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES]
+    """Compile every source to an object (in parallel), then link."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    objs, procs = [], []
+    for src, flags in HIP_SOURCES.items():
+        obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+        objs.append(obj)
+        cmd = [HIPCC, *HIP_FLAGS, *flags, *extra, "-c", os.path.join(CSRC, src), "-o", obj]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+    failed = []
+    for cmd, pr in procs:
+        out, _ = pr.communicate()
+        if pr.returncode != 0:
+            sys.stderr.write(out)
+            failed.append(" ".join(cmd))
+    if failed:
+        raise RuntimeError("build failed: " + "; ".join(failed))
     tmp = HIP_LIB + ".tmp"
-    _run([HIPCC, *HIP_FLAGS, *extra, *srcs, "-o", tmp])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, HIP_LIB)
     return HIP_LIB
 
