@@ -251,10 +251,11 @@ def cpu_threads():
     return max(1, min(n, 16))
 
 
-def cpu_baseline_decode(threads, layers=LAYERS, reps=20):
+def cpu_baseline_decode(threads, layers=LAYERS, seconds=10.0):
     """The oracle (C port of Ops.AttentionDecode and the DecodeAttention steps)
     on a sample of the same workload: `layers` layers of the 4096-context
-    step, mean of `reps` reps after one warm-up (Benchmark/Program.cs:189-211)."""
+    step, repeated for about `seconds` after one warm-up, mean per rep
+    (Benchmark/Program.cs:189-211).  Returns (GB/s, s per rep, reps)."""
     from oracle import oracle as O
     L = CTX + 1
     scale = 1.0 / np.sqrt(D)
@@ -275,14 +276,19 @@ def cpu_baseline_decode(threads, layers=LAYERS, reps=20):
                                threads=threads)
 
     one()
+    reps = 0
     t = time.perf_counter()
-    for _ in range(reps):
+    while time.perf_counter() - t < seconds:
         one()
+        reps += 1
     sec = (time.perf_counter() - t) / reps
-    return decode_bytes_per_layer(L) * layers / sec / 1e9, sec
+    return decode_bytes_per_layer(L) * layers / sec / 1e9, sec, reps
 
 
-def cpu_baseline_prefill(threads, seq=2048):
+def cpu_baseline_prefill(threads, seq=2048, seconds=10.0):
+    """The oracle's prefill (Forward's 1024-token chunks of AttentionScores ->
+    SoftmaxCausal -> AttentionCombine) on config 3, repeated for about
+    `seconds`.  Returns (TFLOP/s, s per run, runs)."""
     from oracle import oracle as O
     scale = 1.0 / np.sqrt(D)
     q = S.bf16_bits_to_f32(S.f32_to_bf16_bits(S.normal(S.seed(3, S.Q), (seq, HQ * D), scale)))
@@ -290,11 +296,14 @@ def cpu_baseline_prefill(threads, seq=2048):
     v = S.bf16_bits_to_f32(S.f32_to_bf16_bits(S.normal(S.seed(3, S.VNEW), (seq, HKV * D), scale)))
     ck = O.new_cache(seq, HKV, D, O.BF16)
     cv = O.new_cache(seq, HKV, D, O.BF16)
+    runs = 0
     t = time.perf_counter()
-    O.prefill_attention(q.reshape(seq, -1), k.reshape(seq, -1), v.reshape(seq, -1), None, None,
-                        ck, cv, O.BF16, HQ, HKV, D, BASE, EPS, 0, threads=threads)
-    sec = time.perf_counter() - t
-    return prefill_flops(0, seq) / sec / 1e12, sec
+    while time.perf_counter() - t < seconds:
+        O.prefill_attention(q.reshape(seq, -1), k.reshape(seq, -1), v.reshape(seq, -1), None, None,
+                            ck, cv, O.BF16, HQ, HKV, D, BASE, EPS, 0, threads=threads)
+        runs += 1
+    sec = (time.perf_counter() - t) / runs
+    return prefill_flops(0, seq) / sec / 1e12, sec, runs
 
 
 def copy_calibration(nbytes=64 << 20, reps=3):
@@ -337,6 +346,9 @@ def main():
                          "or the other configurations (1, 4, 5)")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="submit decode steps call by call instead of replaying a recorded step "
+                         "(for counter collection, which times dispatches one by one)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py measures one GPU: the attention path has no multi-GPU mode in this "
@@ -348,12 +360,13 @@ def main():
     dec = pre = None
     extra = {}
     if args.only in (None, "decode"):
-        dec = time_decode(2, CTX, F16, args.steps, args.warmup)
-        eager = time_decode(2, CTX, F16, args.steps, args.warmup, graph=False)
+        dec = time_decode(2, CTX, F16, args.steps, args.warmup, graph=not args.no_graph)
+        eager = dec if args.no_graph else time_decode(2, CTX, F16, args.steps, args.warmup,
+                                                      graph=False)
     if args.only in (None, "prefill"):
         pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup)
     if args.only in (None, "configs"):
-        c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False)
+        c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False, graph=not args.no_graph)
         extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, QK norm off "
                                         "(the configuration names none)",
                             "unit": "GB/s", "value": round(c1["gbs"], 1), **r4(c1)}
@@ -364,7 +377,7 @@ def main():
         sweep = {}
         for ctx in (1024, 4096, 16384, 32768):
             r = time_decode(5, ctx, F16, max(4, args.steps // 4), args.warmup,
-                            layers_per_step=8)
+                            layers_per_step=8, graph=not args.no_graph)
             sweep[str(ctx)] = {"gbs": round(r["gbs"], 1), "call_us": round(r["call_us"], 3),
                                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                                "bytes": r["bytes_per_layer"]}
@@ -374,16 +387,17 @@ def main():
     cpu = None
     if not args.no_cpu and dec is not None:
         th = cpu_threads()
-        gbs, sec = cpu_baseline_decode(th)
-        tfl, psec = cpu_baseline_prefill(th)
+        gbs, sec, reps = cpu_baseline_decode(th)
+        tfl, psec, runs = cpu_baseline_prefill(th)
         cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
-               "sample": f"the 32-layer 4096-context decode step (one KV set), mean of 20 reps "
-                         f"({sec * 1e3:.1f} ms per rep), C port of Ops.AttentionDecode "
-                         f"(oracle/hymt_oracle.c), fp16 KV",
+               "sample": f"the 32-layer 4096-context decode step (one KV set), mean of {reps} reps "
+                         f"({sec * 1e3:.1f} ms per rep, {reps * sec:.1f} s), C port of "
+                         f"Ops.AttentionDecode (oracle/hymt_oracle.c), fp16 KV",
                "prefill": {"value": round(tfl, 4), "unit": "TFLOP/s",
-                           "sample": f"one 2048-token causal prefill, {psec:.2f} s, "
-                                     f"C port of AttentionScores/SoftmaxCausal/AttentionCombine "
-                                     f"with Forward's 1024 chunking"}}
+                           "sample": f"the 2048-token causal prefill, mean of {runs} runs "
+                                     f"({psec:.3f} s per run, {runs * psec:.1f} s), C port of "
+                                     f"AttentionScores/SoftmaxCausal/AttentionCombine with "
+                                     f"Forward's 1024 chunking"}}
 
     traffic = load_traffic() or {}
     rec = {

@@ -12,7 +12,7 @@
 // from HBM once for all 4 q heads of its GQA group):
 //   workgroup = (split, kv head), 4 waves, `ppw` 64-position pages per split
 //   (one page per split until the split count reaches kMaxSplits, so a
-//   4k-context layer spreads over 260 workgroups, every CU).
+//   4k-context layer spreads over 256 workgroups, every CU).
 //   Wave w owns positions [16w, 16w+16) of every page of its split.  A wave's
 //   16 K rows and its 16x128 V^T sub-tile are each one contiguous 4 KiB block.
 //   The kernel is latency-bound at decode sizes, so the prologue is ordered
