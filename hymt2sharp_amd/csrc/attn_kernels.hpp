@@ -16,16 +16,42 @@ constexpr int kArgPages = 256;  // decode page lists passed in kernel arguments
 constexpr int kItemTiles = 1024; // prefill kv tiles per work item (page ids staged in LDS)
 
 // Paged pool addressing, per layer.  A page holds 64 positions of one kv head
-// for K and for V (16 KiB each in f16/bf16):
-//   K  element  page_base + t*D + d                      (row-major rows)
-//   V  element  page_base + ((t/16)*D + d)*16 + t%16     (transposed in
-//               16-position sub-tiles: [4][D][16])
-//   page_base = (phys*Hkv + kvh) * 64 * D
-// The transposed V gives the P*V MFMA operand 8 consecutive positions per
-// lane (prefill); the 16-position sub-tiles keep one decode wave's share of a
-// page (16 positions x 128 dims) one contiguous 4 KiB block.
-__host__ __device__ inline size_t v_off(int t, int d) {
+// for K and for V; page_base = (phys*Hkv + kvh) * 64 * D elements.
+//
+// f16/bf16 pages (16 KiB each) hold 16-byte chunks of 8 elements in MFMA
+// operand order, so that the operand loads of every kernel, and the copies
+// that stage a page into LDS, are linear 1 KiB wave accesses:
+//   K  chunk (s, j, c) = dims 8j..8j+7 of position 16s + c, at chunk index
+//      (16 s + j) * 16 + c.  Sub-tile s (16 positions) is one 4 KiB block;
+//      16 lanes reading dim chunk j of its 16 positions read 256 bytes.
+//   V  chunk (pc, d) = 8 positions of dim d, at chunk index pc * D + d.
+//      Chunk pc = 4m + g holds positions 32m + 4g + [0, 4) followed by
+//      32m + 16 + 4g + [0, 4): lane (g, c) of a 16x16 S^T MFMA output holds
+//      rows 4g + [0, 4), so the outputs of the two 16-position blocks of one
+//      32-position step form the P.V operand that meets this chunk.
+// f32 pages (VALU decode only): K row-major t*D + d; V transposed in
+// 16-position sub-tiles ((t/16)*D + d)*16 + t%16.
+__host__ __device__ inline size_t k_off16(int t, int d) {
+    return ((size_t)(((t >> 4) * 16 + (d >> 3)) * 16 + (t & 15)) << 3) + (d & 7);
+}
+// position of element e of V chunk pc (f16/bf16 pages)
+__host__ __device__ inline int v_chunk_pos(int pc, int e) {
+    return 32 * (pc >> 2) + 4 * (pc & 3) + 16 * (e >> 2) + (e & 3);
+}
+__host__ __device__ inline size_t v_off16(int t, int d) {
+    const int pc = 4 * (t >> 5) + ((t >> 2) & 3), e = 4 * ((t >> 4) & 1) + (t & 3);
+    return ((size_t)pc * kHeadDim + d) * 8 + e;
+}
+__host__ __device__ inline size_t k_off32(int t, int d) { return (size_t)t * kHeadDim + d; }
+__host__ __device__ inline size_t v_off32(int t, int d) {
     return ((size_t)(t >> 4) * kHeadDim + d) * 16 + (t & 15);
+}
+// by element size: 4 -> f32 page, 2 -> f16/bf16 page
+template <int BYTES> __host__ __device__ inline size_t k_off(int t, int d) {
+    return BYTES == 4 ? k_off32(t, d) : k_off16(t, d);
+}
+template <int BYTES> __host__ __device__ inline size_t v_off(int t, int d) {
+    return BYTES == 4 ? v_off32(t, d) : v_off16(t, d);
 }
 
 struct DecodeArgs {

@@ -130,6 +130,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
     constexpr int VN = Sh::VN, KCPR = Sh::KCPR, KRPI = Sh::KRPI, KLD = Sh::KLD;
     constexpr int VCPD = Sh::VCPD, VDPI = Sh::VDPI, VLD = Sh::VLD;
     using S = typename T::storage;
+    static_assert(sizeof(S) == 4, "the VALU kernel reads f32 pages (row-major K)");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Hkv = a.kv_heads;
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
             for (int e = 0; e < 2; e++) {
                 const int d = lane + 64 * e;
                 const S st = to_elem<T>(nin.x[e]);
-                vp[v_off(t, d)] = st;
+                vp[v_off32(t, d)] = st;
                 s_vnew[d] = from_elem<T>(st);
             }
         }
@@ -544,19 +545,22 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     const float vnew1 = a.vnew[(size_t)kvh * D + lane + 64];
 
     // ---- 3. the K/V stream --------------------------------------------------
-    // K A-operand: lane (grp, c) = K row c, dims 32*ks + 8*grp + [0, 8)
-    // V B-operand: lane (grp, c) = V^T row 16*db + c, positions 4*grp + [0, 4)
+    // K A-operand: lane (grp, c) = K row c, dims 32*ks + 8*grp + [0, 8): chunk
+    //   (wave, 4 ks + grp, c) of the page, one linear 1 KiB load per ks.
+    // V B-operand: lane (grp, c) = V^T row 16*db + c, positions 4*grp + [0, 4):
+    //   half (wave & 1) of V chunk (4 (wave >> 1) + grp, 16 db + c).
     // Whole sub-tiles are loaded (pages are fully allocated); rows at or past
     // pos are masked out of the scores and zeroed in V before use.
     uint4 ka[4], kn[4];
     uint2 vb[8], vn[8];
     auto load_sub = [&](int phys, uint4 *kk, uint2 *vv) {
-        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)(SUB * wave) * D;
-        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)wave * D * SUB;
+        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)wave * 2048 + lane * 8;
+        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)(wave >> 1) * 4096 +
+                             (wave & 1) * 4 + (grp * D + c) * 8;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + (size_t)c * D + 32 * ks + 8 * grp);
+        for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + 512 * ks);
 #pragma unroll
-        for (int db = 0; db < 8; db++) vv[db] = *(const uint2 *)(vp + (size_t)(16 * db + c) * SUB + 4 * grp);
+        for (int db = 0; db < 8; db++) vv[db] = *(const uint2 *)(vp + 128 * db);
     };
     load_sub(phys0, ka, vb);
     if (MULTI) load_sub(phys1, kn, vn);  // two pages in flight
@@ -738,12 +742,12 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     // ---- 8. append the new row to the cache ---------------------------------
     if (extra) {
         const int phys = page_id(newpos / P), t = newpos % P;
-        uint16_t *kp = (uint16_t *)kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)t * D;
+        uint16_t *kp = (uint16_t *)kpool + ((size_t)phys * Hkv + kvh) * page_elems;
         uint16_t *vp = (uint16_t *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            kp[lane + 64 * e] = knew_st[e];
-            vp[v_off(t, lane + 64 * e)] = vnew_st[e];
+            kp[k_off16(t, lane + 64 * e)] = knew_st[e];
+            vp[v_off16(t, lane + 64 * e)] = vnew_st[e];
         }
     }
 }

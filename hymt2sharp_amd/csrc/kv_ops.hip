@@ -49,8 +49,9 @@ __global__ void kv_upload_kernel(const uint16_t *kb, const uint16_t *vb, const i
         const int phys = tab[j / P], t = j % P;
         const size_t pg = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
         const size_t src = (size_t)(j - pos) * Hkv * D + (size_t)kvh * D + d;
-        kpool[pg + (size_t)t * D + d] = to_elem<T>(bf16_to_f32(kb[src]));
-        vpool[pg + v_off(t, d)] = to_elem<T>(bf16_to_f32(vb[src]));
+        constexpr int B = sizeof(typename T::storage);
+        kpool[pg + k_off<B>(t, d)] = to_elem<T>(bf16_to_f32(kb[src]));
+        vpool[pg + v_off<B>(t, d)] = to_elem<T>(bf16_to_f32(vb[src]));
     }
 }
 
@@ -83,8 +84,9 @@ __global__ void kv_read_kernel(const int32_t *tab, const typename T::storage *kp
         const int j = pos + r;
         const int phys = tab[j / P], t = j % P;
         const size_t pg = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
-        ko[i] = from_elem<T>(kpool[pg + (size_t)t * D + d]);
-        vo[i] = from_elem<T>(vpool[pg + v_off(t, d)]);
+        constexpr int B = sizeof(typename T::storage);
+        ko[i] = from_elem<T>(kpool[pg + k_off<B>(t, d)]);
+        vo[i] = from_elem<T>(vpool[pg + v_off<B>(t, d)]);
     }
 }
 

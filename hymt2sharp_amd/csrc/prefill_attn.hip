@@ -127,13 +127,15 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
         gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w; gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
     }
 
-    // V: round into LDS now, transpose after the barrier below
+    // V: round into LDS now, transpose after the barrier below.  Rows past
+    // the chunk (up to the end of its last page) are stored as zeros: the
+    // flash kernel stages whole pages, and P = 0 there must not meet NaN bits.
     {
         uint32_t w[4];
 #pragma unroll
         for (int e = 0; e < 4; e++)
             w[e] = (uint32_t)to_elem<T>(v[2 * e]) | ((uint32_t)to_elem<T>(v[2 * e + 1]) << 16);
-        *(uint4 *)&s_v[r][d0] = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)&s_v[r][d0] = m < a.seq ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
     }
 
     // RoPE (Ops.RopeRange, Ops.cs:157-165) then RMSNorm of the k row
@@ -157,30 +159,35 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; e++)
             w[e] = (uint32_t)to_elem<T>(y[2 * e]) | ((uint32_t)to_elem<T>(y[2 * e + 1]) << 16);
-        *(uint4 *)((S *)a.kpool + page_base + (size_t)(pstart % P + r) * D + d0) = make_uint4(w[0], w[1], w[2], w[3]);
+        *(uint4 *)((S *)a.kpool + page_base + k_off16(pstart % P + r, d0)) = make_uint4(w[0], w[1], w[2], w[3]);
     }
     __syncthreads();
-    // V^T sub-tile [d][16]: thread -> (d = tid/2, positions 8*(tid%2) + [0,8))
+    // V: thread -> (d = tid/2, positions h8 + [0, 8) of the block, h8 = 8*(tid%2)),
+    // i.e. 4 positions in each of two V chunks (8-byte stores)
     {
-        const int d = tid >> 1, h8 = (tid & 1) * 8;
-        S *dst = (S *)a.vpool + page_base + v_off(pstart % P, d) + h8;
+        const int d = tid >> 1, h8 = (tid & 1) * 8, t0 = pstart % P + h8;
+        S *vpage = (S *)a.vpool + page_base;
         const int m0 = pstart + h8 - a.pos0;
-        if (m0 >= 0 && m0 + 8 <= a.seq) {
-            uint32_t w[4];
+        if (m0 >= 0) {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                w[e] = (uint32_t)s_v[h8 + 2 * e][d] | ((uint32_t)s_v[h8 + 2 * e + 1][d] << 16);
-            *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
+            for (int q4 = 0; q4 < 2; q4++) {
+                const int r = h8 + 4 * q4;
+                const uint32_t w0 = (uint32_t)s_v[r][d] | ((uint32_t)s_v[r + 1][d] << 16);
+                const uint32_t w1 = (uint32_t)s_v[r + 2][d] | ((uint32_t)s_v[r + 3][d] << 16);
+                *(uint2 *)(vpage + v_off16(t0 + 4 * q4, d)) = make_uint2(w0, w1);
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                if (m0 + e >= 0 && m0 + e < a.seq) dst[e] = s_v[h8 + e][d];
+                if (m0 + e >= 0) vpage[v_off16(t0 + e, d)] = s_v[h8 + e][d];
         }
     }
 }
 
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
-    const int first = a.pos0 & ~15, last = a.pos0 + a.seq - 1;
+    // blocks of 16 positions from the chunk's first to the end of the page
+    // holding its last position (the V rows past the chunk are zeroed)
+    const int first = a.pos0 & ~15, last = ((a.pos0 + a.seq + kPage - 1) & ~(kPage - 1)) - 1;
     dim3 grid((last - first) / 16 + 1, a.kv_heads), block(256);
     switch (kv_dtype) {
     case 1: hipLaunchKernelGGL(prefill_kv_kernel<F16>, grid, block, 0, s, a); break;
@@ -237,29 +244,40 @@ template <> struct Mfma<F16> {
     }
 };
 
-// K tile rows live at LDS row swz(r): bits 2 and 4 of the row index swapped,
-// so the 16 rows one quarter-wave reads for an S^T block hit distinct banks.
-__device__ __forceinline__ int kswz(int r) { return (r & ~0x14) | ((r & 4) << 2) | ((r & 16) >> 2); }
+// LDS layout of a staged tile.  gfx950 serves a 16-byte LDS access of 16
+// lanes in one pass only when lanes 8i..8i+7 cover one 128-byte aligned
+// segment and the two 8-lane halves of each 16-lane group sit in opposite
+// 128-byte halves of a 256-byte block; any other pattern takes two passes.
+// Both tiles are therefore stored as 16-byte chunks in operand order, so that
+// every operand read and every staging store is one linear 1 KiB wave access.
+// The cache pages already hold their chunks in that order (k_off16 and
+// v_off16), so a tile is staged by a straight copy of its two pages:
+//   K: chunk (kb, j, c) = dims 8j..8j+7 of position 16 kb + c, at index
+//      (kb * 16 + j) * 16 + c;  the S^T A operand of block kb (positions
+//      16 kb + [0, 16)), dim step ks, is chunk (kb, 4 ks + grp, c) for lane
+//      (grp, c), and the S^T output of lane (grp, c) is positions
+//      16 kb + 4 grp + [0, 4).
+//   V: chunk (pc, d) at index pc * 128 + d holds positions
+//      v_chunk_pos(pc, 0..7) of V^T row d;  the P.V A operand of dim block
+//      db, step ks2 is chunk (4 ks2 + grp, 16 db + c) for lane (grp, c), and
+//      its positions are the S^T outputs of lane (grp, c) for blocks 2 ks2
+//      and 2 ks2 + 1: the P^T B operand of that lane, as packed.
 
-// Kv row of S^T block kb, block row r.  Chosen so that, after the softmax,
-// lane (grp, c) holds P for positions 32*(kb/2) + 8*grp + [0, 8) of both
-// blocks of a pair: the P^T operand then pairs with 8 consecutive positions
-// of a V^T row.
-__device__ __forceinline__ int krow(int kb, int r) {
-    return 32 * (kb >> 1) + 8 * (r >> 2) + 4 * (kb & 1) + (r & 3);
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane i writes LDS bytes lds_base + 16 i.
+// Issued as inline assembly so that the compiler does not treat it as an LDS
+// store that every later LDS read might alias (it would then wait for the
+// load before each read and no copy could overlap the work on earlier
+// tiles).  lds_base must be the same in every lane.  The caller orders it:
+// s_waitcnt vmcnt, then a barrier, before any wave reads the destination.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(src)
+                 : "memory", "m0");
 }
-
-// Zero the 16-bit elements of an 8-position V^T chunk starting at column
-// col0 whose position is >= nvalid (unwritten cache rows may hold any bits).
-__device__ __forceinline__ uint4 vmask(uint4 v, int col0, int nvalid) {
-    const int k = nvalid - col0;  // elements kept
-    if (k >= 8) return v;
-    if (k <= 0) return make_uint4(0, 0, 0, 0);
-    const uint32_t keep[4] = {k >= 2 ? 0xFFFFFFFFu : k == 1 ? 0x0000FFFFu : 0u,
-                              k >= 4 ? 0xFFFFFFFFu : k == 3 ? 0x0000FFFFu : 0u,
-                              k >= 6 ? 0xFFFFFFFFu : k == 5 ? 0x0000FFFFu : 0u,
-                              k == 7 ? 0x0000FFFFu : 0u};
-    return make_uint4(v.x & keep[0], v.y & keep[1], v.z & keep[2], v.w & keep[3]);
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
 }
 
 // Row sum of a packed pair of softmax weights (v_dot2c_f32_{bf16,f16} with
@@ -274,7 +292,10 @@ template <> __device__ __forceinline__ float sum2<F16>(uint32_t pair, float acc)
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, pair), __builtin_bit_cast(v2, 0x3C003C00u), acc, false);
 }
 
-constexpr int kRopeLd = 68;  // LDS row stride (floats) of the staged RoPE rows
+// Staged RoPE rows: float4 (tbl, f4, row) at index (tbl * 16 + f4) * 32 + row
+// (tbl 0 = cos, 1 = sin; rows 0..15 block A, 16..31 block B), so the 16 lanes
+// that read one dim chunk of 16 rows read one 256-byte block.
+constexpr int kRopeF4 = 16;  // float4 per table row (rope_dim / 8 <= 16)
 
 // q rows rowq[qq] + c of head h after RoPE and RMSNorm, times qscale, as the
 // S^T B operand: lane (grp, c) holds dims 32*ks + 8*grp + [0, 8).  The RoPE
@@ -354,15 +375,15 @@ __device__ __forceinline__ void q_finish(const FlashArgs &a, const QRaw<IN_BF16>
         }
         float cA[8], cB[8], sA[8], sB[8];
         if (HK) {
-            // LDS rope rows [cos|sin][32 rows][kRopeLd]
-            const float *rc = rope_lds + (qq * 16 + c) * kRopeLd, *rs = rc + 32 * kRopeLd;
-            const int fa = (8 * grp) & (rh - 1), fb = (32 + 8 * grp) & (rh - 1);
+            const float4 *rc = (const float4 *)rope_lds + qq * 16 + c;  // row qq*16 + c
+            const float4 *rs = rc + kRopeF4 * 32;
+            const int fa = ((8 * grp) & (rh - 1)) >> 2, fb = ((32 + 8 * grp) & (rh - 1)) >> 2;
 #pragma unroll
             for (int e4 = 0; e4 < 2; e4++) {
-                const float4 ca = *(const float4 *)(rc + fa + 4 * e4);
-                const float4 cb = *(const float4 *)(rc + fb + 4 * e4);
-                const float4 sa = *(const float4 *)(rs + fa + 4 * e4);
-                const float4 sb = *(const float4 *)(rs + fb + 4 * e4);
+                const float4 ca = rc[(fa + e4) * 32];
+                const float4 cb = rc[(fb + e4) * 32];
+                const float4 sa = rs[(fa + e4) * 32];
+                const float4 sb = rs[(fb + e4) * 32];
                 cA[4 * e4] = ca.x; cA[4 * e4 + 1] = ca.y; cA[4 * e4 + 2] = ca.z; cA[4 * e4 + 3] = ca.w;
                 cB[4 * e4] = cb.x; cB[4 * e4 + 1] = cb.y; cB[4 * e4 + 2] = cb.z; cB[4 * e4 + 3] = cb.w;
                 sA[4 * e4] = sa.x; sA[4 * e4 + 1] = sa.y; sA[4 * e4 + 2] = sa.z; sA[4 * e4 + 3] = sa.w;
@@ -416,20 +437,17 @@ constexpr float kLazy = 8.0f;
 template <typename T>
 __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
-    constexpr int KLD = D + 8;  // 272-byte K rows
-    constexpr int VLD = P + 8;  // 144-byte V^T rows
-    constexpr int KT = P * KLD, VT = D * VLD;  // elements of one staged tile
+    constexpr int KT = P * D;  // elements of one staged K or V tile (16 KiB)
     typedef typename Mfma<T>::vec vec;
-    // slot (buffer, parity) at index 2 * buffer + parity; sK doubles as the
-    // merge area of the epilogue ([head][17][64] float4 = 69632 bytes)
-    __shared__ __attribute__((aligned(16))) uint16_t sK[4 * KT];
-    __shared__ __attribute__((aligned(16))) uint16_t sV[4 * VT];
+    // K slot (buffer, parity) at sKV + (2 * buffer + parity) * KT, its V slot
+    // 4 * KT further; sKV doubles as the merge area of the epilogue
+    // ([head][17][64] float4 = 69632 bytes)
+    __shared__ __attribute__((aligned(16))) uint16_t sKV[8 * KT];
     __shared__ int32_t sTab[kItemTiles];  // physical pages of the item's tiles
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int hw = wave & 3, half = wave >> 2;
     const int grp = lane >> 4, c = lane & 15;
-    const int st = tid & 255;  // staging index within the half
     const int Hkv = a.kv_heads;
 
     // XCD-aware placement: workgroup b runs on XCD b % 8; give each XCD one kv
@@ -452,48 +470,23 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     const uint16_t *kpool = (const uint16_t *)a.kpool;
     const uint16_t *vpool = (const uint16_t *)a.vpool;
 
-    // K/V tile staging through registers: staging thread st of each half moves
-    // 16-byte chunks idx = st + 256*j of the K page (row idx/16, chunk idx%16)
-    // and of the V page (sub-tile idx/256, d (idx%256)/2, positions
-    // 16*sub + 8*(idx%2) + [0,8)) of the tile of its parity.
-    uint4 rk0, rk1, rk2, rk3, rv0, rv1, rv2, rv3;
-#define PF_FETCH(tile) PF_FETCH_P(tile, sTab[(tile) - it.t0])
-#define PF_FETCH_P(tile, phys)                                                              \
-    do {                                                                                    \
-        const int phys_ = (phys);                                                           \
-        const uint16_t *kp_ = kpool + ((size_t)phys_ * Hkv + kvh) * page_elems + st * 8;    \
-        const uint16_t *vp_ = vpool + ((size_t)phys_ * Hkv + kvh) * page_elems + st * 8;    \
-        rk0 = *(const uint4 *)(kp_);                                                        \
-        rk1 = *(const uint4 *)(kp_ + 2048);                                                 \
-        rk2 = *(const uint4 *)(kp_ + 4096);                                                 \
-        rk3 = *(const uint4 *)(kp_ + 6144);                                                 \
-        rv0 = *(const uint4 *)(vp_);                                                        \
-        rv1 = *(const uint4 *)(vp_ + 2048);                                                 \
-        rv2 = *(const uint4 *)(vp_ + 4096);                                                 \
-        rv3 = *(const uint4 *)(vp_ + 6144);                                                 \
-        const int nv_ = L - (tile) * P; /* positions >= L hold no data */                   \
-        if (nv_ < P) {                                                                      \
-            rv0 = vmask(rv0, 0 * 16 + (st & 1) * 8, nv_);                                   \
-            rv1 = vmask(rv1, 1 * 16 + (st & 1) * 8, nv_);                                   \
-            rv2 = vmask(rv2, 2 * 16 + (st & 1) * 8, nv_);                                   \
-            rv3 = vmask(rv3, 3 * 16 + (st & 1) * 8, nv_);                                   \
-        }                                                                                   \
-    } while (0)
-#define PF_STASH(buf)                                                                       \
-    do {                                                                                    \
-        uint16_t *k_ = sK + ((buf) * 2 + half) * KT;                                        \
-        uint16_t *v_ = sV + ((buf) * 2 + half) * VT;                                        \
-        const int kr_ = st / 16, kc_ = (st % 16) * 8;                                       \
-        *(uint4 *)(&k_[kswz(kr_) * KLD + kc_]) = rk0;                                       \
-        *(uint4 *)(&k_[kswz(kr_ + 16) * KLD + kc_]) = rk1;                                  \
-        *(uint4 *)(&k_[kswz(kr_ + 32) * KLD + kc_]) = rk2;                                  \
-        *(uint4 *)(&k_[kswz(kr_ + 48) * KLD + kc_]) = rk3;                                  \
-        const int vr_ = st / 2, vc_ = (st % 2) * 8;                                         \
-        *(uint4 *)(&v_[vr_ * VLD + vc_]) = rv0;                                             \
-        *(uint4 *)(&v_[vr_ * VLD + 16 + vc_]) = rv1;                                        \
-        *(uint4 *)(&v_[vr_ * VLD + 32 + vc_]) = rv2;                                        \
-        *(uint4 *)(&v_[vr_ * VLD + 48 + vc_]) = rv3;                                        \
-    } while (0)
+    // K/V tile staging: the 4 waves of a parity copy both pages of the
+    // parity's tile into its LDS slots with direct global->LDS loads
+    // (global_load_lds_dwordx4: lane i writes LDS bytes base + 16 i), wave hw
+    // taking chunks (4 i + hw) * 64 + lane of each page, i = 0..3.  The LDS
+    // tile is the page verbatim.  V rows past the chunk were zeroed by the k/v
+    // kernel, so whole pages are copied.
+    const uint32_t lds_kv = __builtin_amdgcn_readfirstlane(lds_addr(sKV) + hw * 1024);
+    auto fetch = [&](int phys, int buf) __attribute__((always_inline)) {
+        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
+        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
+        const uint32_t kl = lds_kv + (buf * 2 + half) * KT * 2;
+        const uint32_t vl = lds_kv + (4 + buf * 2 + half) * KT * 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) lds_dma16(kp + i * 2048, kl + i * 4096);
+#pragma unroll
+        for (int i = 0; i < 4; i++) lds_dma16(vp + i * 2048, vl + i * 4096);
+    };
 
     // ---- start: the first tile's loads, the page ids, the pair's RoPE rows
     // and the q rows are all in flight before the first barrier.  The RoPE
@@ -501,17 +494,18 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     // iteration 0.
     const int nt = it.t1 - it.t0;  // <= kItemTiles (host caps items)
     const int half_u = __builtin_amdgcn_readfirstlane(half);  // wave-uniform: scalar page-id load
-    if (half_u < nt) PF_FETCH_P(it.t0 + half_u, a.tab[it.t0 + half_u]);
+    if (half_u < nt) fetch(a.tab[it.t0 + half_u], 0);
     for (int i = tid; i < nt; i += 512) sTab[i] = a.tab[it.t0 + i];
-    float *rope_lds = (float *)(sV + 2 * VT);  // [cos|sin][32][kRopeLd]
+    // the V slot of buffer 1, parity 0 (16 KiB = 2 * kRopeF4 * 32 float4)
+    float *rope_lds = (float *)(sKV + (4 + 2) * KT);
     {
         const int rh = a.rope_half;
-        // thread -> (table, row, 4 dims); 2 * 32 * rh / 4 <= 1024 float4
+        // thread -> (table, 4 dims, row); 2 * 32 * rh / 4 <= 1024 float4
         for (int i = tid; i < 16 * rh; i += 512) {
-            const int tbl = i / (8 * rh), rem = i % (8 * rh), r = rem / (rh / 4), f4 = rem % (rh / 4);
+            const int r = i & 31, f4 = (i >> 5) % (rh / 4), tbl = i / (8 * rh);
             const int row = min((r < 16 ? rowq[0] : rowq[1]) + (r & 15), a.seq - 1);
             const float *src = (tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * rh + 4 * f4;
-            *(float4 *)(rope_lds + (tbl * 32 + r) * kRopeLd + 4 * f4) = *(const float4 *)src;
+            ((float4 *)rope_lds)[(tbl * kRopeF4 + f4) * 32 + r] = *(const float4 *)src;
         }
     }
     vec qf[2][4];
@@ -543,15 +537,15 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     float mrun[2] = {kFloor2, kFloor2}, lrun[2] = {0.f, 0.f};
     const int qmin[2] = {a.pos0 + rowq[0], a.pos0 + rowq[1]};  // first q position of each block
 
-    if (half < nt) PF_STASH(0);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the first tiles has landed
     __syncthreads();
 
     // One tile of this wave's parity for q blocks QQ0..1 (QQ0 = 0: both
     // blocks; QQ0 = 1: the long block alone).
     auto tile_body = [&](auto qq0_tag, int t, int j, int buf) {
         constexpr int QQ0 = decltype(qq0_tag)::value;
-        const uint16_t *kt = sK + (buf * 2 + half) * KT;
-        const uint16_t *vt = sV + (buf * 2 + half) * VT;
+        const uint16_t *kt = sKV + (buf * 2 + half) * KT + lane * 8;
+        const uint16_t *vt = sKV + (4 + buf * 2 + half) * KT + grp * 1024 + c * 8;
         // ---- S^T - m = K Q^T - m (64 kv x 16 q per block), accumulated onto
         // -m; the half's first tile starts from 0 and sets m from its scores
         const bool first = j == 0;
@@ -566,8 +560,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
         for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
             for (int kb = 0; kb < 4; kb++) {
-                const int r = kswz(krow(kb, c));
-                vec kf = __builtin_bit_cast(vec, *(const uint4 *)(&kt[r * KLD + ks * 32 + grp * 8]));
+                vec kf = __builtin_bit_cast(vec, *(const uint4 *)(kt + kb * 2048 + ks * 512));
 #pragma unroll
                 for (int qq = QQ0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
             }
@@ -584,7 +577,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
                 for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                     for (int i = 0; i < 4; i++)
-                        if (kvbase + krow(kb, grp * 4 + i) > qpos) sacc[kb][qq][i] = -INFINITY;
+                        if (kvbase + 16 * kb + 4 * grp + i > qpos) sacc[kb][qq][i] = -INFINITY;
             }
         }
         float mx[2] = {-INFINITY, -INFINITY};
@@ -643,7 +636,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
             }
 #pragma unroll
             for (int db = 0; db < 8; db++) {
-                vec vf = __builtin_bit_cast(vec, *(const uint4 *)(&vt[(db * 16 + c) * VLD + ks2 * 32 + grp * 8]));
+                vec vf = __builtin_bit_cast(vec, *(const uint4 *)(vt + ks2 * 4096 + db * 128));
 #pragma unroll
                 for (int qq = QQ0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
             }
@@ -653,21 +646,19 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     for (int j = 0; 2 * j < nt; j++) {
         const int buf = j & 1;
         const int t = it.t0 + 2 * j + half;  // this wave's tile
-        const bool more = t + 2 < it.t1;     // this thread stages tile t + 2
-        if (more) PF_FETCH(t + 2);
+        // tile t + 2 goes into the other buffer, which every wave finished
+        // reading before the previous barrier
+        if (t + 2 < it.t1) fetch(sTab[t + 2 - it.t0], buf ^ 1);
         if (t < it.t1) {
             if (t < lenA) tile_body(std::integral_constant<int, 0>{}, t, j, buf);
             else tile_body(std::integral_constant<int, 1>{}, t, j, buf);
         }
-        if (more) PF_STASH(buf ^ 1);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
         __syncthreads();
     }
-#undef PF_FETCH
-#undef PF_FETCH_P
-#undef PF_STASH
 
     // ---- combine the two parities: half 1 hands (m, l, O) to half 0 ----
-    float4 *xo = (float4 *)sK + hw * 17 * 64 + lane;
+    float4 *xo = (float4 *)sKV + hw * 17 * 64 + lane;
     if (half) {
 #pragma unroll
         for (int db = 0; db < 8; db++)

@@ -144,7 +144,11 @@ int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const fl
  * per-weight clamp at -80 below the maximum is not applied (such weights are
  * below 2e-35 of the largest, under fp32 resolution of the row sum).
  * Cache dtype f16 or bf16 (MFMA operand type); f32 caches
- * return HYMT_E_UNSUPPORTED.  Replaces HunyuanDenseModel.PrefillAttention
+ * return HYMT_E_UNSUPPORTED.  The V rows after the chunk, up to the end of
+ * the 64-position page that holds its last position, are set to zero (the
+ * reference treats positions >= pos+seq as unwritten; ForwardStep's
+ * postcondition covers [0, pos+seq) only, IComputeBackend.cs:40-47).
+ * Replaces HunyuanDenseModel.PrefillAttention
  * lines 53-83 (HunyuanDenseModel.Prefill.cs), the pf_kvprep + pf_fa32 pair
  * of the Vulkan backend (VulkanBackend.cs:786-802).
  */
