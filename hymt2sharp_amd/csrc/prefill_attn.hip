@@ -270,6 +270,8 @@ template <> struct Mfma<F16> {
 // load before each read and no copy could overlap the work on earlier
 // tiles).  lds_base must be the same in every lane.  The caller orders it:
 // s_waitcnt vmcnt, then a barrier, before any wave reads the destination.
+// m0 is written here and declared clobbered; the kernels that use this keep
+// nothing else in m0.
 __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
                  :
@@ -477,15 +479,16 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     // tile is the page verbatim.  V rows past the chunk were zeroed by the k/v
     // kernel, so whole pages are copied.
     const uint32_t lds_kv = __builtin_amdgcn_readfirstlane(lds_addr(sKV) + hw * 1024);
+    // page 0 = K, 1 = V of the tile in physical page `phys`
+    auto fetch_page = [&](int phys, int buf, int page) __attribute__((always_inline)) {
+        const uint16_t *src = (page ? vpool : kpool) + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
+        const uint32_t dst = lds_kv + ((page ? 4 : 0) + buf * 2 + half) * KT * 2;
+#pragma unroll
+        for (int i = 0; i < 4; i++) lds_dma16(src + i * 2048, dst + i * 4096);
+    };
     auto fetch = [&](int phys, int buf) __attribute__((always_inline)) {
-        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
-        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
-        const uint32_t kl = lds_kv + (buf * 2 + half) * KT * 2;
-        const uint32_t vl = lds_kv + (4 + buf * 2 + half) * KT * 2;
-#pragma unroll
-        for (int i = 0; i < 4; i++) lds_dma16(kp + i * 2048, kl + i * 4096);
-#pragma unroll
-        for (int i = 0; i < 4; i++) lds_dma16(vp + i * 2048, vl + i * 4096);
+        fetch_page(phys, buf, 0);
+        fetch_page(phys, buf, 1);
     };
 
     // ---- start: the first tile's loads, the page ids, the pair's RoPE rows
@@ -542,7 +545,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
 
     // One tile of this wave's parity for q blocks QQ0..1 (QQ0 = 0: both
     // blocks; QQ0 = 1: the long block alone).
-    auto tile_body = [&](auto qq0_tag, int t, int j, int buf) {
+    // nphys >= 0: the tile this wave stages next (into buffer buf ^ 1); its
+    // K page copy is issued after the S MFMAs, its V page copy after the
+    // softmax, so that the copies queue behind work instead of in one burst
+    auto tile_body = [&](auto qq0_tag, int t, int j, int buf, int nphys) {
         constexpr int QQ0 = decltype(qq0_tag)::value;
         const uint16_t *kt = sKV + (buf * 2 + half) * KT + lane * 8;
         const uint16_t *vt = sKV + (4 + buf * 2 + half) * KT + grp * 1024 + c * 8;
@@ -565,6 +571,8 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
                 for (int qq = QQ0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
             }
         }
+
+        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 0);
 
         // ---- online softmax (column c = q row); the causal mask only
         // touches tiles reaching past a block's first row ----
@@ -622,6 +630,8 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) sacc[kb][qq][i] = __builtin_amdgcn_exp2f(sacc[kb][qq][i]);
 
+        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 1);
+
         // ---- O^T += V^T P^T ----
 #pragma unroll
         for (int ks2 = 0; ks2 < 2; ks2++) {
@@ -648,10 +658,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
         const int t = it.t0 + 2 * j + half;  // this wave's tile
         // tile t + 2 goes into the other buffer, which every wave finished
         // reading before the previous barrier
-        if (t + 2 < it.t1) fetch(sTab[t + 2 - it.t0], buf ^ 1);
+        const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
         if (t < it.t1) {
-            if (t < lenA) tile_body(std::integral_constant<int, 0>{}, t, j, buf);
-            else tile_body(std::integral_constant<int, 1>{}, t, j, buf);
+            if (t < lenA) tile_body(std::integral_constant<int, 0>{}, t, j, buf, nphys);
+            else tile_body(std::integral_constant<int, 1>{}, t, j, buf, nphys);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
         __syncthreads();
