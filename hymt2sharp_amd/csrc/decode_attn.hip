@@ -28,16 +28,6 @@ namespace hymt {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T> struct DecodeShape {
-    static constexpr int D = kHeadDim, SUB = 16;
-    static constexpr int VN = Vec16<T>::N;    // elements per 16-byte vector
-    static constexpr int KCPR = D / VN;       // lanes per K row (16 or 32)
-    static constexpr int KRPI = 64 / KCPR;    // K rows per wave load (4 or 2)
-    static constexpr int KLD = SUB / KRPI;    // K loads per lane per sub-tile
-    static constexpr int VCPD = SUB / VN;     // lanes per V^T row of a sub-tile (2 or 4)
-    static constexpr int VDPI = 64 / VCPD;    // V^T rows per wave load (32 or 16)
-    static constexpr int VLD = D / VDPI;      // V loads per lane per sub-tile
-};
 
 // RoPE (Ops.RopeRange, Ops.cs:157-165) of element d of one head row whose
 // values at d and at its rotation partner are x and xp.
@@ -54,314 +44,17 @@ __device__ __forceinline__ int rope_index(int d, int half, int rope_dim) {
     return d < half ? d : d < rope_dim ? d - half : 0;
 }
 
-// One 128-wide head row held as lanes (d, d+64): loads of x, rotation
-// partners, cos/sin and gamma, all issued together (no dependent round trips).
-struct RowIn {
-    float x[2], xp[2], c[2], s[2], w[2];
-    __device__ __forceinline__ void load(const float *row, const float *cs, const float *sn,
-                                         const float *gamma, int lane, int half, int rope_dim) {
-        x[0] = row[lane];
-        x[1] = row[lane + 64];
-        w[0] = gamma ? gamma[lane] : 1.0f;
-        w[1] = gamma ? gamma[lane + 64] : 1.0f;
-        if (half == 64) {  // full-width NeoX RoPE: the partner of d is d^64, same lane
-            xp[0] = x[1];
-            xp[1] = x[0];
-            c[0] = c[1] = cs[lane];
-            s[0] = s[1] = sn[lane];
-            return;
-        }
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const int d = lane + 64 * e;
-            xp[e] = row[rope_partner(d, half, rope_dim)];
-            const int i = rope_index(d, half, rope_dim);
-            c[e] = cs[i];
-            s[e] = sn[i];
-        }
-    }
-    // RoPE then RMSNorm (HunyuanDenseModel.Decode.cs:80-85): y = rope(x) * r * gamma
-    __device__ __forceinline__ void finish(float *y, int lane, int half, int rope_dim, bool norm,
-                                           float eps) const {
-#pragma unroll
-        for (int e = 0; e < 2; e++) y[e] = rope_elem(lane + 64 * e, x[e], xp[e], c[e], s[e], half, rope_dim);
-        if (norm) {
-            const float ss = group_sum<64>(y[0] * y[0] + y[1] * y[1]);
-            const float r = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
-            y[0] = y[0] * r * w[0];
-            y[1] = y[1] * r * w[1];
-        }
-    }
-};
-
-// Combine the 4 wave partials of one split (s_m, s_l, s_acc in LDS, after a
-// workgroup barrier) and either finish the output (single split) or store
-// the split partial for decode_merge_kernel.
-__device__ __forceinline__ void split_epilogue(const DecodeArgs &a, int kvh, int split, int tid,
-                                               const float (&s_m)[4][kGroup], const float (&s_l)[4][kGroup],
-                                               const float (&s_acc)[4][kGroup][kHeadDim]) {
-    constexpr int D = kHeadDim, G = kGroup;
-    const int g = tid >> 6, d0 = (tid & 63) * 2;  // thread -> head g, dims d0, d0+1
-    const int h = kvh * G + g;
-    float M = s_m[0][g];
-#pragma unroll
-    for (int w = 1; w < 4; w++) M = fmaxf(M, s_m[w][g]);
-    float Lw = 0.0f, o0 = 0.0f, o1 = 0.0f;
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-        const float sc = exp2f(s_m[w][g] - M);
-        Lw = fmaf(sc, s_l[w][g], Lw);
-        o0 = fmaf(sc, s_acc[w][g][d0], o0);
-        o1 = fmaf(sc, s_acc[w][g][d0 + 1], o1);
-    }
-    if (a.nsplit == 1) {
-        const float inv = Lw > 0.0f ? 1.0f / Lw : 0.0f;
-        *(float2 *)(a.out + (size_t)h * D + d0) = make_float2(o0 * inv, o1 * inv);
-        return;
-    }
-    *(float2 *)(a.part_acc + ((size_t)h * kMaxSplits + split) * D + d0) = make_float2(o0, o1);
-    if (d0 == 0) *(float2 *)(a.part_ml + ((size_t)h * kMaxSplits + split) * 2) = make_float2(M, Lw);
-}
-
-template <typename T, bool MULTI>
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
-    using Sh = DecodeShape<T>;
-    constexpr int D = kHeadDim, G = kGroup, P = kPage, SUB = Sh::SUB;
-    constexpr int VN = Sh::VN, KCPR = Sh::KCPR, KRPI = Sh::KRPI, KLD = Sh::KLD;
-    constexpr int VCPD = Sh::VCPD, VDPI = Sh::VDPI, VLD = Sh::VLD;
-    using S = typename T::storage;
-    static_assert(sizeof(S) == 4, "the VALU kernel reads f32 pages (row-major K)");
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int Hkv = a.kv_heads;
-    const int kvh = blockIdx.x % Hkv;
-    const int split = blockIdx.x / Hkv;
-    const int npages = (a.L + P - 1) / P;
-    const int page0 = split * a.ppw;
-    const int page_end = MULTI ? min(page0 + a.ppw, npages) : page0 + 1;
-    const int newpos = a.L - 1;
-    const bool owner = page_end == npages;
-
-    __shared__ float s_q[G][D];
-    __shared__ float s_knew[D], s_vnew[D];
-    __shared__ float s_p[4][G][SUB];
-    __shared__ float s_acc[4][G][D];
-    __shared__ float s_m[4][G], s_l[4][G];
-
-    const size_t page_elems = (size_t)P * D;
-    const S *kpool = (const S *)a.kpool;
-    const S *vpool = (const S *)a.vpool;
-    const int kc = lane % KCPR, kg = lane / KCPR;
-    const int vc = lane % VCPD, vd = lane / VCPD;
-    const int half = a.rope_half, rdim = a.rope_dim;
-
-    // ---- prologue loads first: vmcnt retires in order, so the small q/k/v
-    // rows must not queue behind the K/V stream ------------------------------
-    RowIn qin, nin;
-    qin.load(a.q + (size_t)(kvh * G + wave) * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
-    if (owner && wave == 0)
-        nin.load(a.knew + (size_t)kvh * D, a.rope_cos, a.rope_sin, a.knw, lane, half, rdim);
-    if (owner && wave == 1)
-        nin.load(a.vnew + (size_t)kvh * D, a.rope_cos, a.rope_sin, nullptr, lane, half, rdim);
-
-    // this wave's sub-tile of page `page`: positions page*64 + 16*wave + [0, 16)
-    uint4 kb[KLD], vb[VLD];
-    auto load_sub = [&](int page, uint4 *kk, uint4 *vv) {
-        const int base = page * P + SUB * wave;
-        const int inmem = newpos - base;  // positions < newpos are resident
-        const int phys = a.pages_in_args ? a.pages[page] : a.tab[page];
-        const S *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)(SUB * wave) * D;
-        const S *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)wave * D * SUB;
-#pragma unroll
-        for (int j = 0; j < KLD; j++) {
-            const int r = kg + KRPI * j;
-            kk[j] = r < inmem ? *(const uint4 *)(kp + (size_t)r * D + kc * VN) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int j = 0; j < VLD; j++) {
-            const int d = vd + VDPI * j;
-            vv[j] = vc * VN < inmem ? *(const uint4 *)(vp + (size_t)d * SUB + vc * VN) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    load_sub(page0, kb, vb);
-
-    // ---- prologue math: RoPE + RMSNorm of q (wave g: head g), new k and v ----
-    {
-        float y[2];
-        qin.finish(y, lane, half, rdim, a.qnw != nullptr, a.eps);
-        s_q[wave][lane] = y[0] * a.qscale;
-        s_q[wave][lane + 64] = y[1] * a.qscale;
-    }
-    if (owner && wave < 2) {
-        const int t = newpos % P;
-        const int phys = a.pages_in_args ? a.pages[newpos / P] : a.tab[newpos / P];
-        if (wave == 0) {
-            float y[2];
-            nin.finish(y, lane, half, rdim, a.knw != nullptr, a.eps);
-            S *kp = (S *)kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)t * D;
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const S st = to_elem<T>(y[e]);
-                kp[lane + 64 * e] = st;
-                s_knew[lane + 64 * e] = from_elem<T>(st);
-            }
-        } else {
-            S *vp = (S *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                const int d = lane + 64 * e;
-                const S st = to_elem<T>(nin.x[e]);
-                vp[v_off32(t, d)] = st;
-                s_vnew[d] = from_elem<T>(st);
-            }
-        }
-    }
-    __syncthreads();
-
-    float qreg[G][VN];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int e = 0; e < VN; e++) qreg[g][e] = s_q[g][kc * VN + e];
-
-    float acc[VLD][G];
-#pragma unroll
-    for (int j = 0; j < VLD; j++)
-#pragma unroll
-        for (int g = 0; g < G; g++) acc[j][g] = 0.0f;
-    float m_run[G], l_run[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        m_run[g] = kFloor2;
-        l_run[g] = 0.0f;
-    }
-
-    for (int page = page0; page < page_end; page++) {
-        const int base = page * P + SUB * wave;
-        const int nvalid = min(SUB, a.L - base);  // may be <= 0 past the end
-        uint4 kn[KLD], vn[VLD];
-        const bool more = MULTI && page + 1 < page_end;
-        if (more) load_sub(page + 1, kn, vn);
-        if (nvalid > 0) {
-            // ---- scores of rows kg + KRPI*j --------------------------------
-            float sc[KLD][G];
-#pragma unroll
-            for (int j = 0; j < KLD; j++) {
-                const int r = kg + KRPI * j;
-                float kv[VN];
-                Vec16<T>::unpack(kb[j], kv);
-                if (base + r == newpos) {
-#pragma unroll
-                    for (int e = 0; e < VN; e++) kv[e] = s_knew[kc * VN + e];
-                }
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float s = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < VN; e++) s = fmaf(qreg[g][e], kv[e], s);
-                    sc[j][g] = lane_sum<KCPR>(s);
-                }
-            }
-            // ---- online softmax over the sub-tile, per head ----------------
-            float alpha[G];
-#pragma unroll
-            for (int g = 0; g < G; g++) {
-                float mt = -INFINITY;
-#pragma unroll
-                for (int j = 0; j < KLD; j++)
-                    if (kg + KRPI * j < nvalid) mt = fmaxf(mt, sc[j][g]);
-#pragma unroll
-                for (int o = KCPR; o < 64; o <<= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
-                const float mnew = fmaxf(m_run[g], mt);
-                alpha[g] = exp2f(m_run[g] - mnew);
-                float ps = 0.0f;
-#pragma unroll
-                for (int j = 0; j < KLD; j++) {
-                    const float p = kg + KRPI * j < nvalid ? exp2f(fmaxf(sc[j][g] - mnew, kFloor2)) : 0.0f;
-                    sc[j][g] = p;
-                    ps += p;
-                }
-#pragma unroll
-                for (int o = KCPR; o < 64; o <<= 1) ps += __shfl_xor(ps, o, 64);
-                l_run[g] = l_run[g] * alpha[g] + ps;
-                m_run[g] = mnew;
-            }
-            if (kc == 0) {
-#pragma unroll
-                for (int j = 0; j < KLD; j++)
-#pragma unroll
-                    for (int g = 0; g < G; g++) s_p[wave][g][kg + KRPI * j] = sc[j][g];
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-            // ---- P * V over the sub-tile: V^T rows vd + VDPI*j ---------------
-            float preg[G][VN];
-#pragma unroll
-            for (int g = 0; g < G; g++)
-#pragma unroll
-                for (int e = 0; e < VN; e++) preg[g][e] = s_p[wave][g][vc * VN + e];
-#pragma unroll
-            for (int j = 0; j < VLD; j++) {
-                const int d = vd + VDPI * j;
-                float vv[VN];
-                Vec16<T>::unpack(vb[j], vv);
-#pragma unroll
-                for (int e = 0; e < VN; e++) {
-                    const int t = base + vc * VN + e;
-                    if (t == newpos) vv[e] = s_vnew[d];
-                    else if (t > newpos) vv[e] = 0.0f;
-                }
-#pragma unroll
-                for (int g = 0; g < G; g++) {
-                    float s = acc[j][g] * alpha[g];
-#pragma unroll
-                    for (int e = 0; e < VN; e++) s = fmaf(preg[g][e], vv[e], s);
-                    acc[j][g] = s;
-                }
-            }
-            __builtin_amdgcn_wave_barrier();  // s_p is rewritten by the next sub-tile
-        }
-        if (more) {
-#pragma unroll
-            for (int j = 0; j < KLD; j++) kb[j] = kn[j];
-#pragma unroll
-            for (int j = 0; j < VLD; j++) vb[j] = vn[j];
-        }
-    }
-
-    // ---- combine the 4 wave partials of this split --------------------------
-#pragma unroll
-    for (int j = 0; j < VLD; j++)
-#pragma unroll
-        for (int g = 0; g < G; g++) acc[j][g] = lane_sum<VCPD>(acc[j][g]);
-    if (vc == 0) {
-#pragma unroll
-        for (int j = 0; j < VLD; j++)
-#pragma unroll
-            for (int g = 0; g < G; g++) s_acc[wave][g][vd + VDPI * j] = acc[j][g];
-    }
-    if (lane == 0) {  // m_run / l_run are uniform across the wave
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            s_m[wave][g] = m_run[g];
-            s_l[wave][g] = l_run[g];
-        }
-    }
-    __syncthreads();
-    split_epilogue(a, kvh, split, tid, s_m, s_l, s_acc);
-}
 
 // ---------------------------------------------------------------------------
-// f16 / bf16 caches: the two dot products run on MFMA.
+// The two dot products run on MFMA.
 //   S  = K_sub (16 pos x 128) . Qcat^T      v_mfma_f32_16x16x32_{f16,bf16} x4
 //   O += Pcat (16 rows x 16 pos) . V_sub     v_mfma_f32_16x16x16{f16,bf16_1k} x8
 // Qcat columns 0..3 hold q of the 4 heads rounded to the operand type and
 // columns 4..7 the rounding residual (q - hi) rounded again; Pcat rows 0..3 /
 // 4..7 do the same for the softmax weights.  Summing the two halves gives
 // q and P to about 2^-22 (f16) or 2^-18 (bf16) relative, i.e. the fp32 path's
-// accuracy, with K and V consumed exactly as stored.
+// accuracy, with f16/bf16 K and V consumed exactly as stored.  f32 caches use
+// the bf16 MFMAs with K and V split the same way (twice the MFMAs).
 template <typename T> struct DecMfma;
 template <> struct DecMfma<F16> {
     typedef _Float16 v8 __attribute__((ext_vector_type(8)));
@@ -389,6 +82,38 @@ template <typename T> __device__ __forceinline__ uint32_t split_pair(float x) {
     const uint16_t hi = to_elem<T>(x);
     const uint16_t lo = to_elem<T>(x - from_elem<T>(hi));
     return (uint32_t)hi | ((uint32_t)lo << 16);
+}
+
+// f32 operands for the bf16 MFMAs: 8 floats (two uint4) -> hi and lo
+// operands, x = hi + lo to about 2^-17 relative.
+__device__ __forceinline__ void split8(const uint4 &a, const uint4 &b, uint4 &hi, uint4 &lo) {
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const uint32_t p0 = split_pair<BF16>(__uint_as_float(w[2 * e]));
+        const uint32_t p1 = split_pair<BF16>(__uint_as_float(w[2 * e + 1]));
+        h[e] = (p0 & 0xFFFFu) | (p1 << 16);
+        l[e] = (p0 >> 16) | (p1 & 0xFFFF0000u);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+// 4 floats of V (positions 4 grp + j) -> hi and lo operands; positions whose
+// halfword keep mask is clear are zeroed first
+__device__ __forceinline__ void split4(const uint4 &v, const uint32_t (&keep)[2], uint2 &hi, uint2 &lo) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[2], l[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const float x0 = (keep[e] & 0xFFFFu) ? __uint_as_float(w[2 * e]) : 0.0f;
+        const float x1 = (keep[e] & 0xFFFF0000u) ? __uint_as_float(w[2 * e + 1]) : 0.0f;
+        const uint32_t p0 = split_pair<BF16>(x0), p1 = split_pair<BF16>(x1);
+        h[e] = (p0 & 0xFFFFu) | (p1 << 16);
+        l[e] = (p0 >> 16) | (p1 & 0xFFFF0000u);
+    }
+    hi = make_uint2(h[0], h[1]);
+    lo = make_uint2(l[0], l[1]);
 }
 
 // Cross-row sums / maxima (rows are 16 lanes): permlane swaps on gfx950.
@@ -475,7 +200,7 @@ template <int NR, bool FULL> struct RowsIn {
     }
 };
 
-// f16 / bf16 decode.
+// Decode for every cache type.
 //   The cached positions [0, pos) are split by pages: workgroup (split, kv
 //   head), 4 waves; wave w streams the 16-position sub-tile [16w, 16w+16) of
 //   each of the split's pages.
@@ -495,7 +220,13 @@ template <int NR, bool FULL> struct RowsIn {
 template <typename T, bool MULTI, bool PAGES_ARG, bool FULL>
 __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     constexpr int D = kHeadDim, G = kGroup, P = kPage, SUB = 16;
-    using M = DecMfma<T>;
+    // f32 pages: each K and V operand is split on the fly into bf16 hi + lo
+    // (x - hi rounded again) and both parts go through the MFMA, so K and V
+    // enter the products to about 2^-17 relative, as q and P do
+    constexpr bool W4 = sizeof(typename T::storage) == 4;
+    using Op = typename std::conditional<W4, BF16, T>::type;  // MFMA operand type
+    using M = DecMfma<Op>;
+    using S = typename T::storage;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, c = lane & 15;  // MFMA lane group / row-col index
@@ -517,8 +248,8 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     __shared__ float s_m[5][G], s_l[5][G];                                // [4]: the new token
 
     const size_t page_elems = (size_t)P * D;
-    const uint16_t *kpool = (const uint16_t *)a.kpool;
-    const uint16_t *vpool = (const uint16_t *)a.vpool;
+    const S *kpool = (const S *)a.kpool;
+    const S *vpool = (const S *)a.vpool;
     const int half = a.rope_half, rdim = a.rope_dim;
 
     // ---- 1. page ids: the K/V addresses hang on them -----------------------
@@ -551,16 +282,32 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     //   half (wave & 1) of V chunk (4 (wave >> 1) + grp, 16 db + c).
     // Whole sub-tiles are loaded (pages are fully allocated); rows at or past
     // pos are masked out of the scores and zeroed in V before use.
-    uint4 ka[4], kn[4];
-    uint2 vb[8], vn[8];
-    auto load_sub = [&](int phys, uint4 *kk, uint2 *vv) {
-        const uint16_t *kp = kpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)wave * 2048 + lane * 8;
-        const uint16_t *vp = vpool + ((size_t)phys * Hkv + kvh) * page_elems + (size_t)(wave >> 1) * 4096 +
-                             (wave & 1) * 4 + (grp * D + c) * 8;
+    //   f32 pages (row-major K, V^T sub-tiles): the same operands as fp32,
+    //   two 16-byte K loads per ks and one 16-byte V load per db.
+    constexpr int KL = W4 ? 8 : 4;
+    using VL = typename std::conditional<W4, uint4, uint2>::type;
+    uint4 ka[KL], kn[KL];
+    VL vb[8], vn[8];
+    auto load_sub = [&](int phys, uint4 *kk, VL *vv) {
+        const size_t pb = ((size_t)phys * Hkv + kvh) * page_elems;
+        if constexpr (W4) {
+            const S *kp = kpool + pb + (size_t)(SUB * wave + c) * D + 8 * grp;
+            const S *vp = vpool + pb + (size_t)(wave * D + c) * SUB + 4 * grp;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + 512 * ks);
+            for (int ks = 0; ks < 4; ks++) {
+                kk[2 * ks] = *(const uint4 *)(kp + 32 * ks);
+                kk[2 * ks + 1] = *(const uint4 *)(kp + 32 * ks + 4);
+            }
 #pragma unroll
-        for (int db = 0; db < 8; db++) vv[db] = *(const uint2 *)(vp + 128 * db);
+            for (int db = 0; db < 8; db++) vv[db] = *(const VL *)(vp + 256 * db);
+        } else {
+            const S *kp = kpool + pb + (size_t)wave * 2048 + lane * 8;
+            const S *vp = vpool + pb + (size_t)(wave >> 1) * 4096 + (wave & 1) * 4 + (grp * D + c) * 8;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + 512 * ks);
+#pragma unroll
+            for (int db = 0; db < 8; db++) vv[db] = *(const VL *)(vp + 128 * db);
+        }
     };
     load_sub(phys0, ka, vb);
     if (MULTI) load_sub(phys1, kn, vn);  // two pages in flight
@@ -572,7 +319,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
         qin.finish(0, y, lane, half, rdim, a.qnw != nullptr, a.eps, a.qscale);
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            const uint32_t pr = split_pair<T>(y[e]);
+            const uint32_t pr = split_pair<Op>(y[e]);
             s_qop[0][wave][lane + 64 * e] = (uint16_t)pr;
             s_qop[1][wave][lane + 64 * e] = (uint16_t)(pr >> 16);
             s_qf[wave][lane + 64 * e] = y[e];
@@ -591,7 +338,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     // in the softmax's base-2 units: m = max(s, floor), l = exp2(max(s-m, floor)).
     // Its cache stores are issued at the end: vmcnt retires in order, so
     // stores issued here would hold up every later wait on the K/V stream.
-    uint16_t knew_st[2] = {0, 0}, vnew_st[2] = {0, 0};
+    S knew_st[2] = {}, vnew_st[2] = {};
     if (extra) {
         float ky[2];
         kin.finish(0, ky, lane, half, rdim, a.knw != nullptr, a.eps, 1.0f);
@@ -628,7 +375,16 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
             // scores: lane (grp, c<4) <- head c, positions 4*grp + i
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) sacc = M::qk(ka[ks], qb[ks], sacc);
+            for (int ks = 0; ks < 4; ks++) {
+                if constexpr (W4) {
+                    uint4 hi, lo;
+                    split8(ka[2 * ks], ka[2 * ks + 1], hi, lo);
+                    sacc = M::qk(hi, qb[ks], sacc);
+                    sacc = M::qk(lo, qb[ks], sacc);
+                } else {
+                    sacc = M::qk(ka[ks], qb[ks], sacc);
+                }
+            }
             float sc[4], mt = kFloor2;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -648,7 +404,7 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
             uint32_t hp[2], lp[2];
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const uint32_t p0 = split_pair<T>(p[2 * e]), p1 = split_pair<T>(p[2 * e + 1]);
+                const uint32_t p0 = split_pair<Op>(p[2 * e]), p1 = split_pair<Op>(p[2 * e + 1]);
                 hp[e] = (p0 & 0xFFFFu) | (p1 << 16);
                 lp[e] = dpp_from_minus4((p0 >> 16) | (p1 & 0xFFFF0000u));
             }
@@ -675,13 +431,23 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
                 for (int j = 0; j < 4; j++)
                     if (4 * grp + j >= nv) keep[j >> 1] &= ~(0xFFFFu << (16 * (j & 1)));
             }
+            if constexpr (W4) {
 #pragma unroll
-            for (int db = 0; db < 8; db++)
-                acc[db] = M::pv(pa, make_uint2(vb[db].x & keep[0], vb[db].y & keep[1]), acc[db]);
+                for (int db = 0; db < 8; db++) {
+                    uint2 hi, lo;
+                    split4(vb[db], keep, hi, lo);
+                    acc[db] = M::pv(pa, hi, acc[db]);
+                    acc[db] = M::pv(pa, lo, acc[db]);
+                }
+            } else {
+#pragma unroll
+                for (int db = 0; db < 8; db++)
+                    acc[db] = M::pv(pa, make_uint2(vb[db].x & keep[0], vb[db].y & keep[1]), acc[db]);
+            }
         }
         if (MULTI) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) ka[ks] = kn[ks];
+            for (int ks = 0; ks < KL; ks++) ka[ks] = kn[ks];
 #pragma unroll
             for (int db = 0; db < 8; db++) vb[db] = vn[db];
             load_sub(page_id(min(page + 2, plast)), kn, vn);
@@ -742,12 +508,12 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     // ---- 8. append the new row to the cache ---------------------------------
     if (extra) {
         const int phys = page_id(newpos / P), t = newpos % P;
-        uint16_t *kp = (uint16_t *)kpool + ((size_t)phys * Hkv + kvh) * page_elems;
-        uint16_t *vp = (uint16_t *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
+        S *kp = (S *)kpool + ((size_t)phys * Hkv + kvh) * page_elems;
+        S *vp = (S *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            kp[k_off16(t, lane + 64 * e)] = knew_st[e];
-            vp[v_off16(t, lane + 64 * e)] = vnew_st[e];
+            kp[k_off<sizeof(S)>(t, lane + 64 * e)] = knew_st[e];
+            vp[v_off<sizeof(S)>(t, lane + 64 * e)] = vnew_st[e];
         }
     }
 }
@@ -831,26 +597,22 @@ template <typename T> DecodeKernel pick_mfma(bool multi, bool args, bool full) {
 
 hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     DecodeArgs a = args;
-    // Work split.  VALU kernel (f32 cache): pages of all L positions.  MFMA
-    // kernels: pages of the cached positions [0, L-1), the new token riding
+    // Work split: pages of the cached positions [0, L-1), the new token riding
     // with the last split.  One page per split until the split count reaches
     // kMaxSplits (the merge width).
-    const int pages = kv_dtype == 0 ? (a.L + kPage - 1) / kPage : (a.L - 1 + kPage - 1) / kPage;
+    const int pages = (a.L - 1 + kPage - 1) / kPage;
     a.ppw = std::max(1, (pages + kMaxSplits - 1) / kMaxSplits);
     a.nsplit = std::max(1, (pages + a.ppw - 1) / a.ppw);
-    dim3 grid(a.nsplit * a.kv_heads), block(256);
+    dim3 grid(a.nsplit, a.kv_heads), block(256);
     const bool multi = a.ppw > 1, in_args = a.pages_in_args != 0;
     const bool full = a.rope_dim == kHeadDim;
     DecodeKernel k;
     switch (kv_dtype) {
-    case 0: k = multi ? decode_attn_kernel<F32, true> : decode_attn_kernel<F32, false>; break;
+    case 0: k = pick_mfma<F32>(multi, in_args, full); break;
     case 1: k = pick_mfma<F16>(multi, in_args, full); break;
     case 2: k = pick_mfma<BF16>(multi, in_args, full); break;
     default: return hipErrorInvalidValue;
     }
-    // the VALU kernel indexes (split, kv head) linearly, the MFMA kernels by
-    // a 2D grid
-    if (kv_dtype != 0) grid = dim3(a.nsplit, a.kv_heads);
     hipLaunchKernelGGL(k, grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
