@@ -243,6 +243,51 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
             "tokens_per_s": seq / (ms * 1e-3)}
 
 
+def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
+    """The device block store at the config-2 shape (32 layers, fp16 KV): host
+    time of HarvestPrefix and RestorePrefix over a ctx-token prompt (ctx / 64
+    blocks), and the GPU time of one copy-on-write (a write inside a harvested
+    block: every layer's K and V page copied, then the table entry updated),
+    from HIP events around `reps` of them."""
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, ctx + 64, F16)
+    toks = (np.arange(ctx, dtype=np.int32) * 7919) % 120000
+    be.MapRange(0, ctx)
+    be.sync()
+    t = time.perf_counter()
+    for _ in range(reps):
+        be.HarvestPrefix(toks, 64)
+    harvest = (time.perf_counter() - t) / reps
+    be.SetCacheLen(0)
+    t = time.perf_counter()
+    for _ in range(reps):
+        be.RestorePrefix(toks, 64)
+    restore = (time.perf_counter() - t) / reps
+    be.SetCacheLen(ctx)
+    ev = HipEvents(be.stream())
+    pos = ctx - 64 + 5  # inside the last harvested block
+    be.MapRange(pos, 1)  # warm-up copy
+    e0, e1 = ev.new(), ev.new()
+    gpu_ms = 0.0
+    for _ in range(reps):
+        be.SetCacheLen(pos)
+        be.RestorePrefix(toks, 64)  # back onto the harvested page
+        be.sync()
+        ev.record(e0)
+        be.MapRange(pos, 1)  # copy-on-write
+        ev.record(e1)
+        gpu_ms += ev.elapsed_ms(e0, e1)
+    ev.destroy(e0)
+    ev.destroy(e1)
+    be.Dispose()
+    page_bytes = HKV * 64 * D * 2
+    moved = 2 * layers * page_bytes * 2  # K and V pages of every layer, read + written
+    cow_us = gpu_ms * 1e3 / reps
+    return {"workload": f"{layers} layers, fp16 KV, {ctx}-token prompt ({ctx // 64} blocks)",
+            "harvest_us": round(harvest * 1e6, 2), "restore_us": round(restore * 1e6, 2),
+            "cow_us": round(cow_us, 3), "cow_bytes": moved, "cow_gbs": round(moved / (cow_us * 1e-6) / 1e9, 1),
+            "cow_note": "GPU time of one copy-on-write: the page-copy kernel and the table update"}
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -383,6 +428,7 @@ def main():
                                "bytes": r["bytes_per_layer"]}
         extra["config5"] = {"workload": "decode context sweep, fp16 KV, one layer per call",
                             "unit": "GB/s", "by_context": sweep}
+        extra["block_store"] = time_block_store()
 
     cpu = None
     if not args.no_cpu and dec is not None:

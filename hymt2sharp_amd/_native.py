@@ -77,6 +77,9 @@ SIGNATURES = {
     "hymt_kv_map": [_vp, _i, _i],
     "hymt_kv_page": [_vp, _i, ctypes.POINTER(_i)],
     "hymt_kv_set_len": [_vp, _i],
+    "hymt_kv_harvest": [_vp, _vp, _i, _i],
+    "hymt_kv_restore": [_vp, _vp, _i, _i, ctypes.POINTER(_i)],
+    "hymt_kv_store_info": [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i)],
     "hymt_kv_upload": [_vp, _i, _i, _i, _vp, _vp],
     "hymt_kv_read": [_vp, _i, _i, _i, _vp, _vp],
     "hymt_attn_decode": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint],

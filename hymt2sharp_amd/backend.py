@@ -3,7 +3,8 @@ path, over the C ABI of libhymt_hip.so.
 
 HipBackend follows IComputeBackend (Backends/IComputeBackend.cs:14-88) for
 the members this path owns -- Name, SupportsPrefill, UploadKv, SetCacheLen,
-Dispose -- and adds the per-layer attention unit the reference runs inside
+the device block store (SupportsBlockStore, DeviceBlockTokens, HarvestPrefix,
+RestorePrefix), Dispose -- and adds the per-layer attention unit the reference runs inside
 ForwardStep (DecodeAttention / PrefillAttention, HunyuanDenseModel.Decode.cs:64-101,
 HunyuanDenseModel.Prefill.cs:38-89).  create_backend mirrors
 BackendFactory.Create (Backends/BackendFactory.cs:15-44) with the "hip" name
@@ -34,7 +35,7 @@ class HipBackend:
 
     Name = "hip"
     SupportsPrefill = True
-    SupportsBlockStore = False
+    SupportsBlockStore = True
     DeviceBlockTokens = N.PAGE_TOKENS
 
     def __init__(self, device: int = 0):
@@ -89,6 +90,25 @@ class HipBackend:
     def SetCacheLen(self, length: int):
         """IComputeBackend.SetCacheLen (IComputeBackend.cs:82-87)."""
         N.check(self._lib.hymt_kv_set_len(self._h, length))
+
+    def HarvestPrefix(self, tokens, block_tokens: int):
+        """IComputeBackend.HarvestPrefix (IComputeBackend.cs:49-87; Metal's,
+        MetalBackend.cs:330-356): pin every full mapped block of `tokens`."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        N.check(self._lib.hymt_kv_harvest(self._h, _ptr(t), t.size, block_tokens))
+
+    def RestorePrefix(self, tokens, block_tokens: int) -> int:
+        """IComputeBackend.RestorePrefix (MetalBackend.cs:358-382): map the
+        longest stored run of full blocks of `tokens`; tokens restored."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        n = ctypes.c_int()
+        N.check(self._lib.hymt_kv_restore(self._h, _ptr(t), t.size, block_tokens, ctypes.byref(n)))
+        return n.value
+
+    def store_info(self):
+        e, f = ctypes.c_int(), ctypes.c_int()
+        N.check(self._lib.hymt_kv_store_info(self._h, ctypes.byref(e), ctypes.byref(f)))
+        return {"entries": e.value, "pages_free": f.value}
 
     def MapRange(self, pos: int, length: int):
         N.check(self._lib.hymt_kv_map(self._h, pos, length))

@@ -141,6 +141,8 @@ hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s);
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s);
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s);
 hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n, hipStream_t s);
+hipError_t launch_kv_copy_page(void *kpool, void *vpool, size_t layer_bytes, size_t page_bytes, int src,
+                               int dst, int layers, hipStream_t s);
 hipError_t launch_kv_upload(int kv_dtype, const uint16_t *k_bf16, const uint16_t *v_bf16,
                             const int32_t *tab, void *kpool, void *vpool, int pos, int len,
                             int kv_heads, hipStream_t s);

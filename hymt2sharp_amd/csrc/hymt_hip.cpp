@@ -143,6 +143,21 @@ void flush_table(hymt_ctx *c) {
     HIP_TRY(launch_tab_update((int32_t *)c->tab.p, idx.data(), val.data(), (int)idx.size(), c->stream));
 }
 
+// Map [pos, pos+len) for writing: pages for unmapped blocks, fresh pages for
+// blocks pinned by the block store, whose leading rows are copied over first
+// (MetalBackend.cs ExecCopies, :320-332), then the table mirror.
+void map_write(hymt_ctx *c, int pos, int len) {
+    c->pages.ensure_written(pos, len);
+    const std::vector<KvPages::Copy> copies = c->pages.take_copies();
+    if (!c->has_device()) return;
+    const size_t page_bytes = (size_t)c->kv_heads * kPage * c->head_dim * dtype_bytes(c->kv_dtype);
+    const size_t layer_bytes = c->layer_elems * dtype_bytes(c->kv_dtype);
+    for (const KvPages::Copy &x : copies)
+        HIP_TRY(launch_kv_copy_page(c->kpool.p, c->vpool.p, layer_bytes, page_bytes, x.src, x.dst,
+                                    c->layers, c->stream));
+    flush_table(c);
+}
+
 // Ops.EnsureRopeTable (Ops.cs:170-195): capacity max(needed, 4096), grown by
 // doubling; freq_i = 1 / base^(i/half), angle = pos * freq in fp32.
 void ensure_rope(hymt_ctx *c, int needed) {
@@ -355,12 +370,10 @@ int hymt_kv_info(hymt_ctx *c, int *max_tokens, int *pages_total, int *pages_mapp
 int hymt_kv_map(hymt_ctx *c, int pos, int len) {
     if (int r = check_ctx(c, true, false)) return r;
     if (pos < 0 || len < 0) return fail(HYMT_E_ARG, "invalid range");
+    if (c->capturing && c->pages.needs_copy(pos, len)) return fail_capture(c, "a write into a harvested block");
     try {
-        c->pages.ensure_written(pos, len);
-        if (c->has_device()) {
-            HIP_TRY(hipSetDevice(c->device));
-            flush_table(c);
-        }
+        if (c->has_device()) HIP_TRY(hipSetDevice(c->device));
+        map_write(c, pos, len);
     } catch (const CapacityError &e) {
         return fail(HYMT_E_CAPACITY, e.what());
     } catch (const HipError &e) {
@@ -383,6 +396,45 @@ int hymt_kv_set_len(hymt_ctx *c, int len) {
     return HYMT_OK;
 }
 
+int hymt_kv_harvest(hymt_ctx *c, const int32_t *tokens, int n_tokens, int block_tokens) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (n_tokens < 0 || (n_tokens > 0 && !tokens)) return fail(HYMT_E_ARG, "invalid token list");
+    if (int r = refuse_in_capture(c, "hymt_kv_harvest")) return r;
+    try {
+        c->pages.harvest(tokens, n_tokens, block_tokens);
+    } catch (const BlockSizeError &e) {
+        return fail(HYMT_E_UNSUPPORTED, e.what());
+    }
+    return HYMT_OK;
+}
+
+int hymt_kv_restore(hymt_ctx *c, const int32_t *tokens, int n_tokens, int block_tokens,
+                    int *restored_tokens) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (!restored_tokens || n_tokens < 0 || (n_tokens > 0 && !tokens))
+        return fail(HYMT_E_ARG, "invalid token list");
+    if (int r = refuse_in_capture(c, "hymt_kv_restore")) return r;
+    try {
+        *restored_tokens = c->pages.restore(tokens, n_tokens, block_tokens);
+        if (c->has_device()) {
+            HIP_TRY(hipSetDevice(c->device));
+            flush_table(c);
+        }
+    } catch (const BlockSizeError &e) {
+        return fail(HYMT_E_UNSUPPORTED, e.what());
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_kv_store_info(hymt_ctx *c, int *entries, int *pages_free) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (entries) *entries = c->pages.store_entries();
+    if (pages_free) *pages_free = c->pages.pages_free();
+    return HYMT_OK;
+}
+
 int hymt_kv_upload(hymt_ctx *c, int layer, int pos, int len, const uint16_t *k_bf16,
                    const uint16_t *v_bf16) {
     if (int r = check_ctx(c, true, false)) return r;
@@ -396,8 +448,7 @@ int hymt_kv_upload(hymt_ctx *c, int layer, int pos, int len, const uint16_t *k_b
     if (int r = refuse_in_capture(c, "hymt_kv_upload")) return r;
     try {
         HIP_TRY(hipSetDevice(c->device));
-        c->pages.ensure_written(pos, len);
-        flush_table(c);
+        map_write(c, pos, len);
         const size_t stride = (size_t)c->kv_heads * c->head_dim;
         const size_t bytes = (size_t)len * stride * 2;
         stage_in(c, {{k_bf16 + (size_t)pos * stride, bytes, &c->up_k},
@@ -453,10 +504,10 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer decode")) return r;
     if (c->capturing && pos + 1 > c->rope_cap) return fail_capture(c, "RoPE table growth");
+    if (c->capturing && c->pages.needs_copy(pos, 1)) return fail_capture(c, "a write into a harvested block");
     try {
         HIP_TRY(hipSetDevice(c->device));
-        c->pages.ensure_written(pos, 1);
-        flush_table(c);
+        map_write(c, pos, 1);
         ensure_rope(c, pos + 1);
         const size_t D = c->head_dim, qn = (size_t)c->heads * D, kn = (size_t)c->kv_heads * D;
         if (!dev) {
@@ -521,10 +572,10 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer prefill")) return r;
     if (c->capturing && pos + seq > c->rope_cap) return fail_capture(c, "RoPE table growth");
+    if (c->capturing && c->pages.needs_copy(pos, seq)) return fail_capture(c, "a write into a harvested block");
     try {
         HIP_TRY(hipSetDevice(c->device));
-        c->pages.ensure_written(pos, seq);
-        flush_table(c);
+        map_write(c, pos, seq);
         ensure_rope(c, pos + seq);
         const size_t D = c->head_dim, es = dtype_bytes(io_dtype);
         const size_t qn = (size_t)seq * c->heads * D, kn = (size_t)seq * c->kv_heads * D;

@@ -1,5 +1,7 @@
 // kv_ops.hip -- page-table mirroring and bulk K/V row transfers for the
 // paged cache (layout in attn_kernels.hpp).
+#include <algorithm>
+
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
 
@@ -31,6 +33,30 @@ hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// Copy-on-write of one page for the block store (MetalBackend.cs
+// ExecCopies, :320-332, its kv_copy_block kernel): page src -> page dst in
+// every layer's K and V pool.  A page of all kv heads is one contiguous
+// block of page_bytes, copied as 16-byte vectors; grid.y = (layer, K/V).
+__global__ __launch_bounds__(256) void kv_copy_page_kernel(uint4 *kpool, uint4 *vpool, size_t layer_vec,
+                                                           size_t page_vec, int src, int dst) {
+    uint4 *pool = (blockIdx.y & 1) ? vpool : kpool;
+    const size_t base = (size_t)(blockIdx.y >> 1) * layer_vec;
+    const uint4 *from = pool + base + (size_t)src * page_vec;
+    uint4 *to = pool + base + (size_t)dst * page_vec;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < page_vec; i += (size_t)gridDim.x * blockDim.x)
+        to[i] = from[i];
+}
+
+hipError_t launch_kv_copy_page(void *kpool, void *vpool, size_t layer_bytes, size_t page_bytes, int src,
+                               int dst, int layers, hipStream_t s) {
+    if (src == dst || layers <= 0) return hipSuccess;
+    const size_t page_vec = page_bytes / 16;
+    const int bx = (int)std::min<size_t>((page_vec + 255) / 256, 64);
+    hipLaunchKernelGGL(kv_copy_page_kernel, dim3(bx, 2 * layers), dim3(256), 0, s, (uint4 *)kpool,
+                       (uint4 *)vpool, layer_bytes / 16, page_vec, src, dst);
+    return hipGetLastError();
 }
 
 // IComputeBackend.UploadKv (IComputeBackend.cs:31-38): rows [pos, pos+len)

@@ -106,9 +106,37 @@ int hymt_kv_map(hymt_ctx *ctx, int pos, int len);
  * the page table (MetalBackend.cs:55 `_tab`). */
 int hymt_kv_page(hymt_ctx *ctx, int block, int *phys);
 
-/* Live cache length: pages that start at or after `len` return to the free
- * list.  Replaces IComputeBackend.SetCacheLen (IComputeBackend.cs:82-87). */
+/* Live cache length: blocks that start at or after `len` are unmapped and
+ * their pages return to the free list unless the block store pins them.
+ * Replaces IComputeBackend.SetCacheLen (IComputeBackend.cs:82-87). */
 int hymt_kv_set_len(hymt_ctx *ctx, int len);
+
+/*
+ * Device block store (IComputeBackend.SupportsBlockStore = true,
+ * DeviceBlockTokens = HYMT_PAGE_TOKENS; IComputeBackend.cs:49-87), after the
+ * Metal backend's (MetalBackend.cs:224-387).  A full 64-token block of a
+ * sequence is keyed by the chained FNV-1a hash of all tokens up to its end
+ * (KvBlockStore.ChainHash, KvBlockStore.cs:51-60) and the key's tokens are
+ * kept, so a hash collision is a miss.  Pinned pages are never written: a
+ * later write into their block (decode, prefill, upload, hymt_kv_map) maps a
+ * fresh page and first copies the pinned page into it in every layer when
+ * the write starts inside the block.  When the pool runs out, entries are
+ * evicted least recently harvested first, never while their page is mapped
+ * in the live range.
+ *
+ * hymt_kv_harvest replaces HarvestPrefix: pins the page of every full block
+ * of tokens[0, n_tokens) that is mapped.  hymt_kv_restore replaces
+ * RestorePrefix: maps the longest run of full blocks of tokens[0, n_tokens)
+ * found in the store, from block 0, and sets *restored_tokens to the number
+ * of tokens restored (a multiple of 64); the caller then sets the cache
+ * length (hymt_kv_set_len).  block_tokens other than 64 -> HYMT_E_UNSUPPORTED.
+ * Neither may run while a recording is open.
+ */
+int hymt_kv_harvest(hymt_ctx *ctx, const int32_t *tokens, int n_tokens, int block_tokens);
+int hymt_kv_restore(hymt_ctx *ctx, const int32_t *tokens, int n_tokens, int block_tokens,
+                    int *restored_tokens);
+/* Store entries and pages held by neither the table nor the store. */
+int hymt_kv_store_info(hymt_ctx *ctx, int *entries, int *pages_free);
 
 /* Copy rows [pos, pos+len) of one layer from the model's flat bf16 caches
  * (row j at k_bf16 + j*kv_stride) into the device cache, converting to the
