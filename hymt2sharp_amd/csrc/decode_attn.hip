@@ -13,8 +13,9 @@
 //   workgroup = (split, kv head), 4 waves, `ppw` 64-position pages per split
 //   (one page per split until the split count reaches kMaxSplits, so a
 //   4k-context layer spreads over 256 workgroups, every CU).
-//   Wave w owns positions [16w, 16w+16) of every page of its split.  A wave's
-//   16 K rows and its 16x128 V^T sub-tile are each one contiguous 4 KiB block.
+//   Wave w owns 16 positions of every page of its split: those of V chunks 2w
+//   and 2w+1 (f16/bf16 pages) or the sub-tile [16w, 16w+16) (f32 pages), so
+//   that its K and V operand loads are whole 128-byte segments.
 //   The kernel is latency-bound at decode sizes, so the prologue is ordered
 //   for the shortest dependent chain: page ids (scalar loads) first, then the
 //   q rows, then the K/V stream; no workgroup barrier before the final
@@ -276,10 +277,13 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     const float vnew1 = a.vnew[(size_t)kvh * D + lane + 64];
 
     // ---- 3. the K/V stream --------------------------------------------------
-    // K A-operand: lane (grp, c) = K row c, dims 32*ks + 8*grp + [0, 8): chunk
-    //   (wave, 4 ks + grp, c) of the page, one linear 1 KiB load per ks.
-    // V B-operand: lane (grp, c) = V^T row 16*db + c, positions 4*grp + [0, 4):
-    //   half (wave & 1) of V chunk (4 (wave >> 1) + grp, 16 db + c).
+    // f16/bf16 pages: wave w takes the 16 positions of V chunks 2w and 2w+1,
+    // so that its V loads are whole 16-byte chunks; S row / P.V index
+    // 4 grp + i of the wave is page position posw(i) below.
+    // K A-operand: lane (grp, c) = K row c (position posw of index c), dims
+    //   32*ks + 8*grp + [0, 8): two 128-byte segments per 16 lanes.
+    // V B-operand: lane (grp, c) = V^T row 16*db + c, indices 4*grp + [0, 4):
+    //   half (grp & 1) of V chunk (2 w + (grp >> 1), 16 db + c).
     // Whole sub-tiles are loaded (pages are fully allocated); rows at or past
     // pos are masked out of the scores and zeroed in V before use.
     //   f32 pages (row-major K, V^T sub-tiles): the same operands as fp32,
@@ -301,8 +305,9 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 #pragma unroll
             for (int db = 0; db < 8; db++) vv[db] = *(const VL *)(vp + 256 * db);
         } else {
-            const S *kp = kpool + pb + (size_t)wave * 2048 + lane * 8;
-            const S *vp = vpool + pb + (size_t)(wave >> 1) * 4096 + (wave & 1) * 4 + (grp * D + c) * 8;
+            const S *kp = kpool + pb + 2048 * (2 * (wave >> 1) + ((c >> 2) & 1)) + 128 * grp +
+                          8 * (8 * (wave & 1) + 4 * (c >> 3) + (c & 3));
+            const S *vp = vpool + pb + (size_t)(2 * wave + (grp >> 1)) * 1024 + 8 * c + 4 * (grp & 1);
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + 512 * ks);
 #pragma unroll
@@ -363,15 +368,21 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     }
 
     // ---- 6. attention over the split's cached sub-tiles ---------------------
+    // page position of S row / P.V index 4 grp + i of this wave, and the
+    // smallest one (f32 pages: the sub-tile [16 w, 16 w + 16))
+    auto posw = [&](int i) {
+        return W4 ? SUB * wave + 4 * grp + i
+                  : 32 * (wave >> 1) + 8 * (wave & 1) + 4 * (grp >> 1) + 16 * (grp & 1) + i;
+    };
+    const int pmin = W4 ? SUB * wave : 32 * (wave >> 1) + 8 * (wave & 1);
     f32x4 acc[8];
 #pragma unroll
     for (int db = 0; db < 8; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = kFloor2, l_run = 0.0f;  // lanes c < 4: head c
 
     for (int page = page0; page < page_end; page++) {
-        const int base = page * P + SUB * wave;
-        const int nv = newpos - base;  // valid rows of this sub-tile (>= 16: all)
-        if (nv > 0) {
+        const int nv = newpos - page * P;  // positions of this page below pos
+        if (nv > pmin) {
             // scores: lane (grp, c<4) <- head c, positions 4*grp + i
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -389,14 +400,14 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 sc[i] = sacc[i] + dpp_from_plus4(sacc[i]);
-                if (4 * grp + i < nv) mt = fmaxf(mt, sc[i]);
+                if (posw(i) < nv) mt = fmaxf(mt, sc[i]);
             }
             mt = xrow32_max(xrow16_max(mt));
             const float mnew = fmaxf(m_run, mt);
             float p[4], ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[i] = 4 * grp + i < nv ? exp2f(fmaxf(sc[i] - mnew, kFloor2)) : 0.0f;
+                p[i] = posw(i) < nv ? exp2f(fmaxf(sc[i] - mnew, kFloor2)) : 0.0f;
                 ps += p[i];
             }
             ps = xrow32_sum(xrow16_sum(ps));
@@ -426,10 +437,10 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
             // V: zero the positions at or past pos (halfword masks of this
             // lane's 4 positions); they may hold stale data
             uint32_t keep[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
-            if (nv < SUB) {
+            if (nv < P) {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
-                    if (4 * grp + j >= nv) keep[j >> 1] &= ~(0xFFFFu << (16 * (j & 1)));
+                    if (posw(j) >= nv) keep[j >> 1] &= ~(0xFFFFu << (16 * (j & 1)));
             }
             if constexpr (W4) {
 #pragma unroll
