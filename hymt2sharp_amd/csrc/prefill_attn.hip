@@ -209,6 +209,17 @@ struct FlashItem {
 
 __device__ inline FlashItem flash_item(const FlashArgs &a, int item) {
     FlashItem it;
+    if (flash_splits(pair_tiles(a.pos0, 0, a.nb16, a.seq), a.cap) == 1) {
+        // pair 0 is the longest: when it is not split no pair is, and item i
+        // is pair i
+        it.pair = item < a.npairs ? item : -1;
+        it.split = 0;
+        it.nsplit = 1;
+        it.t0 = 0;
+        it.t1 = item < a.npairs ? pair_tiles(a.pos0, item, a.nb16, a.seq) : 0;
+        it.first = item;
+        return it;
+    }
     int first = 0;
     for (int pr = 0; pr < a.npairs; pr++) {
         const int nt = pair_tiles(a.pos0, pr, a.nb16, a.seq);
