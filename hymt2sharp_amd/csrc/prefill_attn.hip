@@ -436,6 +436,24 @@ __device__ __forceinline__ void q_finish(const FlashArgs &a, const QRaw<IN_BF16>
     }
 }
 
+// Instruction order of a 16-read, 16 * (2 - QQ0)-MFMA product (S or P.V of
+// one tile): DEPTH LDS reads ahead, then one read after the MFMAs of each
+// operand, so that DEPTH reads stay in flight.  Left to itself the scheduler
+// keeps one or two reads ahead and each MFMA waits out the LDS latency;
+// measured at 2048 tokens, 8 ahead with one MFMA per read (the long block
+// alone) and 6 ahead with two (both blocks) are fastest.
+template <int QQ0> __device__ __forceinline__ void lds_pipeline() {
+    constexpr int DEPTH = QQ0 ? 8 : 6, MPR = 2 - QQ0;
+    // masks: 0x100 LDS read, 0x008 MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, DEPTH, 0);
+#pragma unroll
+    for (int i = 0; i < 16 - DEPTH; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, MPR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, MPR * DEPTH, 0);
+}
+
 // Lazy running maximum: a row's reference m moves only when a tile holds a
 // score above m + kLazy (log2 units).  Weights p = 2^(s - m) then stay below
 // 2^kLazy and most tiles skip the rescale of O and l entirely.
@@ -582,6 +600,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
                 for (int qq = QQ0; qq < 2; qq++) sacc[kb][qq] = Mfma<T>::mma(kf, qf[qq][ks], sacc[kb][qq]);
             }
         }
+        lds_pipeline<QQ0>();
 
         if (nphys >= 0) fetch_page(nphys, buf ^ 1, 0);
 
@@ -662,9 +681,15 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
                 for (int qq = QQ0; qq < 2; qq++) o[db][qq] = Mfma<T>::mma(vf, pf[qq], o[db][qq]);
             }
         }
+        lds_pipeline<QQ0>();
     };
 
-    for (int j = 0; 2 * j < nt; j++) {
+    // Tile pairs j < jA hold a tile of both blocks on parity 0 at least; from
+    // jA on the long block runs alone, in a loop of its own where the short
+    // block's q rows and scores are dead.
+    const int jA = min(max(0, lenA - it.t0 + 1) >> 1, (nt + 1) >> 1);
+    int j = 0;
+    for (; j < jA; j++) {
         const int buf = j & 1;
         const int t = it.t0 + 2 * j + half;  // this wave's tile
         // tile t + 2 goes into the other buffer, which every wave finished
@@ -675,6 +700,14 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
             else tile_body(std::integral_constant<int, 1>{}, t, j, buf, nphys);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
+        __syncthreads();
+    }
+    for (; 2 * j < nt; j++) {
+        const int buf = j & 1;
+        const int t = it.t0 + 2 * j + half;
+        const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
+        if (t < it.t1) tile_body(std::integral_constant<int, 1>{}, t, j, buf, nphys);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
