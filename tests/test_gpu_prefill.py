@@ -63,6 +63,7 @@ def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, wi
                                       S.f32_to_bf16_bits(v), qnw, knw, io_dtype=BF16)
         else:
             got = be.PrefillAttention(0, pos, q, k, v, qnw, knw)
+        be.sync()
         kd, vd = be.ReadKv(0, pos, seq)
     finally:
         be.Dispose()
@@ -140,3 +141,28 @@ def test_chunked_equals_monolithic(hip_available):
         be.Dispose()
     check(np.concatenate(parts), mono, v0, BF16)
     assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+
+
+def test_back_to_back_launches_on_one_context(hip_available):
+    """Many prefills of different shapes in a row on one context leave no
+    state behind that changes a later call: the last equals the same call on
+    a fresh context holding the same cache rows, bit for bit."""
+    shapes = [(0, 1), (0, 300), (37, 29), (0, 2048), (64, 64), (5, 1), (1000, 100)] * 2
+    cap = 2048 + 64
+    be = make_backend(1, cap, BF16)
+    try:
+        for i, (pos, seq) in enumerate(shapes):
+            q, k, v, qnw, knw = new_token(14, i, "gamma", seq=seq)
+            got = be.PrefillAttention(0, pos, q, k, v, qnw, knw)
+        be.sync()
+        kc, vc = be.ReadKv(0, 0, 1000)
+    finally:
+        be.Dispose()
+    fresh = make_backend(1, cap, BF16)
+    try:
+        fresh.UploadKv(0, 0, 1000, S.f32_to_bf16_bits(kc), S.f32_to_bf16_bits(vc))
+        again = fresh.PrefillAttention(0, 1000, q, k, v, qnw, knw)
+        fresh.sync()
+    finally:
+        fresh.Dispose()
+    assert np.array_equal(got, again)
