@@ -93,7 +93,16 @@ SIGNATURES = {
     "hymt_graph_end": [_vp, ctypes.POINTER(_vp)],
     "hymt_graph_launch": [_vp, _vp],
     "hymt_graph_destroy": [_vp, _vp],
+    "hymt_weight_upload": [_vp, _i, _i, _i, _vp, ctypes.c_size_t, ctypes.POINTER(_vp)],
+    "hymt_weight_free": [_vp, _vp],
+    "hymt_weight_info": [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                         ctypes.POINTER(ctypes.c_size_t)],
+    "hymt_gemv": [_vp, _vp, _vp, _vp, _i],
 }
+
+# weight types (GgmlTensorType codes) and gemv flags, as in include/hymt_hip.h
+W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
+GEMV_ACCUMULATE = 1
 
 _lib = None
 _synth = None

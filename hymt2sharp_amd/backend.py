@@ -175,6 +175,29 @@ class HipBackend:
     def sync(self):
         N.check(self._lib.hymt_sync(self._h))
 
+    # ---- quantized weights (the weight half of LoadModel, IComputeBackend.cs:25-29)
+    def weight_upload(self, wtype: int, rows: int, cols: int, data) -> int:
+        """Upload a rows x cols matrix given as rows of GGUF blocks; returns a
+        handle for gemv / weight_free."""
+        raw = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+        h = ctypes.c_void_p()
+        N.check(self._lib.hymt_weight_upload(self._h, wtype, rows, cols, _ptr(raw), raw.nbytes,
+                                             ctypes.byref(h)))
+        return h.value
+
+    def weight_free(self, w):
+        N.check(self._lib.hymt_weight_free(self._h, w))
+
+    def weight_info(self, w) -> dict:
+        t, r, c, b = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+        N.check(self._lib.hymt_weight_info(w, ctypes.byref(t), ctypes.byref(r), ctypes.byref(c),
+                                           ctypes.byref(b)))
+        return {"type": t.value, "rows": r.value, "cols": c.value, "device_bytes": b.value}
+
+    def gemv(self, w, x_dev, y_dev, accumulate: bool = False):
+        """y (+)= W x on device vectors (enqueued on the context's stream)."""
+        N.check(self._lib.hymt_gemv(self._h, w, x_dev, y_dev, N.GEMV_ACCUMULATE if accumulate else 0))
+
     def stream(self) -> int:
         s = ctypes.c_void_p()
         N.check(self._lib.hymt_get_stream(self._h, ctypes.byref(s)))

@@ -23,6 +23,8 @@ HIP_SOURCES = {
     "decode_attn.hip": [],
     "prefill_attn.hip": [],
     "kv_ops.hip": [],
+    "gemv.hip": [],
+    "weights.cpp": [],
 }
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 BUILD_DIR = os.path.join(PKG, "_build")

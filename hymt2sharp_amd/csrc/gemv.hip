@@ -1,0 +1,364 @@
+// gemv.hip -- y (+)= W x for the reference's quantized weight formats, one
+// token (decode): the weight GEMVs of a decode step (HunyuanDenseModel.Decode.cs
+// DecodeQkv / DecodeLinear / DecodeGateUp; Vulkan dec_gemvadd_*.comp).
+//
+// Weights sit in HBM in the device layout of hymt_weight_upload (weights.cpp):
+// every format is cut into 32-value units whose bytes are 8- or 16-byte
+// aligned, so a lane reads its units with plain vector loads.  HBM-bound: a
+// decode GEMV moves 1-15 MB, so the kernel is as much about memory latency as
+// bandwidth: a lane issues the loads of all its units before it touches x.
+//
+// Work split: 256 threads (4 waves).  A wave takes RW consecutive rows; lane l
+// handles units t = l + 64 k (k < K, K = RW * UPR / 64, UPR = cols / 32
+// units per row, a multiple of 64), i.e. unit t % UPR of row t / UPR.  x is
+// staged in LDS with the sums of its 8-value runs (the formats' offset and
+// min terms need sums of x, not per-value products).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "weights.hpp"
+
+namespace hymt {
+namespace {
+
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
+
+// bytes 0..3 of w as floats
+__device__ __forceinline__ void bytes4(uint32_t w, float *o) {
+    // (v_cvt_f32_ubyte0..3)
+    o[0] = (float)(w & 0xFFu);
+    o[1] = (float)((w >> 8) & 0xFFu);
+    o[2] = (float)((w >> 16) & 0xFFu);
+    o[3] = (float)(w >> 24);
+}
+
+__device__ __forceinline__ float dot4(const float *a, float4 b, float acc) {
+    acc = fmaf(a[0], b.x, acc);
+    acc = fmaf(a[1], b.y, acc);
+    acc = fmaf(a[2], b.z, acc);
+    return fmaf(a[3], b.w, acc);
+}
+
+// ---- per-format units: load() issues the loads of unit u of row r, dot()
+// returns its contribution given x (LDS) and the 8-value sums xs (LDS) ----
+
+struct UnitF32 {
+    static constexpr int kMax = 4;  // units in flight per lane
+    uint4 v[8];
+    __device__ void load(const WeightDev &w, int r, int u) {
+        const uint4 *p = (const uint4 *)((const float *)w.q + (size_t)r * w.cols + 32 * u);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = p[i];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
+        const float4 *xv = (const float4 *)(x + 32 * u);
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float wv[4] = {__uint_as_float(v[i].x), __uint_as_float(v[i].y), __uint_as_float(v[i].z),
+                                 __uint_as_float(v[i].w)};
+            a = dot4(wv, xv[i], a);
+        }
+        return a;
+    }
+};
+
+struct UnitF16 {
+    static constexpr int kMax = 4;  // units in flight per lane
+    uint4 v[4];
+    __device__ void load(const WeightDev &w, int r, int u) {
+        const uint4 *p = (const uint4 *)((const uint16_t *)w.q + (size_t)r * w.cols + 32 * u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = p[i];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
+        const float4 *xv = (const float4 *)(x + 32 * u);
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t h[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+            const float w0[4] = {h2f(h[0] & 0xFFFF), h2f(h[0] >> 16), h2f(h[1] & 0xFFFF), h2f(h[1] >> 16)};
+            const float w1[4] = {h2f(h[2] & 0xFFFF), h2f(h[2] >> 16), h2f(h[3] & 0xFFFF), h2f(h[3] >> 16)};
+            a = dot4(w0, xv[2 * i], a);
+            a = dot4(w1, xv[2 * i + 1], a);
+        }
+        return a;
+    }
+};
+
+// Q8_0 (Q8_0.cs:16-35): q int8 [rows][cols], d fp32 [rows][cols/32]
+struct UnitQ8_0 {
+    static constexpr int kMax = 8;  // units in flight per lane
+    uint4 v[2];
+    float d;
+    __device__ void load(const WeightDev &w, int r, int u) {
+        const uint4 *p = (const uint4 *)((const int8_t *)w.q + (size_t)r * w.cols + 32 * u);
+        v[0] = p[0];
+        v[1] = p[1];
+        d = w.d[(size_t)r * (w.cols / 32) + u];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
+        const float4 *xv = (const float4 *)(x + 32 * u);
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t wd = i < 4 ? (&v[0].x)[i] : (&v[1].x)[i - 4];
+            const float q[4] = {(float)(int8_t)(wd & 0xFF), (float)(int8_t)((wd >> 8) & 0xFF),
+                                (float)(int8_t)((wd >> 16) & 0xFF), (float)(int8_t)(wd >> 24)};
+            a = dot4(q, xv[i], a);
+        }
+        return d * a;
+    }
+};
+
+// Q4_K (Q4K.cs:8-19, 36-61): 144-byte super-blocks as stored.  Unit u is
+// super-block u/8, sub = u%8 -> g = sub/2, h = sub%2: qs bytes
+// 32 g + 16 h + [0,16), their low nibbles at 64 g + 16 h + i (scale 2 g),
+// high nibbles at 64 g + 32 + 16 h + i (scale 2 g + 1).
+struct UnitQ4_K {
+    static constexpr int kMax = 8;  // units in flight per lane
+    uint4 hdr, qs;
+    __device__ void load(const WeightDev &w, int r, int u) {
+        const uint8_t *b = (const uint8_t *)w.q + ((size_t)r * (w.cols / 256) + u / 8) * 144;
+        hdr = *(const uint4 *)b;
+        qs = *(const uint4 *)(b + 16 + 16 * (u % 8));
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
+        const int g = (u % 8) / 2, h = u % 2;
+        const int base = 256 * (u / 8) + 64 * g + 16 * h;
+        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+        // scale bytes s[0..11] are hdr.y, hdr.z, hdr.w; byte k of a dword by
+        // shift (a run-time index into a register array would go to scratch)
+        auto byte = [](uint32_t w, int k) { return (int)((w >> (8 * k)) & 0xFFu); };
+        int sc[2], m[2];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int j = 2 * g + t;  // GetScaleMin (Q4K.cs:8-19)
+            if (j < 4) {
+                sc[t] = byte(hdr.y, j) & 63;
+                m[t] = byte(hdr.z, j) & 63;
+            } else {
+                sc[t] = (byte(hdr.w, j - 4) & 0xF) | ((byte(hdr.y, j - 4) >> 6) << 4);
+                m[t] = (byte(hdr.w, j - 4) >> 4) | ((byte(hdr.z, j - 4) >> 6) << 4);
+            }
+        }
+        const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
+        const float4 *xl = (const float4 *)(x + base), *xh = (const float4 *)(x + base + 32);
+        float al = 0.f, ah = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float lo[4], hi[4];
+            bytes4(wd[i] & 0x0F0F0F0Fu, lo);
+            bytes4((wd[i] >> 4) & 0x0F0F0F0Fu, hi);
+            al = dot4(lo, xl[i], al);
+            ah = dot4(hi, xh[i], ah);
+        }
+        const float sl = xs[base / 8] + xs[base / 8 + 1], sh = xs[base / 8 + 4] + xs[base / 8 + 5];
+        return d * (sc[0] * al + sc[1] * ah) - dmin * (m[0] * sl + m[1] * sh);
+    }
+};
+
+// Q6_K (Q6K.cs:37-66): 208-byte super-blocks ql[128] qh[64] sc[16], d fp32
+// [rows][cols/256].  Unit u: super-block u/8, l8 = u%8 -> half n = l8/4,
+// p = l8%4, l = 8 p + i (i < 8): values at 128 n + 32 j + l for j < 4.
+struct UnitQ6_K {
+    static constexpr int kMax = 8;  // units in flight per lane
+    uint2 a, b, h, sc;
+    float d;
+    __device__ void load(const WeightDev &w, int r, int u) {
+        const size_t sb = (size_t)r * (w.cols / 256) + u / 8;
+        const uint8_t *blk = (const uint8_t *)w.q + sb * 208;
+        const int n = (u % 8) / 4, p = u % 4;
+        a = *(const uint2 *)(blk + 64 * n + 8 * p);
+        b = *(const uint2 *)(blk + 64 * n + 32 + 8 * p);
+        h = *(const uint2 *)(blk + 128 + 32 * n + 8 * p);
+        sc = *(const uint2 *)(blk + 192 + 8 * n);
+        d = w.d[sb];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
+        const int n = (u % 8) / 4, p = u % 4;
+        const int base = 256 * (u / 8) + 128 * n + 8 * p;
+        // int8 scale i (0..7) of this half: byte i of sc, by shift
+        auto scale = [&](int i) { return (float)(int8_t)((((i < 4) ? sc.x : sc.y) >> (8 * (i & 3))) & 0xFFu); };
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int hw = 0; hw < 2; hw++) {  // i = 4 hw + [0, 4)
+            const uint32_t A = hw ? a.y : a.x, B = hw ? b.y : b.x, H = hw ? h.y : h.x;
+            const uint32_t q1 = (A & 0x0F0F0F0Fu) | ((H & 0x03030303u) << 4);
+            const uint32_t q2 = (B & 0x0F0F0F0Fu) | (((H >> 2) & 0x03030303u) << 4);
+            const uint32_t q3 = ((A >> 4) & 0x0F0F0F0Fu) | (((H >> 4) & 0x03030303u) << 4);
+            const uint32_t q4 = ((B >> 4) & 0x0F0F0F0Fu) | (((H >> 6) & 0x03030303u) << 4);
+            const uint32_t qq[4] = {q1, q2, q3, q4};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float f[4];
+                bytes4(qq[j], f);
+                acc[j] = dot4(f, *(const float4 *)(x + base + 32 * j + 4 * hw), acc[j]);
+            }
+        }
+        float a_ = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) a_ += scale(p / 2 + 2 * j) * (acc[j] - 32.f * xs[(base + 32 * j) / 8]);
+        return d * a_;
+    }
+};
+
+// Q2_0C (Q2_0C.cs:13-26): codes [rows][cols/4] bytes, d fp32 [rows][cols/512];
+// unit u = 8 bytes = values 32 u + [0, 32), value (2 c - 3) d.
+struct UnitQ2_0C {
+    static constexpr int kMax = 8;  // units in flight per lane
+    uint2 q;
+    float d;
+    __device__ void load(const WeightDev &w, int r, int u) {
+        q = *(const uint2 *)((const uint8_t *)w.q + (size_t)r * (w.cols / 4) + 8 * u);
+        d = w.d[(size_t)r * (w.cols / 512) + u / 16];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
+        const float4 *xv = (const float4 *)(x + 32 * u);
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t wd = i ? q.y : q.x;  // 16 codes: byte b holds values 4b + [0,4)
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                // value 4 b + s of byte b is bits 2 s of byte b
+                float f[4];
+                bytes4((wd >> (2 * s)) & 0x03030303u, f);  // codes (4b + s) for b = 0..3
+                const float4 x0 = xv[4 * i], x1 = xv[4 * i + 1], x2 = xv[4 * i + 2], x3 = xv[4 * i + 3];
+                const float xsel[4] = {(&x0.x)[s], (&x1.x)[s], (&x2.x)[s], (&x3.x)[s]};
+                a = fmaf(f[0], xsel[0], a);
+                a = fmaf(f[1], xsel[1], a);
+                a = fmaf(f[2], xsel[2], a);
+                a = fmaf(f[3], xsel[3], a);
+            }
+        }
+        const float sx = xs[4 * u] + xs[4 * u + 1] + xs[4 * u + 2] + xs[4 * u + 3];
+        return d * (2.f * a - 3.f * sx);
+    }
+};
+
+// STQ1_0 (STQ1_0.cs:57-101): slots [rows][cols/8] bytes (two per byte), signs
+// [rows][cols/32] bytes, d fp32 [rows][cols/256].  Unit u: block u/8, chunk
+// c = (u%8)/2, groups 16 c + 8 hg + [0, 8) (hg = u%2): 4 slot bytes, 1 sign
+// byte; group gi's lanes are values 64 c + 8 hg + gi + 16 lane.
+struct UnitSTQ1_0 {
+    static constexpr int kMax = 8;  // units in flight per lane
+    uint32_t slots;
+    uint32_t signs;
+    float d;
+    __device__ void load(const WeightDev &w, int r, int u) {
+        slots = *(const uint32_t *)((const uint8_t *)w.q + (size_t)r * (w.cols / 8) + 4 * u);
+        signs = ((const uint8_t *)w.q2)[(size_t)r * (w.cols / 32) + u];
+        d = w.d[(size_t)r * (w.cols / 256) + u / 8];
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs, const uint8_t *book) const {
+        const int c = (u % 8) / 2, hg = u % 2;
+        const int base = 256 * (u / 8) + 64 * c + 8 * hg;
+        float a = 0.f;
+#pragma unroll
+        for (int gi = 0; gi < 8; gi++) {
+            const int idx = (((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF);
+            const uint32_t pk = book[idx];
+#pragma unroll
+            for (int ln = 0; ln < 4; ln++) a = fmaf((float)((pk >> (2 * ln)) & 3), x[base + gi + 16 * ln], a);
+        }
+        const float sx = xs[base / 8] + xs[base / 8 + 2] + xs[base / 8 + 4] + xs[base / 8 + 6];
+        return d * (a - sx);
+    }
+};
+
+// STQ1_0.Codebook (STQ1_0.cs:57-63)
+__constant__ uint8_t kStqBook[32] = {
+    0xA9, 0x89, 0x29, 0x09, 0xA6, 0x86, 0x26, 0x06, 0x9A, 0x92, 0x1A, 0x12, 0x6A, 0x62, 0x4A, 0x42,
+    0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68,
+};
+
+template <typename Unit, bool STQ>
+__global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__restrict__ xg, float *__restrict__ y,
+                                                   int rw, int accumulate) {
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    float *x = smem;               // [cols]
+    float *xs = smem + w.cols;     // [cols / 8]
+    __shared__ uint8_t book[32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int upr = w.cols / 32;
+    const int K = rw * upr / 64;  // <= Unit::kMax
+    const int row0 = (blockIdx.x * 4 + wave) * rw;
+
+    // 1. this lane's weight loads, all issued before anything waits
+    constexpr int kMaxK = Unit::kMax;
+    Unit un[kMaxK];
+#pragma unroll
+    for (int k = 0; k < kMaxK; k++) {
+        if (k < K) {
+            const int t = lane + 64 * k, r = min(row0 + t / upr, w.rows - 1);
+            un[k].load(w, r, t % upr);
+        }
+    }
+    // 2. x and its 8-value sums into LDS
+    for (int i = tid; i < w.cols / 4; i += 256) ((float4 *)x)[i] = ((const float4 *)xg)[i];
+    if (STQ && tid < 32) book[tid] = kStqBook[tid];
+    __syncthreads();
+    for (int i = tid; i < w.cols / 8; i += 256) {
+        const float4 a = ((const float4 *)x)[2 * i], b = ((const float4 *)x)[2 * i + 1];
+        xs[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+    }
+    __syncthreads();
+    // 3. dot products; the k of one row are consecutive (upr / 64 per row)
+    const int kpr = upr / 64;
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxK; k++) {
+        if (k < K) {
+            const int t = lane + 64 * k;
+            if constexpr (STQ) part += un[k].dot(w, 0, t % upr, x, xs, book);
+            else part += un[k].dot(w, 0, t % upr, x, xs);
+            if ((k + 1) % kpr == 0) {
+                const float s = wave_sum(part);
+                part = 0.f;
+                const int r = row0 + k / kpr;
+                if (lane == 0 && r < w.rows) y[r] = accumulate ? y[r] + s : s;
+            }
+        }
+    }
+}
+
+template <typename Unit, bool STQ>
+hipError_t launch_t(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s) {
+    const int upr = w.cols / 32;
+    if (w.cols % 2048 != 0 || upr > Unit::kMax * 64) return hipErrorInvalidValue;  // a row's units must fit a wave
+    // rows per wave: as many units per lane as fit (K <= kMax), but at least
+    // one workgroup per CU when the matrix allows
+    int rw = Unit::kMax * 64 / upr;
+    if (rw < 1) rw = 1;
+    while (rw > 1 && (w.rows + 4 * rw - 1) / (4 * rw) < 256) rw /= 2;
+    const int blocks = (w.rows + 4 * rw - 1) / (4 * rw);
+    const size_t lds = (size_t)w.cols * 4 + (size_t)w.cols / 8 * 4;
+    hipLaunchKernelGGL((gemv_kernel<Unit, STQ>), dim3(blocks), dim3(256), lds, s, w, x, y, rw, accumulate);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s) {
+    switch (w.type) {
+    case kW_F32: return launch_t<UnitF32, false>(w, x, y, accumulate, s);
+    case kW_F16: return launch_t<UnitF16, false>(w, x, y, accumulate, s);
+    case kW_Q8_0: return launch_t<UnitQ8_0, false>(w, x, y, accumulate, s);
+    case kW_Q4_K: return launch_t<UnitQ4_K, false>(w, x, y, accumulate, s);
+    case kW_Q6_K: return launch_t<UnitQ6_K, false>(w, x, y, accumulate, s);
+    case kW_Q2_0C: return launch_t<UnitQ2_0C, false>(w, x, y, accumulate, s);
+    case kW_STQ1_0: return launch_t<UnitSTQ1_0, true>(w, x, y, accumulate, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace hymt

@@ -19,6 +19,7 @@
 
 #include "attn_kernels.hpp"
 #include "kv_pages.hpp"
+#include "weights.hpp"
 
 using namespace hymt;
 
@@ -777,3 +778,88 @@ int hymt_graph_destroy(hymt_ctx *c, hymt_graph *g) {
 }
 
 }  // extern "C"
+
+// ---- quantized weights ------------------------------------------------------
+
+struct hymt_weight {
+    hymt::WeightDev dev;
+    void *mem = nullptr;
+    size_t bytes = 0;
+};
+
+int hymt_weight_upload(hymt_ctx *c, int type, int rows, int cols, const void *data, size_t bytes,
+                       hymt_weight **out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!out || !data) return fail(HYMT_E_ARG, "null weight data or out pointer");
+    *out = nullptr;
+    if (int r = refuse_in_capture(c, "hymt_weight_upload")) return r;
+    const long rb = hymt::gguf_row_bytes(type, cols);
+    if (rb < 0) return fail(HYMT_E_UNSUPPORTED, "weight type " + std::to_string(type) + " is not supported");
+    if (rows < 1 || cols < 2048 || cols > 8192 || cols % 2048 != 0)
+        return fail(HYMT_E_UNSUPPORTED, "weight shape " + std::to_string(rows) + " x " + std::to_string(cols) +
+                                            ": cols must be a multiple of 2048 up to 8192");
+    if (bytes != (size_t)rows * (size_t)rb)
+        return fail(HYMT_E_ARG, "weight data is " + std::to_string(bytes) + " bytes, expected " +
+                                    std::to_string((size_t)rows * (size_t)rb));
+    hymt::PackedWeight pk;
+    if (!hymt::pack_weight(type, rows, cols, (const uint8_t *)data, pk))
+        return fail(HYMT_E_UNSUPPORTED, "weight type " + std::to_string(type) + " is not supported");
+    hymt_weight *w = new (std::nothrow) hymt_weight();
+    if (!w) return fail(HYMT_E_OOM, "host allocation failed");
+    (void)hipSetDevice(c->device);
+    hipError_t e = hipMalloc(&w->mem, pk.buf.size());
+    if (e != hipSuccess) {
+        delete w;
+        return fail(HYMT_E_OOM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    }
+    e = hipMemcpy(w->mem, pk.buf.data(), pk.buf.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(w->mem);
+        delete w;
+        return fail(HYMT_E_DEVICE, std::string("hipMemcpy: ") + hipGetErrorString(e));
+    }
+    uint8_t *base = (uint8_t *)w->mem;
+    w->bytes = pk.buf.size();
+    w->dev.type = type;
+    w->dev.rows = rows;
+    w->dev.cols = cols;
+    w->dev.q = base + pk.off_q;
+    w->dev.q2 = pk.off_q2 == SIZE_MAX ? nullptr : base + pk.off_q2;
+    w->dev.d = pk.off_d == SIZE_MAX ? nullptr : (const float *)(base + pk.off_d);
+    *out = w;
+    return HYMT_OK;
+}
+
+int hymt_weight_free(hymt_ctx *c, hymt_weight *w) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w) return HYMT_OK;
+    if (int r = refuse_in_capture(c, "hymt_weight_free")) return r;
+    (void)hipSetDevice(c->device);
+    (void)hipStreamSynchronize(c->stream);
+    hipError_t e = hipFree(w->mem);
+    delete w;
+    if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipFree: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size_t *device_bytes) {
+    if (!w) return fail(HYMT_E_ARG, "null weight");
+    if (type) *type = w->dev.type;
+    if (rows) *rows = w->dev.rows;
+    if (cols) *cols = w->dev.cols;
+    if (device_bytes) *device_bytes = w->bytes;
+    return HYMT_OK;
+}
+
+int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int flags) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or vector");
+    if (flags & ~HYMT_GEMV_ACCUMULATE) return fail(HYMT_E_ARG, "unknown gemv flags");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_gemv(w->dev, x, y, flags & HYMT_GEMV_ACCUMULATE, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}

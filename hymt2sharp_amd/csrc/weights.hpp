@@ -1,0 +1,49 @@
+// weights.hpp -- device layout of the quantized weight matrices (decode GEMV).
+//
+// A matrix of rows x cols values arrives as rows of GGUF blocks (the bytes
+// GgufFile hands to the reference's kernels; block structs in
+// BlockLayout.cs:9-106).  hymt_weight_upload repacks it so that every 32-value
+// unit of a row is read with aligned vector loads:
+//   F32, F16   as stored, [rows][cols]
+//   Q8_0       q: int8 [rows][cols]; d: fp32 [rows][cols/32]
+//   Q4_K       q: the 144-byte super-blocks as stored (already 16-byte aligned)
+//   Q6_K       q: 208-byte super-blocks ql[128] qh[64] scales[16]; d: fp32
+//              [rows][cols/256]
+//   Q2_0C      q: the code bytes [rows][cols/4]; d: fp32 [rows][cols/512]
+//   STQ1_0     q: the slot bytes [rows][cols/8]; q2: the sign bytes
+//              [rows][cols/32]; d: fp32 [rows][cols/256]
+// (fp16 scales widened to fp32 exactly on the host).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+namespace hymt {
+
+// GgmlTensorType codes (GgmlTensorType.cs)
+constexpr int kW_F32 = 0, kW_F16 = 1, kW_Q8_0 = 8, kW_Q4_K = 12, kW_Q6_K = 14, kW_Q2_0C = 40, kW_STQ1_0 = 43;
+
+struct WeightDev {
+    int type, rows, cols;
+    const void *q;
+    const void *q2;
+    const float *d;
+};
+
+// Bytes of one GGUF row of cols values; -1 for an unsupported type.
+long gguf_row_bytes(int type, int cols);
+
+// The device layout of a matrix: one buffer, q / q2 / d at 256-byte aligned
+// offsets (q2, d = SIZE_MAX when absent).
+struct PackedWeight {
+    std::vector<uint8_t> buf;
+    size_t off_q = 0, off_q2 = SIZE_MAX, off_d = SIZE_MAX;
+};
+bool pack_weight(int type, int rows, int cols, const uint8_t *src, PackedWeight &out);
+
+hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s);
+
+}  // namespace hymt

@@ -47,3 +47,28 @@ def f32_to_bf16_bits(x) -> np.ndarray:
 
 def bf16_bits_to_f32(h) -> np.ndarray:
     return (np.asarray(h, dtype=np.uint32) << 16).view(np.float32)
+
+
+# ---- synthetic quantized weights ---------------------------------------------------
+# (block byte counts per format, BlockLayout.cs:9-106; offset of the fp16
+# scale fields that must hold a finite, moderate value)
+_W_BLOCK = {8: (32, 34, (0,)), 12: (256, 144, (0, 2)), 14: (256, 210, (208,)), 40: (512, 130, (0,)),
+            43: (256, 42, (40,))}
+
+
+def random_weight(s: int, wtype: int, rows: int, cols: int) -> bytes:
+    """rows x cols weights as rows of GGUF blocks: uniform random quant bytes,
+    fp16 scales drawn from [2^-9, 2^-6) so the values stay O(1)."""
+    rng = np.random.default_rng(s)
+    if wtype == N.W_F32:
+        return (rng.standard_normal(rows * cols) * 0.05).astype(np.float32).tobytes()
+    if wtype == N.W_F16:
+        return (rng.standard_normal(rows * cols) * 0.05).astype(np.float16).tobytes()
+    vals, nbytes, scale_offs = _W_BLOCK[wtype]
+    nb = rows * (cols // vals)
+    raw = rng.integers(0, 256, (nb, nbytes), dtype=np.uint8)
+    for off in scale_offs:
+        d = (2.0 ** rng.uniform(-9, -6, nb)).astype(np.float16).view(np.uint16)
+        raw[:, off] = d & 0xFF
+        raw[:, off + 1] = d >> 8
+    return raw.tobytes()

@@ -219,6 +219,37 @@ int hymt_dev_alloc(hymt_ctx *ctx, size_t bytes, void **dptr);
 int hymt_dev_free(hymt_ctx *ctx, void *dptr);
 int hymt_memcpy(hymt_ctx *ctx, void *dst, const void *src, size_t bytes, int kind);
 
+/* ---- quantized weights and the decode GEMV ------------------------------------
+ * The weight half of IComputeBackend.LoadModel (IComputeBackend.cs:25-29) and of
+ * the decode graph's matrix-vector products (HunyuanDenseModel.Decode.cs
+ * DecodeQkv / DecodeLinear / DecodeGateUp; VulkanBackend.cs:400-568 with
+ * dec_gemvadd_*.comp): a matrix of rows x cols values arrives as the rows of
+ * GGUF blocks GgufFile hands the reference's kernels (GgufFile.cs:111), in one
+ * of the types below (GgmlTensorType.cs codes), and is repacked into the
+ * device layout.  cols must be a multiple of 2048 up to 8192 (the model's
+ * 2048 and 6144). */
+#define HYMT_W_F32 0
+#define HYMT_W_F16 1
+#define HYMT_W_Q8_0 8
+#define HYMT_W_Q4_K 12
+#define HYMT_W_Q6_K 14
+#define HYMT_W_Q2_0C 40
+#define HYMT_W_STQ1_0 43
+
+typedef struct hymt_weight hymt_weight;
+
+/* Upload (host data, `bytes` = rows x the type's row bytes).  Not recordable. */
+int hymt_weight_upload(hymt_ctx *ctx, int type, int rows, int cols, const void *data, size_t bytes,
+                       hymt_weight **out);
+int hymt_weight_free(hymt_ctx *ctx, hymt_weight *w);
+int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size_t *device_bytes);
+
+/* y[rows] = W x[cols], or y += W x with HYMT_GEMV_ACCUMULATE (the residual add
+ * of dec_gemvadd_*).  x and y are device pointers; the call only enqueues work
+ * and may be recorded.  fp32 activations and accumulation. */
+#define HYMT_GEMV_ACCUMULATE 1
+int hymt_gemv(hymt_ctx *ctx, const hymt_weight *w, const float *x, float *y, int flags);
+
 #ifdef __cplusplus
 }
 #endif

@@ -131,6 +131,15 @@ void orc_forward_prefill_attention(float *q, float *k, const float *v, const flo
 void orc_attention_f64(const float *q, const float *cache_k, const float *cache_v, int heads,
                        int kv_heads, int head_dim, int start, int seq, double scale, double *out);
 
+/*
+ * Quantized weight rows (hymt_quant.c): GGUF type codes 0 F32, 1 F16, 8 Q8_0,
+ * 12 Q4_K, 14 Q6_K, 40 Q2_0C, 43 STQ1_0 (GgmlTensorType.cs).  Pinned by the
+ * round trips of independent encoders in tests/test_quant_oracle.py.
+ */
+long orc_row_bytes(int type, int n);
+int orc_dequant_row(int type, const void *row, int n, float *y);
+int orc_gemv(int type, const void *w, int rows, int cols, const float *x, float *y, int accumulate);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,10 @@ def _declare(L):
     L.orc_prefill_attention.argtypes = layer + [_i, _vp, _i]
     L.orc_forward_prefill_attention.argtypes = layer + [_i, _vp, _i]
     L.orc_attention_f64.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _i, ctypes.c_double, _vp]
+    L.orc_row_bytes.restype = ctypes.c_long
+    L.orc_row_bytes.argtypes = [_i, _i]
+    L.orc_dequant_row.argtypes = [_i, _vp, _i, _vp]
+    L.orc_gemv.argtypes = [_i, _vp, _i, _i, _vp, _vp, _i]
 
 
 def _p(a):
@@ -260,3 +264,35 @@ def rel_err(a, b) -> float:
     b = np.asarray(b, dtype=np.float64)
     den = np.maximum(1e-3, np.maximum(np.abs(a), np.abs(b)))
     return float(np.max(np.abs(a - b) / den)) if a.size else 0.0
+
+
+# ---- quantized weight rows (hymt_quant.c) ------------------------------------
+
+W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
+
+
+def row_bytes(wtype: int, n: int) -> int:
+    return int(lib().orc_row_bytes(wtype, n))
+
+
+def dequant(wtype: int, data, rows: int, cols: int) -> np.ndarray:
+    """[rows][cols] fp32 values of a matrix stored as rows of GGUF blocks."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+    rb = row_bytes(wtype, cols)
+    assert raw.size == rb * rows, (raw.size, rb, rows)
+    out = np.empty((rows, cols), np.float32)
+    for r in range(rows):
+        if lib().orc_dequant_row(wtype, _p(raw[r * rb:(r + 1) * rb]), cols, _p(out[r])) != 0:
+            raise ValueError(wtype)
+    return out
+
+
+def gemv(wtype: int, data, rows: int, cols: int, x, y=None) -> np.ndarray:
+    """y (+)= W x in double over the dequantized rows (y given: accumulate)."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+    x = np.ascontiguousarray(x, np.float32)
+    acc = y is not None
+    out = np.array(y, np.float32, copy=True) if acc else np.empty(rows, np.float32)
+    if lib().orc_gemv(wtype, _p(raw), rows, cols, _p(x), _p(out), int(acc)) != 0:
+        raise ValueError(wtype)
+    return out
