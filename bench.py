@@ -41,6 +41,7 @@ sys.path.insert(0, ROOT)
 
 from hymt2sharp_amd import BF16, F16, F32, HipBackend  # noqa: E402
 from hymt2sharp_amd import synth as S  # noqa: E402
+from hymt2sharp_amd import _native as N  # noqa: E402
 
 HQ, HKV, D = 16, 4, 128
 BASE, EPS = 10000.0, 1e-6
@@ -243,6 +244,56 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
             "tokens_per_s": seq / (ms * 1e-3)}
 
 
+GEMV_CASES = [  # (name, weight type, rows, cols): the decode step's matrix shapes
+    ("q4k_gate_up", N.W_Q4_K, 12288, 2048), ("q4k_down", N.W_Q4_K, 2048, 6144),
+    ("q4k_qkv", N.W_Q4_K, 3072, 2048), ("q2c_gate_up", N.W_Q2_0C, 12288, 2048),
+    ("q2c_down", N.W_Q2_0C, 2048, 6144), ("stq_gate_up", N.W_STQ1_0, 12288, 2048),
+    ("q8_gate_up", N.W_Q8_0, 12288, 2048), ("q6k_lm_head", N.W_Q6_K, 120818, 2048),
+]
+
+
+def time_gemv(reps=200, min_bytes=320 << 20):
+    """y += W x at the decode step's shapes, one call per copy of W, cycling
+    over enough copies (> the 256 MB MALL) that every call streams W from HBM.
+    GB/s counts the GGUF bytes of W (the algorithmic weight stream)."""
+    be = HipBackend(0)
+    out = {}
+    try:
+        ev = HipEvents(be.stream())
+        for name, wt, rows, cols in GEMV_CASES:
+            raw = S.random_weight(S.seed(6, 20, wt), wt, rows, cols)
+            nbytes = len(raw)
+            copies = max(2, -(-min_bytes // nbytes))
+            ws = [be.weight_upload(wt, rows, cols, raw) for _ in range(copies)]
+            x = np.ones(cols, np.float32) / cols
+            dx, dy = be.alloc(cols * 4), be.alloc(rows * 4)
+            be.upload(dx, x)
+            be.upload(dy, np.zeros(rows, np.float32))
+            n = max(reps, copies)
+            for i in range(copies):
+                be.gemv(ws[i], dx, dy, True)
+            be.sync()
+            e0, e1 = ev.new(), ev.new()
+            ev.record(e0)
+            for i in range(n):
+                be.gemv(ws[i % copies], dx, dy, True)
+            ev.record(e1)
+            be.sync()
+            us = ev.elapsed_ms(e0, e1) / n * 1e3
+            ev.destroy(e0)
+            ev.destroy(e1)
+            for w in ws:
+                be.weight_free(w)
+            be.free(dx)
+            be.free(dy)
+            gbs = nbytes / (us * 1e-6) / 1e9
+            out[name] = {"rows": rows, "cols": cols, "bytes": nbytes, "us": round(us, 3),
+                         "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "copies": copies}
+    finally:
+        be.Dispose()
+    return out
+
+
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
     """The device block store at the config-2 shape (32 layers, fp16 KV): host
     time of HarvestPrefix and RestorePrefix over a ctx-token prompt (ctx / 64
@@ -386,9 +437,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "configs"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv"], default=None,
                     help="run one leg: the config-2 decode step, the config-3 prefill, "
-                         "or the other configurations (1, 4, 5)")
+                         "the other configurations (1, 4, 5), or the weight GEMVs")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
     ap.add_argument("--no-graph", action="store_true",
@@ -429,6 +480,10 @@ def main():
         extra["config5"] = {"workload": "decode context sweep, fp16 KV, one layer per call",
                             "unit": "GB/s", "by_context": sweep}
         extra["block_store"] = time_block_store()
+    if args.only in (None, "gemv"):
+        extra["gemv"] = {"workload": "decode weight GEMV y += W x (batch 1, fp32 x/y) at the "
+                                     "decode step's shapes, W streamed from HBM",
+                         "unit": "GB/s of GGUF weight bytes", "cases": time_gemv()}
 
     cpu = None
     if not args.no_cpu and dec is not None:

@@ -97,12 +97,13 @@ SIGNATURES = {
     "hymt_weight_free": [_vp, _vp],
     "hymt_weight_info": [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i),
                          ctypes.POINTER(ctypes.c_size_t)],
-    "hymt_gemv": [_vp, _vp, _vp, _vp, _i],
+    "hymt_gemv": [_vp, _vp, _vp, _vp, _i, _vp, ctypes.c_float],
+    "hymt_embed": [_vp, _vp, _i, _vp],
 }
 
 # weight types (GgmlTensorType codes) and gemv flags, as in include/hymt_hip.h
 W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
-GEMV_ACCUMULATE = 1
+GEMV_ACCUMULATE, GEMV_IN_RMSNORM, GEMV_IN_SWIGLU = 1, 2, 4
 
 _lib = None
 _synth = None

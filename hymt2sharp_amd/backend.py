@@ -194,9 +194,35 @@ class HipBackend:
                                            ctypes.byref(b)))
         return {"type": t.value, "rows": r.value, "cols": c.value, "device_bytes": b.value}
 
-    def gemv(self, w, x_dev, y_dev, accumulate: bool = False):
-        """y (+)= W x on device vectors (enqueued on the context's stream)."""
-        N.check(self._lib.hymt_gemv(self._h, w, x_dev, y_dev, N.GEMV_ACCUMULATE if accumulate else 0))
+    def gemv(self, w, x_dev, y_dev, accumulate: bool = False, rmsnorm=None, eps: float = 1e-6,
+             swiglu: bool = False):
+        """y (+)= W x' on device vectors (enqueued on the context's stream);
+        x' = RMSNorm(x) * rmsnorm (a device pointer) or silu(gate) * up."""
+        flags = (N.GEMV_ACCUMULATE if accumulate else 0) | (N.GEMV_IN_RMSNORM if rmsnorm else 0) | \
+                (N.GEMV_IN_SWIGLU if swiglu else 0)
+        N.check(self._lib.hymt_gemv(self._h, w, x_dev, y_dev, flags, rmsnorm, eps))
+
+    # ---- the model: IComputeBackend.LoadModel / ForwardStep (IComputeBackend.cs:25-47)
+    def LoadModel(self, tensors: dict, config, max_tokens: int = 4096, kv_dtype: int = N.BF16):
+        """tensors: GGUF name -> model.Tensor; config: model.ModelConfig.
+        Uploads every weight, creates the KV cache, keeps activations on the
+        device (hymt2sharp_amd/model.py)."""
+        from .model import DeviceModel
+        if getattr(self, "_model", None) is not None:
+            self._model.free()
+        self._model = DeviceModel(self, config, tensors, max_tokens, kv_dtype)
+        return self
+
+    def ForwardStep(self, tokens, pos: int) -> np.ndarray:
+        """Logits of the last token after running `tokens` at positions pos..;
+        the device KV holds [0, pos) before and [0, pos + len) after."""
+        if getattr(self, "_model", None) is None:
+            raise N.InvalidOperationError(N.HYMT_E_STATE, "LoadModel first")
+        return self._model.forward(tokens, pos)
+
+    def embed(self, w, row: int, out_dev):
+        """out = row `row` of W, dequantized (device pointer)."""
+        N.check(self._lib.hymt_embed(self._h, w, row, out_dev))
 
     def stream(self) -> int:
         s = ctypes.c_void_p()
@@ -222,6 +248,9 @@ class HipBackend:
 
     # -- IDisposable ------------------------------------------------------
     def Dispose(self):
+        if getattr(self, "_model", None) is not None and getattr(self, "_h", None):
+            self._model.free()
+            self._model = None
         if self._h:
             N.check(self._lib.hymt_destroy(self._h))
             self._h = None

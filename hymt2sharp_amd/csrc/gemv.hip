@@ -8,11 +8,12 @@
 // decode GEMV moves 1-15 MB, so the kernel is as much about memory latency as
 // bandwidth: a lane issues the loads of all its units before it touches x.
 //
-// Work split: 256 threads (4 waves).  A wave takes RW consecutive rows; lane l
-// handles units t = l + 64 k (k < K, K = RW * UPR / 64, UPR = cols / 32
-// units per row, a multiple of 64), i.e. unit t % UPR of row t / UPR.  x is
-// staged in LDS with the sums of its 8-value runs (the formats' offset and
-// min terms need sums of x, not per-value products).
+// Work split: 256 threads (4 waves).  A row takes a group of LPR lanes (8..64,
+// a power of two); lane j of the group handles units j + LPR k (k < K =
+// UPR / LPR, UPR = cols / 32 units per row), so neighbouring lanes read
+// neighbouring bytes and a row costs one reduction over its group (DPP).  x
+// is staged in LDS with the sums of its 8-value runs (the formats' offset
+// and min terms need sums of x, not per-value products).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -23,9 +24,16 @@ namespace hymt {
 namespace {
 
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+// Sum over aligned groups of `lanes` lanes (8, 16, 32 or 64); every lane of
+// a group receives it.  DPP within a row of 16 (quad_perm xor 1, xor 2,
+// half-row mirror, row mirror), lane shuffles across rows.
+__device__ __forceinline__ float group_sum(float v, int lanes) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, false));
+    if (lanes >= 16) v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
+    if (lanes >= 32) v += __shfl_xor(v, 16, 64);
+    if (lanes >= 64) v += __shfl_xor(v, 32, 64);
     return v;
 }
 
@@ -69,6 +77,12 @@ struct UnitF32 {
         }
         return a;
     }
+    __device__ void store(int u, float dsc, float *o) const {
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            *(float4 *)(o + 32 * u + 4 * i) = make_float4(__uint_as_float(v[i].x), __uint_as_float(v[i].y),
+                                                          __uint_as_float(v[i].z), __uint_as_float(v[i].w));
+    }
 };
 
 struct UnitF16 {
@@ -91,6 +105,17 @@ struct UnitF16 {
             a = dot4(w1, xv[2 * i + 1], a);
         }
         return a;
+    }
+    __device__ void store(int u, float, float *o) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t h[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                o[32 * u + 8 * i + 2 * e] = h2f(h[e] & 0xFFFF);
+                o[32 * u + 8 * i + 2 * e + 1] = h2f(h[e] >> 16);
+            }
+        }
     }
 };
 
@@ -117,6 +142,14 @@ struct UnitQ8_0 {
         }
         return d * a;
     }
+    __device__ void store(int u, float, float *o) const {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t wd = i < 4 ? (&v[0].x)[i] : (&v[1].x)[i - 4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[32 * u + 4 * i + e] = d * (float)(int8_t)((wd >> (8 * e)) & 0xFF);
+        }
+    }
 };
 
 // Q4_K (Q4K.cs:8-19, 36-61): 144-byte super-blocks as stored.  Unit u is
@@ -131,17 +164,14 @@ struct UnitQ4_K {
         hdr = *(const uint4 *)b;
         qs = *(const uint4 *)(b + 16 + 16 * (u % 8));
     }
-    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
-        const int g = (u % 8) / 2, h = u % 2;
-        const int base = 256 * (u / 8) + 64 * g + 16 * h;
-        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
-        // scale bytes s[0..11] are hdr.y, hdr.z, hdr.w; byte k of a dword by
-        // shift (a run-time index into a register array would go to scratch)
+    // scales and mins of sub-blocks 2 g and 2 g + 1 (GetScaleMin, Q4K.cs:8-19);
+    // scale bytes s[0..11] are hdr.y, hdr.z, hdr.w, byte k of a dword taken by
+    // shift (a run-time index into a register array would go to scratch)
+    __device__ void scales(int g, int (&sc)[2], int (&m)[2]) const {
         auto byte = [](uint32_t w, int k) { return (int)((w >> (8 * k)) & 0xFFu); };
-        int sc[2], m[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const int j = 2 * g + t;  // GetScaleMin (Q4K.cs:8-19)
+            const int j = 2 * g + t;
             if (j < 4) {
                 sc[t] = byte(hdr.y, j) & 63;
                 m[t] = byte(hdr.z, j) & 63;
@@ -150,6 +180,13 @@ struct UnitQ4_K {
                 m[t] = (byte(hdr.w, j - 4) >> 4) | ((byte(hdr.z, j - 4) >> 6) << 4);
             }
         }
+    }
+    __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
+        const int g = (u % 8) / 2, h = u % 2;
+        const int base = 256 * (u / 8) + 64 * g + 16 * h;
+        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+        int sc[2], m[2];
+        scales(g, sc, m);
         const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
         const float4 *xl = (const float4 *)(x + base), *xh = (const float4 *)(x + base + 32);
         float al = 0.f, ah = 0.f;
@@ -163,6 +200,26 @@ struct UnitQ4_K {
         }
         const float sl = xs[base / 8] + xs[base / 8 + 1], sh = xs[base / 8 + 4] + xs[base / 8 + 5];
         return d * (sc[0] * al + sc[1] * ah) - dmin * (m[0] * sl + m[1] * sh);
+    }
+    __device__ void store(int u, float, float *o) const {
+        const int g = (u % 8) / 2, h = u % 2;
+        const int base = 256 * (u / 8) + 64 * g + 16 * h;
+        const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
+        int sc[2], m[2];
+        scales(g, sc, m);
+        const float d1 = d * sc[0], m1 = dmin * m[0], d2 = d * sc[1], m2 = dmin * m[1];
+        const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float lo[4], hi[4];
+            bytes4(wd[i] & 0x0F0F0F0Fu, lo);
+            bytes4((wd[i] >> 4) & 0x0F0F0F0Fu, hi);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                o[base + 4 * i + e] = d1 * lo[e] - m1;
+                o[base + 32 + 4 * i + e] = d2 * hi[e] - m2;
+            }
+        }
     }
 };
 
@@ -209,6 +266,27 @@ struct UnitQ6_K {
         for (int j = 0; j < 4; j++) a_ += scale(p / 2 + 2 * j) * (acc[j] - 32.f * xs[(base + 32 * j) / 8]);
         return d * a_;
     }
+    __device__ void store(int u, float, float *o) const {
+        const int n = (u % 8) / 4, p = u % 4;
+        const int base = 256 * (u / 8) + 128 * n + 8 * p;
+        auto scale = [&](int i) { return (float)(int8_t)((((i < 4) ? sc.x : sc.y) >> (8 * (i & 3))) & 0xFFu); };
+#pragma unroll
+        for (int hw = 0; hw < 2; hw++) {
+            const uint32_t A = hw ? a.y : a.x, B = hw ? b.y : b.x, H = hw ? h.y : h.x;
+            const uint32_t qq[4] = {(A & 0x0F0F0F0Fu) | ((H & 0x03030303u) << 4),
+                                    (B & 0x0F0F0F0Fu) | (((H >> 2) & 0x03030303u) << 4),
+                                    ((A >> 4) & 0x0F0F0F0Fu) | (((H >> 4) & 0x03030303u) << 4),
+                                    ((B >> 4) & 0x0F0F0F0Fu) | (((H >> 6) & 0x03030303u) << 4)};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float f[4];
+                bytes4(qq[j], f);
+                const float ds = d * scale(p / 2 + 2 * j);
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[base + 32 * j + 4 * hw + e] = ds * (f[e] - 32.f);
+            }
+        }
+    }
 };
 
 // Q2_0C (Q2_0C.cs:13-26): codes [rows][cols/4] bytes, d fp32 [rows][cols/512];
@@ -243,6 +321,17 @@ struct UnitQ2_0C {
         const float sx = xs[4 * u] + xs[4 * u + 1] + xs[4 * u + 2] + xs[4 * u + 3];
         return d * (2.f * a - 3.f * sx);
     }
+    __device__ void store(int u, float, float *o) const {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t wd = i ? q.y : q.x;
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+                    o[32 * u + 16 * i + 4 * b + t] = (float)((int)((wd >> (8 * b + 2 * t)) & 3u) * 2 - 3) * d;
+        }
+    }
 };
 
 // STQ1_0 (STQ1_0.cs:57-101): slots [rows][cols/8] bytes (two per byte), signs
@@ -262,16 +351,29 @@ struct UnitSTQ1_0 {
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs, const uint8_t *book) const {
         const int c = (u % 8) / 2, hg = u % 2;
         const int base = 256 * (u / 8) + 64 * c + 8 * hg;
+        uint32_t pk[8];
+#pragma unroll
+        for (int gi = 0; gi < 8; gi++) pk[gi] = book[(((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF)];
         float a = 0.f;
 #pragma unroll
-        for (int gi = 0; gi < 8; gi++) {
-            const int idx = (((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF);
-            const uint32_t pk = book[idx];
+        for (int ln = 0; ln < 4; ln++) {
+            const float4 xa = *(const float4 *)(x + base + 16 * ln), xb = *(const float4 *)(x + base + 16 * ln + 4);
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-            for (int ln = 0; ln < 4; ln++) a = fmaf((float)((pk >> (2 * ln)) & 3), x[base + gi + 16 * ln], a);
+            for (int gi = 0; gi < 8; gi++) a = fmaf((float)((pk[gi] >> (2 * ln)) & 3), xv[gi], a);
         }
         const float sx = xs[base / 8] + xs[base / 8 + 2] + xs[base / 8 + 4] + xs[base / 8 + 6];
         return d * (a - sx);
+    }
+    __device__ void store(int u, const uint8_t *book, float *o) const {
+        const int c = (u % 8) / 2, hg = u % 2;
+        const int base = 256 * (u / 8) + 64 * c + 8 * hg;
+#pragma unroll
+        for (int gi = 0; gi < 8; gi++) {
+            const uint32_t pk = book[(((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF)];
+#pragma unroll
+            for (int ln = 0; ln < 4; ln++) o[base + gi + 16 * ln] = (float)((int)((pk >> (2 * ln)) & 3u) - 1) * d;
+        }
     }
 };
 
@@ -283,80 +385,138 @@ __constant__ uint8_t kStqBook[32] = {
 
 template <typename Unit, bool STQ>
 __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__restrict__ xg, float *__restrict__ y,
-                                                   int rw, int accumulate) {
+                                                   int lpr, int flags, const float *__restrict__ nw, float eps) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
     float *x = smem;               // [cols]
     float *xs = smem + w.cols;     // [cols / 8]
     __shared__ uint8_t book[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int upr = w.cols / 32;
-    const int K = rw * upr / 64;  // <= Unit::kMax
-    const int row0 = (blockIdx.x * 4 + wave) * rw;
+    const int K = upr / lpr;  // units per lane, <= Unit::kMax
+    const int row = (blockIdx.x * 4 + wave) * (64 / lpr) + lane / lpr;
+    const int sub = lane % lpr;
 
     // 1. this lane's weight loads, all issued before anything waits
     constexpr int kMaxK = Unit::kMax;
     Unit un[kMaxK];
+    const int rl = min(row, w.rows - 1);
 #pragma unroll
-    for (int k = 0; k < kMaxK; k++) {
-        if (k < K) {
-            const int t = lane + 64 * k, r = min(row0 + t / upr, w.rows - 1);
-            un[k].load(w, r, t % upr);
+    for (int k = 0; k < kMaxK; k++)
+        if (k < K) un[k].load(w, rl, sub + lpr * k);
+    // 2. x, as the input mode makes it, and its 8-value sums into LDS
+    const int n4 = w.cols / 4;
+    if (flags & kGemvInSwiGLU) {
+        // xg = gate[cols] then up[cols]; x = silu(gate) * up
+        // (Ops.SiLUMulRange, Ops.cs:1016-1052: g / (1 + exp(-g)) * u)
+        for (int i = tid; i < n4; i += 256) {
+            const float4 g = ((const float4 *)xg)[i], u = ((const float4 *)xg)[n4 + i];
+            ((float4 *)x)[i] = make_float4(g.x / (1.f + expf(-g.x)) * u.x, g.y / (1.f + expf(-g.y)) * u.y,
+                                           g.z / (1.f + expf(-g.z)) * u.z, g.w / (1.f + expf(-g.w)) * u.w);
+        }
+    } else {
+        for (int i = tid; i < n4; i += 256) ((float4 *)x)[i] = ((const float4 *)xg)[i];
+    }
+    if (STQ && tid < 32) book[tid] = kStqBook[tid];
+    if (flags & kGemvInRmsNorm) {
+        // x = x / sqrt(mean(x^2) + eps) * nw (Ops.RmsNorm, Ops.cs:12-90): each
+        // thread scales the float4s it staged once the workgroup has the sum
+        __shared__ float red[4];
+        float ss = 0.f;
+        for (int i = tid; i < n4; i += 256) {
+            const float4 v = ((const float4 *)x)[i];
+            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        }
+        ss = group_sum(ss, 64);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const float rr = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)w.cols + eps);
+        for (int i = tid; i < n4; i += 256) {
+            const float4 v = ((const float4 *)x)[i], g = ((const float4 *)nw)[i];
+            ((float4 *)x)[i] = make_float4(v.x * rr * g.x, v.y * rr * g.y, v.z * rr * g.z, v.w * rr * g.w);
         }
     }
-    // 2. x and its 8-value sums into LDS
-    for (int i = tid; i < w.cols / 4; i += 256) ((float4 *)x)[i] = ((const float4 *)xg)[i];
-    if (STQ && tid < 32) book[tid] = kStqBook[tid];
     __syncthreads();
     for (int i = tid; i < w.cols / 8; i += 256) {
         const float4 a = ((const float4 *)x)[2 * i], b = ((const float4 *)x)[2 * i + 1];
         xs[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
     }
     __syncthreads();
-    // 3. dot products; the k of one row are consecutive (upr / 64 per row)
-    const int kpr = upr / 64;
+    // 3. dot products, then the row's sum over its lane group
     float part = 0.f;
 #pragma unroll
     for (int k = 0; k < kMaxK; k++) {
         if (k < K) {
-            const int t = lane + 64 * k;
-            if constexpr (STQ) part += un[k].dot(w, 0, t % upr, x, xs, book);
-            else part += un[k].dot(w, 0, t % upr, x, xs);
-            if ((k + 1) % kpr == 0) {
-                const float s = wave_sum(part);
-                part = 0.f;
-                const int r = row0 + k / kpr;
-                if (lane == 0 && r < w.rows) y[r] = accumulate ? y[r] + s : s;
-            }
+            if constexpr (STQ) part += un[k].dot(w, 0, sub + lpr * k, x, xs, book);
+            else part += un[k].dot(w, 0, sub + lpr * k, x, xs);
         }
+    }
+    const float s = group_sum(part, lpr);
+    if (sub == 0 && row < w.rows) y[row] = (flags & kGemvAccumulate) ? y[row] + s : s;
+}
+
+// One row of the matrix, dequantized (the embedding lookup,
+// HunyuanDenseModel.Embed, HunyuanDenseModel.cs:494-557): a workgroup of 256
+// threads, one unit per thread and pass.
+template <typename Unit, bool STQ>
+__global__ __launch_bounds__(256) void embed_kernel(WeightDev w, int row, float *__restrict__ out) {
+    __shared__ uint8_t book[32];
+    if (STQ && threadIdx.x < 32) book[threadIdx.x] = kStqBook[threadIdx.x];
+    __syncthreads();
+    for (int u = threadIdx.x; u < w.cols / 32; u += 256) {
+        Unit un;
+        un.load(w, row, u);
+        if constexpr (STQ) un.store(u, book, out);
+        else un.store(u, 0.f, out);
     }
 }
 
 template <typename Unit, bool STQ>
-hipError_t launch_t(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s) {
+hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
+                    hipStream_t s) {
     const int upr = w.cols / 32;
     if (w.cols % 2048 != 0 || upr > Unit::kMax * 64) return hipErrorInvalidValue;  // a row's units must fit a wave
-    // rows per wave: as many units per lane as fit (K <= kMax), but at least
-    // one workgroup per CU when the matrix allows
-    int rw = Unit::kMax * 64 / upr;
-    if (rw < 1) rw = 1;
-    while (rw > 1 && (w.rows + 4 * rw - 1) / (4 * rw) < 256) rw /= 2;
-    const int blocks = (w.rows + 4 * rw - 1) / (4 * rw);
+    // lanes per row: the fewest (most units in flight per lane, K <= kMax), but
+    // more while the grid would leave CUs idle
+    int lpr = 8;
+    while (upr / lpr > Unit::kMax) lpr *= 2;
+    auto blocks = [&](int l) { return (w.rows + 4 * (64 / l) - 1) / (4 * (64 / l)); };
+    while (lpr < 64 && blocks(lpr) < 256) lpr *= 2;
     const size_t lds = (size_t)w.cols * 4 + (size_t)w.cols / 8 * 4;
-    hipLaunchKernelGGL((gemv_kernel<Unit, STQ>), dim3(blocks), dim3(256), lds, s, w, x, y, rw, accumulate);
+    hipLaunchKernelGGL((gemv_kernel<Unit, STQ>), dim3(blocks(lpr)), dim3(256), lds, s, w, x, y, lpr, flags, nw, eps);
+    return hipGetLastError();
+}
+
+template <typename Unit, bool STQ>
+hipError_t launch_embed_t(const WeightDev &w, int row, float *out, hipStream_t s) {
+    hipLaunchKernelGGL((embed_kernel<Unit, STQ>), dim3(1), dim3(256), 0, s, w, row, out);
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s) {
+hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
+                       hipStream_t s) {
     switch (w.type) {
-    case kW_F32: return launch_t<UnitF32, false>(w, x, y, accumulate, s);
-    case kW_F16: return launch_t<UnitF16, false>(w, x, y, accumulate, s);
-    case kW_Q8_0: return launch_t<UnitQ8_0, false>(w, x, y, accumulate, s);
-    case kW_Q4_K: return launch_t<UnitQ4_K, false>(w, x, y, accumulate, s);
-    case kW_Q6_K: return launch_t<UnitQ6_K, false>(w, x, y, accumulate, s);
-    case kW_Q2_0C: return launch_t<UnitQ2_0C, false>(w, x, y, accumulate, s);
-    case kW_STQ1_0: return launch_t<UnitSTQ1_0, true>(w, x, y, accumulate, s);
+    case kW_F32: return launch_t<UnitF32, false>(w, x, y, flags, nw, eps, s);
+    case kW_F16: return launch_t<UnitF16, false>(w, x, y, flags, nw, eps, s);
+    case kW_Q8_0: return launch_t<UnitQ8_0, false>(w, x, y, flags, nw, eps, s);
+    case kW_Q4_K: return launch_t<UnitQ4_K, false>(w, x, y, flags, nw, eps, s);
+    case kW_Q6_K: return launch_t<UnitQ6_K, false>(w, x, y, flags, nw, eps, s);
+    case kW_Q2_0C: return launch_t<UnitQ2_0C, false>(w, x, y, flags, nw, eps, s);
+    case kW_STQ1_0: return launch_t<UnitSTQ1_0, true>(w, x, y, flags, nw, eps, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_embed(const WeightDev &w, int row, float *out, hipStream_t s) {
+    switch (w.type) {
+    case kW_F32: return launch_embed_t<UnitF32, false>(w, row, out, s);
+    case kW_F16: return launch_embed_t<UnitF16, false>(w, row, out, s);
+    case kW_Q8_0: return launch_embed_t<UnitQ8_0, false>(w, row, out, s);
+    case kW_Q4_K: return launch_embed_t<UnitQ4_K, false>(w, row, out, s);
+    case kW_Q6_K: return launch_embed_t<UnitQ6_K, false>(w, row, out, s);
+    case kW_Q2_0C: return launch_embed_t<UnitQ2_0C, false>(w, row, out, s);
+    case kW_STQ1_0: return launch_embed_t<UnitSTQ1_0, true>(w, row, out, s);
     default: return hipErrorInvalidValue;
     }
 }

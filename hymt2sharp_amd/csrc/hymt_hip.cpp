@@ -851,13 +851,32 @@ int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size
     return HYMT_OK;
 }
 
-int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int flags) {
+int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int flags, const float *norm_w,
+              float eps) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or vector");
-    if (flags & ~HYMT_GEMV_ACCUMULATE) return fail(HYMT_E_ARG, "unknown gemv flags");
+    if (flags & ~(HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_RMSNORM | HYMT_GEMV_IN_SWIGLU))
+        return fail(HYMT_E_ARG, "unknown gemv flags");
+    if ((flags & HYMT_GEMV_IN_RMSNORM) && (flags & HYMT_GEMV_IN_SWIGLU))
+        return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM and HYMT_GEMV_IN_SWIGLU exclude each other");
+    if ((flags & HYMT_GEMV_IN_RMSNORM) && !norm_w) return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM needs norm_w");
     try {
         HIP_TRY(hipSetDevice(c->device));
-        HIP_TRY(hymt::launch_gemv(w->dev, x, y, flags & HYMT_GEMV_ACCUMULATE, c->stream));
+        HIP_TRY(hymt::launch_gemv(w->dev, x, y, flags, norm_w, eps, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_embed(hymt_ctx *c, const hymt_weight *w, int row, float *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w || !out) return fail(HYMT_E_ARG, "null weight or output");
+    if (row < 0 || row >= w->dev.rows)
+        return fail(HYMT_E_ARG, "row " + std::to_string(row) + " outside [0, " + std::to_string(w->dev.rows) + ")");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_embed(w->dev, row, out, c->stream));
     } catch (const HipError &e) {
         return map_hip(e);
     }

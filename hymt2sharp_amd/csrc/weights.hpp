@@ -44,6 +44,10 @@ struct PackedWeight {
 };
 bool pack_weight(int type, int rows, int cols, const uint8_t *src, PackedWeight &out);
 
-hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int accumulate, hipStream_t s);
+// gemv flags (as HYMT_GEMV_* in include/hymt_hip.h)
+constexpr int kGemvAccumulate = 1, kGemvInRmsNorm = 2, kGemvInSwiGLU = 4;
+hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
+                       hipStream_t s);
+hipError_t launch_embed(const WeightDev &w, int row, float *out, hipStream_t s);
 
 }  // namespace hymt

@@ -72,3 +72,48 @@ def random_weight(s: int, wtype: int, rows: int, cols: int) -> bytes:
         raw[:, off] = d & 0xFF
         raw[:, off + 1] = d >> 8
     return raw.tobytes()
+
+
+def random_model(s: int, cfg, types: dict | None = None, tied: bool = False) -> dict:
+    """A hunyuan-dense model of the config's shape with seeded random weights:
+    GGUF name -> model.Tensor.  `types` maps a role ("attn", "ffn", "embd",
+    "out") to a weight type, or to a list of types taken per layer in turn
+    (default Q4_K, and Q6_K for the embedding and output, as in the Q4_K_M
+    files); norm weights are F32 ~ U(0.9, 1.1)."""
+    from .model import Tensor
+    t = {"attn": N.W_Q4_K, "ffn": N.W_Q4_K, "embd": N.W_Q6_K, "out": N.W_Q6_K}
+    t.update(types or {})
+
+    def ty(role, l=0):
+        v = t[role]
+        return v[l % len(v)] if isinstance(v, (list, tuple)) else v
+
+    H, F, qd, kd = cfg.hidden_size, cfg.ffn_size, cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    out, k = {}, [0]
+
+    def m(name, wt, rows, cols):
+        k[0] += 1
+        out[name] = Tensor(wt, rows, cols, random_weight(s * 1000 + k[0], wt, rows, cols))
+
+    def v(name, n):
+        k[0] += 1
+        out[name] = Tensor(N.W_F32, 1, n, uniform(s * 1000 + k[0], n, 0.9, 1.1).astype(np.float32).tobytes())
+
+    for l in range(cfg.num_layers):
+        p = f"blk.{l}."
+        v(p + "attn_norm.weight", H)
+        v(p + "ffn_norm.weight", H)
+        v(p + "attn_q_norm.weight", cfg.head_dim)
+        v(p + "attn_k_norm.weight", cfg.head_dim)
+        m(p + "attn_q.weight", ty("attn", l), qd, H)
+        m(p + "attn_k.weight", ty("attn", l), kd, H)
+        m(p + "attn_v.weight", ty("attn", l), kd, H)
+        m(p + "attn_output.weight", ty("attn", l), H, qd)
+        m(p + "ffn_gate.weight", ty("ffn", l), F, H)
+        m(p + "ffn_up.weight", ty("ffn", l), F, H)
+        m(p + "ffn_down.weight", ty("ffn", l), H, F)
+    m("token_embd.weight", ty("embd"), cfg.vocab_size, H)
+    if not tied:
+        m("output.weight", ty("out"), cfg.vocab_size, H)
+    v("output_norm.weight", H)
+    return out

@@ -244,11 +244,26 @@ int hymt_weight_upload(hymt_ctx *ctx, int type, int rows, int cols, const void *
 int hymt_weight_free(hymt_ctx *ctx, hymt_weight *w);
 int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size_t *device_bytes);
 
-/* y[rows] = W x[cols], or y += W x with HYMT_GEMV_ACCUMULATE (the residual add
- * of dec_gemvadd_*).  x and y are device pointers; the call only enqueues work
- * and may be recorded.  fp32 activations and accumulation. */
+/* y[rows] = W x'[cols], or y += W x' with HYMT_GEMV_ACCUMULATE (the residual
+ * add of dec_gemvadd_*), where x' is x as the input flags make it:
+ *   HYMT_GEMV_IN_RMSNORM  x' = x / sqrt(mean(x^2) + eps) * norm_w[cols]
+ *                         (Ops.RmsNorm, Ops.cs:12-90: the RMSNorm before a
+ *                         block's projections, dec_prekv / dec_preffn)
+ *   HYMT_GEMV_IN_SWIGLU   x holds gate[cols] then up[cols];
+ *                         x' = gate / (1 + exp(-gate)) * up (Ops.SiLUMul,
+ *                         Ops.cs:999-1052: the FFN's down projection input)
+ * x, y and norm_w are device pointers; the call only enqueues work and may be
+ * recorded.  fp32 activations and accumulation. */
 #define HYMT_GEMV_ACCUMULATE 1
-int hymt_gemv(hymt_ctx *ctx, const hymt_weight *w, const float *x, float *y, int flags);
+#define HYMT_GEMV_IN_RMSNORM 2
+#define HYMT_GEMV_IN_SWIGLU 4
+int hymt_gemv(hymt_ctx *ctx, const hymt_weight *w, const float *x, float *y, int flags,
+              const float *norm_w, float eps);
+
+/* out[cols] = row `row` of W, dequantized (the embedding lookup,
+ * HunyuanDenseModel.Embed, HunyuanDenseModel.cs:494-557).  out is a device
+ * pointer; the call only enqueues work and may be recorded. */
+int hymt_embed(hymt_ctx *ctx, const hymt_weight *w, int row, float *out);
 
 #ifdef __cplusplus
 }
