@@ -294,6 +294,74 @@ def time_gemv(reps=200, min_bytes=320 << 20):
     return out
 
 
+def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16):
+    """Whole decode step of the 32-layer hunyuan-dense model (synthetic Q4_K
+    layers, Q6_K embedding and output as in a Q4_K_M file, fp16 KV) at
+    position `ctx` over a resident ctx-row cache: embedding row, per layer the
+    q/k/v GEMV with RMSNorm input, decode attention, output GEMV with residual,
+    gate/up GEMV with RMSNorm input, down GEMV with SwiGLU input and residual,
+    then the output norm and projection.  Timed two ways: recorded (one
+    hymt_graph_launch per token, HIP events) and eager (ForwardStep per
+    token from Python, including the logits download).  Bytes per token: the
+    GGUF bytes of every weight read (one embedding row) plus the KV reads and
+    writes of the attention calls."""
+    from hymt2sharp_amd.model import ModelConfig
+    cfg = ModelConfig(eps=EPS)
+    t = S.random_model(5, cfg)
+    emb = t["token_embd.weight"]
+    wbytes = sum(len(x.data) for n, x in t.items() if n != "token_embd.weight") + \
+        len(emb.data) // emb.rows
+    kvbytes = cfg.num_layers * decode_bytes_per_layer(ctx + 1, 4 if kv_dtype == F32 else 2)
+    be = HipBackend(0)
+    try:
+        be.LoadModel(t, cfg, max_tokens=ctx + 1, kv_dtype=kv_dtype)
+        del t
+        pool = decode_pool(2, ctx, n=4)
+        for layer in range(cfg.num_layers):
+            be.UploadKv(layer, 0, ctx, *pool[layer % len(pool)])
+        del pool
+        m, tok = be._model, 4242
+        for _ in range(warmup):
+            logits = be.ForwardStep([tok], ctx)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            logits = be.ForwardStep([tok], ctx)
+        eager_ms = (time.perf_counter() - t0) * 1e3 / steps
+        assert np.all(np.isfinite(logits))
+        be.graph_begin()
+        m.step(tok, ctx)
+        g = be.graph_end()
+        ev = HipEvents(be.stream())
+        for _ in range(warmup):
+            be.graph_launch(g)
+        be.sync()
+        e0, e1 = ev.new(), ev.new()
+        ev.record(e0)
+        for _ in range(steps):
+            be.graph_launch(g)
+        ev.record(e1)
+        be.sync()
+        ms = ev.elapsed_ms(e0, e1) / steps
+        ev.destroy(e0)
+        ev.destroy(e1)
+        be.graph_destroy(g)
+        out = np.empty(cfg.vocab_size, np.float32)
+        be.download(out, m.logits)
+        assert np.max(np.abs(out - logits)) <= 1e-5 * np.max(np.abs(logits)), \
+            "recorded step differs from the eager one"
+    finally:
+        be.Dispose()
+    gbs = (wbytes + kvbytes) / (ms * 1e-3) / 1e9
+    return {"workload": "32-layer hunyuan-dense decode step (hidden 2048, FFN 6144, vocab 120818; "
+                        "Q4_K layers, Q6_K embedding/output, synthetic weights), fp16 KV, "
+                        f"position {ctx} over a {ctx}-row cache",
+            "tokens_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+            "eager_tokens_per_s": round(1e3 / eager_ms, 1), "eager_ms_per_token": round(eager_ms, 4),
+            "weight_bytes": wbytes, "kv_bytes": kvbytes, "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "submission": "recorded step (hymt_graph_launch); eager = ForwardStep from Python"}
+
+
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
     """The device block store at the config-2 shape (32 layers, fp16 KV): host
     time of HarvestPrefix and RestorePrefix over a ctx-token prompt (ctx / 64
@@ -437,9 +505,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv", "model"],
+                    default=None,
                     help="run one leg: the config-2 decode step, the config-3 prefill, "
-                         "the other configurations (1, 4, 5), or the weight GEMVs")
+                         "the other configurations (1, 4, 5), the weight GEMVs or the "
+                         "whole-model decode step")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
     ap.add_argument("--no-graph", action="store_true",
@@ -484,6 +554,8 @@ def main():
         extra["gemv"] = {"workload": "decode weight GEMV y += W x (batch 1, fp32 x/y) at the "
                                      "decode step's shapes, W streamed from HBM",
                          "unit": "GB/s of GGUF weight bytes", "cases": time_gemv()}
+    if args.only in (None, "model"):
+        extra["model"] = time_model(steps=max(5, args.steps // 2), warmup=args.warmup)
 
     cpu = None
     if not args.no_cpu and dec is not None:

@@ -383,7 +383,7 @@ __constant__ uint8_t kStqBook[32] = {
     0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68,
 };
 
-template <typename Unit, bool STQ>
+template <typename Unit, bool STQ, int NJ>
 __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__restrict__ xg, float *__restrict__ y,
                                                    int lpr, int flags, const float *__restrict__ nw, float eps) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -396,50 +396,82 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     const int row = (blockIdx.x * 4 + wave) * (64 / lpr) + lane / lpr;
     const int sub = lane % lpr;
 
-    // 1. this lane's weight loads, all issued before anything waits
+    // 1. the activations first (small, from L2: their data returns while the
+    // weight loads below are still in flight), then this lane's weight loads,
+    // all issued before anything waits.  Thread tid holds the 8 values
+    // [8i, 8i+8) for i = tid + 256j, j < NJ = cols / 2048.
+    constexpr int nj = NJ;
+    float4 xa[NJ], xb[NJ], ua[NJ], ub[NJ], ga[NJ], gb[NJ];
+    const bool swiglu = flags & kGemvInSwiGLU, rms = flags & kGemvInRmsNorm;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        if (j < nj) {
+            const int i = tid + 256 * j;
+            xa[j] = ((const float4 *)xg)[2 * i];
+            xb[j] = ((const float4 *)xg)[2 * i + 1];
+            if (swiglu) {
+                ua[j] = ((const float4 *)(xg + w.cols))[2 * i];
+                ub[j] = ((const float4 *)(xg + w.cols))[2 * i + 1];
+            }
+            if (rms) {
+                ga[j] = ((const float4 *)nw)[2 * i];
+                gb[j] = ((const float4 *)nw)[2 * i + 1];
+            }
+        }
+    }
     constexpr int kMaxK = Unit::kMax;
     Unit un[kMaxK];
     const int rl = min(row, w.rows - 1);
 #pragma unroll
     for (int k = 0; k < kMaxK; k++)
         if (k < K) un[k].load(w, rl, sub + lpr * k);
-    // 2. x, as the input mode makes it, and its 8-value sums into LDS
-    const int n4 = w.cols / 4;
-    if (flags & kGemvInSwiGLU) {
-        // xg = gate[cols] then up[cols]; x = silu(gate) * up
-        // (Ops.SiLUMulRange, Ops.cs:1016-1052: g / (1 + exp(-g)) * u)
-        for (int i = tid; i < n4; i += 256) {
-            const float4 g = ((const float4 *)xg)[i], u = ((const float4 *)xg)[n4 + i];
-            ((float4 *)x)[i] = make_float4(g.x / (1.f + expf(-g.x)) * u.x, g.y / (1.f + expf(-g.y)) * u.y,
-                                           g.z / (1.f + expf(-g.z)) * u.z, g.w / (1.f + expf(-g.w)) * u.w);
-        }
-    } else {
-        for (int i = tid; i < n4; i += 256) ((float4 *)x)[i] = ((const float4 *)xg)[i];
-    }
     if (STQ && tid < 32) book[tid] = kStqBook[tid];
-    if (flags & kGemvInRmsNorm) {
-        // x = x / sqrt(mean(x^2) + eps) * nw (Ops.RmsNorm, Ops.cs:12-90): each
-        // thread scales the float4s it staged once the workgroup has the sum
+    // 2. x as the input mode makes it, into LDS with its 8-value sums
+    auto silu_mul = [](float4 g, float4 u) {
+        // Ops.SiLUMulRange (Ops.cs:1016-1052): g / (1 + exp(-g)) * u
+        return make_float4(g.x / (1.f + expf(-g.x)) * u.x, g.y / (1.f + expf(-g.y)) * u.y,
+                           g.z / (1.f + expf(-g.z)) * u.z, g.w / (1.f + expf(-g.w)) * u.w);
+    };
+    if (swiglu) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            if (j < nj) {
+                xa[j] = silu_mul(xa[j], ua[j]);
+                xb[j] = silu_mul(xb[j], ub[j]);
+            }
+    }
+    if (rms) {
+        // x / sqrt(mean(x^2) + eps) * nw (Ops.RmsNorm, Ops.cs:12-90)
         __shared__ float red[4];
         float ss = 0.f;
-        for (int i = tid; i < n4; i += 256) {
-            const float4 v = ((const float4 *)x)[i];
-            ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
-        }
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            if (j < nj) {
+                const float4 a = xa[j], b = xb[j];
+                ss += ((a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w)) +
+                      ((b.x * b.x + b.y * b.y) + (b.z * b.z + b.w * b.w));
+            }
         ss = group_sum(ss, 64);
         if (lane == 0) red[wave] = ss;
         __syncthreads();
         const float rr = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)w.cols + eps);
-        for (int i = tid; i < n4; i += 256) {
-            const float4 v = ((const float4 *)x)[i], g = ((const float4 *)nw)[i];
-            ((float4 *)x)[i] = make_float4(v.x * rr * g.x, v.y * rr * g.y, v.z * rr * g.z, v.w * rr * g.w);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            if (j < nj) {
+                const float4 a = xa[j], b = xb[j], g = ga[j], h = gb[j];
+                xa[j] = make_float4(a.x * rr * g.x, a.y * rr * g.y, a.z * rr * g.z, a.w * rr * g.w);
+                xb[j] = make_float4(b.x * rr * h.x, b.y * rr * h.y, b.z * rr * h.z, b.w * rr * h.w);
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+        if (j < nj) {
+            const int i = tid + 256 * j;
+            const float4 a = xa[j], b = xb[j];
+            ((float4 *)x)[2 * i] = a;
+            ((float4 *)x)[2 * i + 1] = b;
+            xs[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
         }
-    }
-    __syncthreads();
-    for (int i = tid; i < w.cols / 8; i += 256) {
-        const float4 a = ((const float4 *)x)[2 * i], b = ((const float4 *)x)[2 * i + 1];
-        xs[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-    }
     __syncthreads();
     // 3. dot products, then the row's sum over its lane group
     float part = 0.f;
@@ -474,7 +506,8 @@ template <typename Unit, bool STQ>
 hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
                     hipStream_t s) {
     const int upr = w.cols / 32;
-    if (w.cols % 2048 != 0 || upr > Unit::kMax * 64) return hipErrorInvalidValue;  // a row's units must fit a wave
+    // a row's units must fit a wave; a thread stages at most 4 x 8 values of x
+    if (w.cols % 2048 != 0 || w.cols > 8192 || upr > Unit::kMax * 64) return hipErrorInvalidValue;
     // lanes per row: the fewest (most units in flight per lane, K <= kMax), but
     // more while the grid would leave CUs idle
     int lpr = 8;
@@ -482,7 +515,13 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     auto blocks = [&](int l) { return (w.rows + 4 * (64 / l) - 1) / (4 * (64 / l)); };
     while (lpr < 64 && blocks(lpr) < 256) lpr *= 2;
     const size_t lds = (size_t)w.cols * 4 + (size_t)w.cols / 8 * 4;
-    hipLaunchKernelGGL((gemv_kernel<Unit, STQ>), dim3(blocks(lpr)), dim3(256), lds, s, w, x, y, lpr, flags, nw, eps);
+    const dim3 grid(blocks(lpr));
+    switch (w.cols / 2048) {
+    case 1: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 1>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 2>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    case 3: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 3>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    default: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 4>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    }
     return hipGetLastError();
 }
 
