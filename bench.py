@@ -294,7 +294,7 @@ def time_gemv(reps=200, min_bytes=320 << 20):
     return out
 
 
-def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16):
+def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefill_reps=5):
     """Whole decode step of the 32-layer hunyuan-dense model (synthetic Q4_K
     layers, Q6_K embedding and output as in a Q4_K_M file, fp16 KV) at
     position `ctx` over a resident ctx-row cache: embedding row, per layer the
@@ -304,10 +304,15 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16):
     hymt_graph_launch per token, HIP events) and eager (ForwardStep per
     token from Python, including the logits download).  Bytes per token: the
     GGUF bytes of every weight read (one embedding row) plus the KV reads and
-    writes of the attention calls."""
+    writes of the attention calls.  Then a prompt_len-token prefill through
+    ForwardStep (bf16 GEMMs over dense weight copies, the flash prefill
+    kernel), wall clock including the logits download."""
     from hymt2sharp_amd.model import ModelConfig
     cfg = ModelConfig(eps=EPS)
     t = S.random_model(5, cfg)
+    qd, kd = cfg.num_heads * cfg.head_dim, cfg.num_kv_heads * cfg.head_dim
+    layer_shapes = [(qd + 2 * kd, cfg.hidden_size), (cfg.hidden_size, qd),
+                    (2 * cfg.ffn_size, cfg.hidden_size), (cfg.hidden_size, cfg.ffn_size)]
     emb = t["token_embd.weight"]
     wbytes = sum(len(x.data) for n, x in t.items() if n != "token_embd.weight") + \
         len(emb.data) // emb.rows
@@ -349,8 +354,21 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16):
         be.download(out, m.logits)
         assert np.max(np.abs(out - logits)) <= 1e-5 * np.max(np.abs(logits)), \
             "recorded step differs from the eager one"
+        # prefill of a prompt_len-token prompt at position 0 (chunks of 1024
+        # rows, bf16 GEMMs over the dense copies), wall clock per ForwardStep
+        prompt = list(np.random.default_rng(9).integers(0, cfg.vocab_size, prompt_len))
+        be.ForwardStep(prompt, 0)
+        t0 = time.perf_counter()
+        for _ in range(prefill_reps):
+            logits = be.ForwardStep(prompt, 0)
+        pf_ms = (time.perf_counter() - t0) * 1e3 / prefill_reps
+        assert np.all(np.isfinite(logits))
     finally:
         be.Dispose()
+    # prefill FLOPs: 2 per weight value per row, plus causal attention per layer
+    params = sum(r * c for r, c in layer_shapes) * cfg.num_layers
+    pf_flops = 2.0 * prompt_len * params + cfg.num_layers * prefill_flops(0, prompt_len) + \
+        2.0 * cfg.vocab_size * cfg.hidden_size
     gbs = (wbytes + kvbytes) / (ms * 1e-3) / 1e9
     return {"workload": "32-layer hunyuan-dense decode step (hidden 2048, FFN 6144, vocab 120818; "
                         "Q4_K layers, Q6_K embedding/output, synthetic weights), fp16 KV, "
@@ -359,7 +377,14 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16):
             "eager_tokens_per_s": round(1e3 / eager_ms, 1), "eager_ms_per_token": round(eager_ms, 4),
             "weight_bytes": wbytes, "kv_bytes": kvbytes, "gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "submission": "recorded step (hymt_graph_launch); eager = ForwardStep from Python"}
+            "submission": "recorded step (hymt_graph_launch); eager = ForwardStep from Python",
+            "prefill": {"prompt_tokens": prompt_len, "ms": round(pf_ms, 3),
+                        "tokens_per_s": round(prompt_len / (pf_ms * 1e-3), 1),
+                        "tflops": round(pf_flops / (pf_ms * 1e-3) / 1e12, 1),
+                        "frac": round(pf_flops / (pf_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+                        "flops": pf_flops,
+                        "timing": "wall clock per ForwardStep(prompt, 0), mean of "
+                                  f"{prefill_reps}, chunks of 1024 rows"}}
 
 
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):

@@ -99,11 +99,18 @@ SIGNATURES = {
                          ctypes.POINTER(ctypes.c_size_t)],
     "hymt_gemv": [_vp, _vp, _vp, _vp, _i, _vp, ctypes.c_float],
     "hymt_embed": [_vp, _vp, _i, _vp],
+    "hymt_weight_dense": [_vp, _vp],
+    "hymt_gemm": [_vp, _vp, _i, _i, _vp, _i, _vp, _i],
+    "hymt_embed_rows": [_vp, _vp, _vp, _i, _vp],
+    "hymt_rows_rmsnorm": [_vp, _vp, _i, _i, _vp, ctypes.c_float, _vp],
+    "hymt_rows_swiglu": [_vp, _vp, _i, _i, _vp],
+    "hymt_to_bf16": [_vp, _vp, ctypes.c_size_t, _vp],
 }
 
 # weight types (GgmlTensorType codes) and gemv flags, as in include/hymt_hip.h
 W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
 GEMV_ACCUMULATE, GEMV_IN_RMSNORM, GEMV_IN_SWIGLU = 1, 2, 4
+GEMM_ACCUMULATE, GEMM_OUT_BF16 = 1, 2
 
 _lib = None
 _synth = None

@@ -203,14 +203,17 @@ class HipBackend:
         N.check(self._lib.hymt_gemv(self._h, w, x_dev, y_dev, flags, rmsnorm, eps))
 
     # ---- the model: IComputeBackend.LoadModel / ForwardStep (IComputeBackend.cs:25-47)
-    def LoadModel(self, tensors: dict, config, max_tokens: int = 4096, kv_dtype: int = N.BF16):
+    def LoadModel(self, tensors: dict, config, max_tokens: int = 4096, kv_dtype: int = N.BF16,
+                  prefill: bool = True):
         """tensors: GGUF name -> model.Tensor; config: model.ModelConfig.
         Uploads every weight, creates the KV cache, keeps activations on the
-        device (hymt2sharp_amd/model.py)."""
+        device (hymt2sharp_amd/model.py).  prefill: also keep bf16 dense
+        copies of the layer weights so that multi-token calls run as GEMMs."""
         from .model import DeviceModel
         if getattr(self, "_model", None) is not None:
             self._model.free()
-        self._model = DeviceModel(self, config, tensors, max_tokens, kv_dtype)
+            self._model = None
+        self._model = DeviceModel(self, config, tensors, max_tokens, kv_dtype, prefill=prefill)
         return self
 
     def ForwardStep(self, tokens, pos: int) -> np.ndarray:
@@ -223,6 +226,32 @@ class HipBackend:
     def embed(self, w, row: int, out_dev):
         """out = row `row` of W, dequantized (device pointer)."""
         N.check(self._lib.hymt_embed(self._h, w, row, out_dev))
+
+    # ---- prefill: dense weights, GEMMs and row kernels (device pointers)
+    def weight_dense(self, w):
+        """Give W a bf16 dense copy for gemm (synchronous)."""
+        N.check(self._lib.hymt_weight_dense(self._h, w))
+
+    def gemm(self, w, x_dev, m: int, y_dev, row0: int = 0, nrows: int | None = None,
+             accumulate: bool = False, out_bf16: bool = False):
+        """y[m][nrows] (+)= x[m][cols] . W[row0:row0+nrows]^T (x bf16; y fp32 or bf16)."""
+        if nrows is None:
+            nrows = self.weight_info(w)["rows"] - row0
+        flags = (N.GEMM_ACCUMULATE if accumulate else 0) | (N.GEMM_OUT_BF16 if out_bf16 else 0)
+        N.check(self._lib.hymt_gemm(self._h, w, row0, nrows, x_dev, m, y_dev, flags))
+
+    def embed_rows(self, w, rows, out_dev):
+        r = np.ascontiguousarray(rows, dtype=np.int32)
+        N.check(self._lib.hymt_embed_rows(self._h, w, _ptr(r), r.size, out_dev))
+
+    def rows_rmsnorm(self, x_dev, m: int, n: int, norm_w_dev, eps: float, out_dev):
+        N.check(self._lib.hymt_rows_rmsnorm(self._h, x_dev, m, n, norm_w_dev, eps, out_dev))
+
+    def rows_swiglu(self, gu_dev, m: int, n: int, out_dev):
+        N.check(self._lib.hymt_rows_swiglu(self._h, gu_dev, m, n, out_dev))
+
+    def to_bf16(self, x_dev, count: int, out_dev):
+        N.check(self._lib.hymt_to_bf16(self._h, x_dev, count, out_dev))
 
     def stream(self) -> int:
         s = ctypes.c_void_p()

@@ -25,6 +25,8 @@ HIP_SOURCES = {
     "kv_ops.hip": [],
     "gemv.hip": [],
     "weights.cpp": [],
+    "rows.hip": [],
+    "gemm.cpp": [],
 }
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 BUILD_DIR = os.path.join(PKG, "_build")
@@ -64,7 +66,8 @@ def build_hip(extra=()):
     if failed:
         raise RuntimeError("build failed: " + "; ".join(failed))
     tmp = HIP_LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-L/opt/rocm/lib", "-lhipblaslt",
+          "-Wl,-rpath,/opt/rocm/lib", "-o", tmp])
     os.replace(tmp, HIP_LIB)
     return HIP_LIB
 

@@ -525,6 +525,32 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     return hipGetLastError();
 }
 
+// Rows of the matrix, dequantized to fp32: workgroup b writes row
+// rows[b] (or row0 + b when rows is null) at out + b * cols.  Embedding of a
+// prompt (HunyuanDenseModel.Embed's row loop, HunyuanDenseModel.cs:541-556)
+// and the source of the dense copies the prefill GEMMs read.
+template <typename Unit, bool STQ>
+__global__ __launch_bounds__(256) void rows_kernel(WeightDev w, const int *__restrict__ rows, int row0,
+                                                   float *__restrict__ out) {
+    __shared__ uint8_t book[32];
+    if (STQ && threadIdx.x < 32) book[threadIdx.x] = kStqBook[threadIdx.x];
+    __syncthreads();
+    const int row = rows ? rows[blockIdx.x] : row0 + (int)blockIdx.x;
+    float *o = out + (size_t)blockIdx.x * w.cols;
+    for (int u = threadIdx.x; u < w.cols / 32; u += 256) {
+        Unit un;
+        un.load(w, row, u);
+        if constexpr (STQ) un.store(u, book, o);
+        else un.store(u, 0.f, o);
+    }
+}
+
+template <typename Unit, bool STQ>
+hipError_t launch_rows_t(const WeightDev &w, const int *rows, int row0, int n, float *out, hipStream_t s) {
+    hipLaunchKernelGGL((rows_kernel<Unit, STQ>), dim3(n), dim3(256), 0, s, w, rows, row0, out);
+    return hipGetLastError();
+}
+
 template <typename Unit, bool STQ>
 hipError_t launch_embed_t(const WeightDev &w, int row, float *out, hipStream_t s) {
     hipLaunchKernelGGL((embed_kernel<Unit, STQ>), dim3(1), dim3(256), 0, s, w, row, out);
@@ -543,6 +569,20 @@ hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int flags, 
     case kW_Q6_K: return launch_t<UnitQ6_K, false>(w, x, y, flags, nw, eps, s);
     case kW_Q2_0C: return launch_t<UnitQ2_0C, false>(w, x, y, flags, nw, eps, s);
     case kW_STQ1_0: return launch_t<UnitSTQ1_0, true>(w, x, y, flags, nw, eps, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_rows(const WeightDev &w, const int *rows, int row0, int n, float *out, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    switch (w.type) {
+    case kW_F32: return launch_rows_t<UnitF32, false>(w, rows, row0, n, out, s);
+    case kW_F16: return launch_rows_t<UnitF16, false>(w, rows, row0, n, out, s);
+    case kW_Q8_0: return launch_rows_t<UnitQ8_0, false>(w, rows, row0, n, out, s);
+    case kW_Q4_K: return launch_rows_t<UnitQ4_K, false>(w, rows, row0, n, out, s);
+    case kW_Q6_K: return launch_rows_t<UnitQ6_K, false>(w, rows, row0, n, out, s);
+    case kW_Q2_0C: return launch_rows_t<UnitQ2_0C, false>(w, rows, row0, n, out, s);
+    case kW_STQ1_0: return launch_rows_t<UnitSTQ1_0, true>(w, rows, row0, n, out, s);
     default: return hipErrorInvalidValue;
     }
 }

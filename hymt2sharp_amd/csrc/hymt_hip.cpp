@@ -111,6 +111,7 @@ struct hymt_ctx {
     DevBuf part_o, part_ml;
     // staging for host-pointer calls
     DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
+    DevBuf rows_idx;  // token ids of hymt_embed_rows
     HostBuf h_in, h_out;
 
     // stream capture (hymt_graph_begin .. hymt_graph_end)
@@ -299,7 +300,7 @@ int hymt_destroy(hymt_ctx *c) {
         (void)hipStreamSynchronize(c->stream);
         for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->dec_ml,
                           &c->dec_acc, &c->part_o, &c->part_ml, &c->in_q,
-                          &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v})
+                          &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v, &c->rows_idx})
             b->release();
         c->h_in.release();
         c->h_out.release();
@@ -785,6 +786,7 @@ struct hymt_weight {
     hymt::WeightDev dev;
     void *mem = nullptr;
     size_t bytes = 0;
+    uint16_t *dense = nullptr;  // bf16 [rows][cols] copy for the prefill GEMMs (hymt_weight_dense)
 };
 
 int hymt_weight_upload(hymt_ctx *c, int type, int rows, int cols, const void *data, size_t bytes,
@@ -837,6 +839,10 @@ int hymt_weight_free(hymt_ctx *c, hymt_weight *w) {
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
     hipError_t e = hipFree(w->mem);
+    if (w->dense) {
+        const hipError_t e2 = hipFree(w->dense);
+        if (e == hipSuccess) e = e2;
+    }
     delete w;
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipFree: ") + hipGetErrorString(e));
     return HYMT_OK;
@@ -847,7 +853,7 @@ int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size
     if (type) *type = w->dev.type;
     if (rows) *rows = w->dev.rows;
     if (cols) *cols = w->dev.cols;
-    if (device_bytes) *device_bytes = w->bytes;
+    if (device_bytes) *device_bytes = w->bytes + (w->dense ? (size_t)w->dev.rows * w->dev.cols * 2 : 0);
     return HYMT_OK;
 }
 
@@ -877,6 +883,120 @@ int hymt_embed(hymt_ctx *c, const hymt_weight *w, int row, float *out) {
     try {
         HIP_TRY(hipSetDevice(c->device));
         HIP_TRY(hymt::launch_embed(w->dev, row, out, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+// ---- prefill: dense weights, GEMMs and row kernels ----------------------------
+
+int hymt_weight_dense(hymt_ctx *c, hymt_weight *w) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w) return fail(HYMT_E_ARG, "null weight");
+    if (int r = refuse_in_capture(c, "hymt_weight_dense")) return r;
+    if (w->dense) return HYMT_OK;
+    const int rows = w->dev.rows, cols = w->dev.cols;
+    const int chunk = std::max(1, std::min(rows, (int)((64u << 20) / ((size_t)cols * 4))));
+    void *tmp = nullptr;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hipMalloc((void **)&w->dense, (size_t)rows * cols * 2));
+        HIP_TRY(hipMalloc(&tmp, (size_t)chunk * cols * 4));
+        for (int r0 = 0; r0 < rows; r0 += chunk) {
+            const int n = std::min(chunk, rows - r0);
+            HIP_TRY(hymt::launch_rows(w->dev, nullptr, r0, n, (float *)tmp, c->stream));
+            HIP_TRY(hymt::launch_to_bf16((const float *)tmp, (size_t)n * cols, w->dense + (size_t)r0 * cols,
+                                         c->stream));
+        }
+        HIP_TRY(hipStreamSynchronize(c->stream));
+        HIP_TRY(hipFree(tmp));
+    } catch (const HipError &e) {
+        if (tmp) (void)hipFree(tmp);
+        if (w->dense) (void)hipFree(w->dense);
+        w->dense = nullptr;
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_gemm(hymt_ctx *c, const hymt_weight *w, int row0, int nrows, const void *x, int m, void *y, int flags) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or matrix");
+    if (!w->dense) return fail(HYMT_E_STATE, "weight has no dense copy (hymt_weight_dense)");
+    if (flags & ~(HYMT_GEMM_ACCUMULATE | HYMT_GEMM_OUT_BF16)) return fail(HYMT_E_ARG, "unknown gemm flags");
+    if ((flags & HYMT_GEMM_ACCUMULATE) && (flags & HYMT_GEMM_OUT_BF16))
+        return fail(HYMT_E_ARG, "HYMT_GEMM_ACCUMULATE needs an fp32 output");
+    if (row0 < 0 || nrows < 1 || row0 + nrows > w->dev.rows)
+        return fail(HYMT_E_ARG, "rows [" + std::to_string(row0) + ", " + std::to_string(row0 + nrows) +
+                                    ") outside the weight's " + std::to_string(w->dev.rows));
+    if (m < 0) return fail(HYMT_E_ARG, "negative row count");
+    if (int r = refuse_in_capture(c, "hymt_gemm")) return r;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::gemm_bf16(c->stream, w->dense + (size_t)row0 * w->dev.cols, nrows, w->dev.cols,
+                                (const uint16_t *)x, m, y, flags & HYMT_GEMM_OUT_BF16, flags & HYMT_GEMM_ACCUMULATE));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_embed_rows(hymt_ctx *c, const hymt_weight *w, const int32_t *rows, int n, float *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!w || !rows || !out) return fail(HYMT_E_ARG, "null weight, rows or output");
+    if (n < 0) return fail(HYMT_E_ARG, "negative row count");
+    for (int i = 0; i < n; i++)
+        if (rows[i] < 0 || rows[i] >= w->dev.rows)
+            return fail(HYMT_E_ARG, "row " + std::to_string(rows[i]) + " outside [0, " +
+                                        std::to_string(w->dev.rows) + ")");
+    if (int r = refuse_in_capture(c, "hymt_embed_rows")) return r;
+    if (n == 0) return HYMT_OK;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        c->rows_idx.reserve((size_t)n * 4);
+        HIP_TRY(hipMemcpyAsync(c->rows_idx.p, rows, (size_t)n * 4, hipMemcpyHostToDevice, c->stream));
+        HIP_TRY(hymt::launch_rows(w->dev, (const int *)c->rows_idx.p, 0, n, out, c->stream));
+        HIP_TRY(hipStreamSynchronize(c->stream));  // the host array may go once this returns
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_rows_rmsnorm(hymt_ctx *c, const float *x, int m, int n, const float *norm_w, float eps, void *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!x || !norm_w || !out) return fail(HYMT_E_ARG, "null input, weight or output");
+    if (m < 0 || n < 4 || n > 8192 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4 up to 8192");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_rows_rmsnorm(x, m, n, norm_w, eps, (uint16_t *)out, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_rows_swiglu(hymt_ctx *c, const float *gate_up, int m, int n, void *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!gate_up || !out) return fail(HYMT_E_ARG, "null input or output");
+    if (m < 0 || n < 4 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_rows_swiglu(gate_up, m, n, (uint16_t *)out, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_to_bf16(hymt_ctx *c, const float *x, size_t count, void *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!x || !out) return fail(HYMT_E_ARG, "null input or output");
+    if (count % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "count must be a multiple of 4");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_to_bf16(x, count, (uint16_t *)out, c->stream));
     } catch (const HipError &e) {
         return map_hip(e);
     }

@@ -49,5 +49,16 @@ constexpr int kGemvAccumulate = 1, kGemvInRmsNorm = 2, kGemvInSwiGLU = 4;
 hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
                        hipStream_t s);
 hipError_t launch_embed(const WeightDev &w, int row, float *out, hipStream_t s);
+// n rows of W as fp32 rows at out: rows[i] (device array) or row0 + i
+hipError_t launch_rows(const WeightDev &w, const int *rows, int row0, int n, float *out, hipStream_t s);
+// row kernels of the prefill (rows.hip); bf16 outputs are RNE-rounded bits
+hipError_t launch_rows_rmsnorm(const float *x, int m, int n, const float *w, float eps, uint16_t *out,
+                               hipStream_t s);
+hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipStream_t s);
+hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s);
+// y[m][n] (+)= x[m][k] . W[n][k]^T, bf16 operands, fp32 accumulation
+// (gemm.cpp, hipBLASLt); y is fp32 or, with y_bf16, bf16
+hipError_t gemm_bf16(hipStream_t s, const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y,
+                     bool y_bf16, bool accumulate);
 
 }  // namespace hymt

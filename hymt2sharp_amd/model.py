@@ -16,6 +16,20 @@ One decode step of a token at position `pos`:
 q, k and v (and gate and up) of a layer are uploaded as one matrix when
 their types agree (rows concatenated), so each takes one GEMV.  Everything
 stays on the device; only the logits come back.
+
+A call with several tokens runs them as a prefill, in chunks of up to 1024
+rows as Forward chunks a prompt (HunyuanDenseModel.cs:342-355), over bf16
+dense copies of the layer weights (the Vulkan prefill's 16-bit weight
+copies, VulkanBackend.cs:760-880):
+    X = token_embd[tokens]                                  hymt_embed_rows
+    per layer l:
+        XN = bf16 RMSNorm(X, attn_norm)                     hymt_rows_rmsnorm
+        Q, K, V = XN . Wq^T, XN . Wk^T, XN . Wv^T (bf16)    hymt_gemm OUT_BF16
+        AO = causal attention (RoPE, QK norm, append)       hymt_attn_prefill
+        X += bf16(AO) . Wo^T                                hymt_to_bf16, hymt_gemm ACCUMULATE
+        GU = bf16 RMSNorm(X, ffn_norm) . [Wgate; Wup]^T     hymt_rows_rmsnorm, hymt_gemm
+        X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu, hymt_gemm ACCUMULATE
+    logits = Wout RMSNorm(X[last], output_norm)             hymt_gemv IN_RMSNORM
 """
 from __future__ import annotations
 
@@ -52,8 +66,11 @@ class Tensor:
 
 
 class DeviceModel:
-    def __init__(self, be, cfg: ModelConfig, tensors: dict, max_tokens: int, kv_dtype: int = N.BF16):
-        self.be, self.cfg = be, cfg
+    PREFILL_CHUNK = 1024
+
+    def __init__(self, be, cfg: ModelConfig, tensors: dict, max_tokens: int, kv_dtype: int = N.BF16,
+                 prefill: bool = True):
+        self.be, self.cfg, self.prefill_enabled = be, cfg, prefill
         c = cfg
         self._weights, self._bufs = [], []
         be.configure(c.num_heads, c.num_kv_heads, c.head_dim, c.rope_dim, c.rope_base, c.eps)
@@ -79,16 +96,22 @@ class DeviceModel:
             self._weights.extend(out)
             return out
 
+        def dense(ws):
+            if prefill:
+                for w in ws:
+                    be.weight_dense(w)
+            return ws
+
         self.layers = []
         for l in range(c.num_layers):
             p = f"blk.{l}."
             self.layers.append({
                 "attn_norm": vec(p + "attn_norm.weight"), "ffn_norm": vec(p + "ffn_norm.weight"),
                 "q_norm": vec(p + "attn_q_norm.weight"), "k_norm": vec(p + "attn_k_norm.weight"),
-                "qkv": mat(p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"),
-                "o": mat(p + "attn_output.weight")[0],
-                "gate_up": mat(p + "ffn_gate.weight", p + "ffn_up.weight"),
-                "down": mat(p + "ffn_down.weight")[0],
+                "qkv": dense(mat(p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight")),
+                "o": dense(mat(p + "attn_output.weight"))[0],
+                "gate_up": dense(mat(p + "ffn_gate.weight", p + "ffn_up.weight")),
+                "down": dense(mat(p + "ffn_down.weight"))[0],
             })
         self.embd = mat("token_embd.weight")[0]
         # the output projection falls back to the tied embedding (HunyuanDenseModel.cs:419)
@@ -101,6 +124,13 @@ class DeviceModel:
         self.ao = self._buf(qd)
         self.gu = self._buf(2 * c.ffn_size)
         self.logits = self._buf(c.vocab_size)
+        self._pf = None  # prefill activations, allocated on the first prefill
+        # the SwiGLU row kernel reads gate and up from one [m][2F] GEMM output,
+        # so prompts of a model whose gate and up types differ (two matrices)
+        # run as decode steps; so do those of an fp32 cache (the prefill
+        # kernels read 16-bit pages)
+        self.prefill_enabled = prefill and kv_dtype != N.F32 and \
+            all(len(L["gate_up"]) == 1 for L in self.layers)
 
     def _buf(self, n):
         p = self.be.alloc(4 * n)
@@ -130,12 +160,56 @@ class DeviceModel:
             be.gemv(L["down"], self.gu, self.h, accumulate=True, swiglu=True)
         be.gemv(self.out, self.h, self.logits, rmsnorm=self.out_norm, eps=c.eps)
 
+    def _prefill_bufs(self):
+        if self._pf is None:
+            c, C = self.cfg, self.PREFILL_CHUNK
+            H, F, qd, kd = c.hidden_size, c.ffn_size, self.qd, self.kd
+            self._pf = {"x": self._buf(C * H), "xn": self._buf(C * H // 2),
+                        "q": self._buf(C * qd // 2), "k": self._buf(C * kd // 2),
+                        "v": self._buf(C * kd // 2), "ao": self._buf(C * qd),
+                        "ao16": self._buf(C * qd // 2), "gu": self._buf(C * 2 * F),
+                        "act": self._buf(C * F // 2)}
+        return self._pf
+
+    def prefill(self, tokens, pos: int):
+        """Enqueue one prefill chunk (len(tokens) <= PREFILL_CHUNK) at
+        positions [pos, pos + len); the last row's logits land in self.logits."""
+        be, c, B = self.be, self.cfg, self._prefill_bufs()
+        m, H, F, qd, kd = len(tokens), c.hidden_size, c.ffn_size, self.qd, self.kd
+        assert 0 < m <= self.PREFILL_CHUNK
+        be.embed_rows(self.embd, tokens, B["x"])
+        for l, L in enumerate(self.layers):
+            be.rows_rmsnorm(B["x"], m, H, L["attn_norm"], c.eps, B["xn"])
+            qkv = L["qkv"]
+            outs = (B["q"], B["k"], B["v"])
+            if len(qkv) == 1:
+                for (r0, n), y in zip(((0, qd), (qd, kd), (qd + kd, kd)), outs):
+                    be.gemm(qkv[0], B["xn"], m, y, row0=r0, nrows=n, out_bf16=True)
+            else:
+                for w, y in zip(qkv, outs):
+                    be.gemm(w, B["xn"], m, y, out_bf16=True)
+            be.prefill_dev(l, pos, m, B["q"], B["k"], B["v"], N.BF16, L["q_norm"], L["k_norm"], B["ao"])
+            be.to_bf16(B["ao"], m * qd, B["ao16"])
+            be.gemm(L["o"], B["ao16"], m, B["x"], accumulate=True)
+            be.rows_rmsnorm(B["x"], m, H, L["ffn_norm"], c.eps, B["xn"])
+            be.gemm(L["gate_up"][0], B["xn"], m, B["gu"])
+            be.rows_swiglu(B["gu"], m, F, B["act"])
+            be.gemm(L["down"], B["act"], m, B["x"], accumulate=True)
+        be.gemv(self.out, B["x"] + 4 * (m - 1) * H, self.logits, rmsnorm=self.out_norm, eps=c.eps)
+
     def forward(self, tokens, pos: int) -> np.ndarray:
         """ForwardStep (IComputeBackend.cs:40-47): the tokens at positions
-        pos, pos+1, ..., one decode step each; returns the last token's logits.
-        (A prompt runs token by token here: the prefill GEMMs are not built.)"""
-        for i, t in enumerate(tokens):
-            self.step(int(t), pos + i)
+        pos, pos+1, ...; returns the last token's logits.  One token is a
+        decode step; several run as prefill chunks when the dense copies were
+        made (LoadModel(prefill=True)), else as decode steps one by one."""
+        tokens = [int(t) for t in tokens]
+        if len(tokens) > 1 and self.prefill_enabled:
+            for i in range(0, len(tokens), self.PREFILL_CHUNK):
+                chunk = tokens[i:i + self.PREFILL_CHUNK]
+                self.prefill(chunk, pos + i)
+        else:
+            for i, t in enumerate(tokens):
+                self.step(t, pos + i)
         out = np.empty(self.cfg.vocab_size, np.float32)
         self.be.download(out, self.logits)
         return out

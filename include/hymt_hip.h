@@ -265,6 +265,44 @@ int hymt_gemv(hymt_ctx *ctx, const hymt_weight *w, const float *x, float *y, int
  * pointer; the call only enqueues work and may be recorded. */
 int hymt_embed(hymt_ctx *ctx, const hymt_weight *w, int row, float *out);
 
+/* ---- prefill: dense weights, GEMMs and row kernels ----------------------------
+ * The prefill half of ForwardStep (HunyuanDenseModel.Forward's prefill blocks,
+ * HunyuanDenseModel.Prefill.cs; the Vulkan prefill sequence of
+ * VulkanBackend.cs:760-880, which keeps 16-bit dense copies of the layer
+ * weights and runs GEMMs over the prompt's rows).  Matrices are row-major;
+ * bf16 values are uint16 bit patterns rounded to nearest even. */
+
+/* Give the weight a bf16 [rows][cols] dense copy of its dequantized values
+ * (held until hymt_weight_free; 2 bytes per value of device memory).
+ * Synchronous; not recordable. */
+int hymt_weight_dense(hymt_ctx *ctx, hymt_weight *w);
+
+/* y[m][nrows] = x[m][cols] . W[row0 : row0+nrows][cols]^T over the dense
+ * copy, bf16 operands and fp32 accumulation (the Gemm calls of
+ * VulkanBackend.cs:782-856).  y is fp32 [m][nrows], bf16 with
+ * HYMT_GEMM_OUT_BF16, or fp32 accumulated into (y +=, the residual add) with
+ * HYMT_GEMM_ACCUMULATE.  x, y device pointers; not recordable. */
+#define HYMT_GEMM_ACCUMULATE 1
+#define HYMT_GEMM_OUT_BF16 2
+int hymt_gemm(hymt_ctx *ctx, const hymt_weight *w, int row0, int nrows, const void *x, int m, void *y,
+              int flags);
+
+/* out[i][cols] = row rows[i] of W dequantized, fp32 (the prompt's embedding,
+ * HunyuanDenseModel.Embed, HunyuanDenseModel.cs:494-557).  rows is a host
+ * array, out a device pointer; returns when the rows are written. */
+int hymt_embed_rows(hymt_ctx *ctx, const hymt_weight *w, const int32_t *rows, int n, float *out);
+
+/* out[i] = bf16(x[i] / sqrt(mean(x[i]^2) + eps) * norm_w) for m rows of n
+ * fp32 values (Ops.RmsNorm, Ops.cs:12-90).  n a multiple of 4 up to 8192. */
+int hymt_rows_rmsnorm(hymt_ctx *ctx, const float *x, int m, int n, const float *norm_w, float eps, void *out);
+
+/* out[i][j] = bf16(g / (1 + exp(-g)) * u), g = gate_up[i][j], u =
+ * gate_up[i][n + j] (Ops.SiLUMul, Ops.cs:999-1052). */
+int hymt_rows_swiglu(hymt_ctx *ctx, const float *gate_up, int m, int n, void *out);
+
+/* out[i] = bf16(x[i]) for count fp32 values (count a multiple of 4). */
+int hymt_to_bf16(hymt_ctx *ctx, const float *x, size_t count, void *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,188 @@
+"""Prefill side of ForwardStep on the GPU through the C ABI: the row kernels
+(RMSNorm, SwiGLU and rounding into bf16), the dense bf16 weight copies, the
+bf16 GEMMs (hipBLASLt) and the whole multi-token ForwardStep against the
+oracle's decode steps over the same tokens (oracle/model.py).
+
+Bounds: row kernels within one bf16 ulp of the oracle's fp32/double value
+rounded to bf16 (the fp32 sums may fall either side of a rounding edge);
+rounding of fp32 input bit-exact; dense copies bit-exact for all but a few
+values at rounding edges; GEMMs within 1e-5 of sum |x w| per output against
+a double product of the same bf16 operands.  Prefill logits: the weights and
+activations enter the GEMMs as bf16 (relative error 2^-9 each), so the
+logits carry a stated bound of 1.5e-2 of the largest logit after two layers
+(measured 1e-3 to 5e-3), against 1e-4 for the fp32 decode path."""
+import numpy as np
+import pytest
+
+from hymt2sharp_amd import HipBackend
+from hymt2sharp_amd import _native as N
+from hymt2sharp_amd import synth as S
+from hymt2sharp_amd.model import DeviceModel, ModelConfig
+from oracle import oracle as O
+from oracle.model import OracleModel
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_bits(x):
+    return S.f32_to_bf16_bits(np.asarray(x, np.float32))
+
+
+def bf16_val(bits):
+    return (np.asarray(bits, np.uint32) << 16).view(np.float32)
+
+
+def ulp_diff(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    return np.abs(a - b)  # same-sign values: one bit pattern step = one ulp
+
+
+@pytest.fixture
+def be(hip_available):
+    b = HipBackend(0)
+    yield b
+    b.Dispose()
+
+
+def dev(be, arr):
+    p = be.alloc(max(arr.nbytes, 4))
+    be.upload(p, arr)
+    return p
+
+
+def test_rows_rmsnorm_swiglu_and_rounding(be):
+    rng = np.random.default_rng(3)
+    m, n = 37, 2048
+    x = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    dx, dw, do = dev(be, x), dev(be, w), be.alloc(m * n * 2)
+    be.rows_rmsnorm(dx, m, n, dw, 1e-5, do)
+    be.sync()
+    got = be.download(np.empty((m, n), np.uint16), do)
+    ref = bf16_bits(O.rmsnorm(x, w, 1e-5))
+    assert ulp_diff(got, ref).max() <= 1 and np.mean(got == ref) > 0.99
+    # SwiGLU: gate then up per row
+    F = 6144
+    gu = (rng.standard_normal((m, 2 * F)) * 4).astype(np.float32)
+    dgu, dact = dev(be, gu), be.alloc(m * F * 2)
+    be.rows_swiglu(dgu, m, F, dact)
+    be.sync()
+    got = be.download(np.empty((m, F), np.uint16), dact)
+    g, u = gu[:, :F].astype(np.float64), gu[:, F:].astype(np.float64)
+    ref = bf16_bits((g / (1 + np.exp(-g)) * u).astype(np.float32))
+    assert ulp_diff(got, ref).max() <= 1 and np.mean(got == ref) > 0.99
+    # rounding: bit-exact RNE (Ops.cs:664-665)
+    be.to_bf16(dx, m * n, do)
+    be.sync()
+    got = be.download(np.empty((m, n), np.uint16), do)
+    assert np.array_equal(got, bf16_bits(x))
+    for p in (dx, dw, do, dgu, dact):
+        be.free(p)
+
+
+@pytest.mark.parametrize("wtype", [N.W_Q4_K, N.W_Q6_K, N.W_Q8_0, N.W_Q2_0C, N.W_STQ1_0, N.W_F16])
+def test_dense_copy_and_embed_rows(be, wtype):
+    rows, cols = 300, 2048
+    raw = S.random_weight(500 + wtype, wtype, rows, cols)
+    full = O.dequant(wtype, raw, rows, cols)
+    w = be.weight_upload(wtype, rows, cols, raw)
+    try:
+        be.weight_dense(w)
+        be.weight_dense(w)  # a second call keeps the copy
+        info = be.weight_info(w)
+        assert info["device_bytes"] >= rows * cols * 2
+        ids = np.array([0, 299, 7, 7, 150], np.int32)
+        out = be.alloc(ids.size * cols * 4)
+        be.embed_rows(w, ids, out)
+        got = be.download(np.empty((ids.size, cols), np.float32), out)
+        assert np.all(np.abs(got - full[ids]) <= 2e-7 * np.abs(full[ids]).max(axis=1, keepdims=True))
+        with pytest.raises(N.ArgumentError):
+            be.embed_rows(w, np.array([rows], np.int32), out)
+        be.free(out)
+    finally:
+        be.weight_free(w)
+
+
+@pytest.mark.parametrize("m", [1, 37, 256])
+def test_gemm_matches_double_product(be, m):
+    rows, cols = 640, 2048
+    raw = S.random_weight(900 + m, N.W_Q4_K, rows, cols)
+    wd = bf16_val(bf16_bits(O.dequant(N.W_Q4_K, raw, rows, cols))).astype(np.float64)
+    rng = np.random.default_rng(m)
+    xb = bf16_bits(rng.standard_normal((m, cols)).astype(np.float32))
+    x = bf16_val(xb).astype(np.float64)
+    y0 = rng.standard_normal((m, rows)).astype(np.float32)
+    w = be.weight_upload(N.W_Q4_K, rows, cols, raw)
+    be.weight_dense(w)
+    dxb, dy, dy16 = dev(be, xb), dev(be, y0), be.alloc(m * rows * 2)
+    try:
+        mag = np.abs(x) @ np.abs(wd).T
+        ref = x @ wd.T
+        # fp32 out, all rows
+        be.gemm(w, dxb, m, dy)
+        be.sync()
+        got = be.download(np.empty((m, rows), np.float32), dy)
+        assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-6)
+        # accumulate into y
+        be.upload(dy, y0)
+        be.gemm(w, dxb, m, dy, accumulate=True)
+        be.sync()
+        got = be.download(np.empty((m, rows), np.float32), dy)
+        assert np.all(np.abs(got - (ref + y0)) <= 1e-5 * (mag + np.abs(y0)) + 1e-6)
+        # a row range, bf16 out
+        be.gemm(w, dxb, m, dy16, row0=128, nrows=256, out_bf16=True)
+        be.sync()
+        got = bf16_val(be.download(np.empty((m, 256), np.uint16), dy16)).astype(np.float64)
+        sub, smag = ref[:, 128:384], mag[:, 128:384]
+        assert np.all(np.abs(got - sub) <= 2.0 ** -8 * np.abs(sub) + 1e-5 * smag + 1e-6)
+        with pytest.raises(N.ArgumentError):
+            be.gemm(w, dxb, m, dy, row0=600, nrows=64)
+        with pytest.raises(N.ArgumentError):
+            be.gemm(w, dxb, m, dy, accumulate=True, out_bf16=True)
+    finally:
+        for p in (dxb, dy, dy16):
+            be.free(p)
+        be.weight_free(w)
+
+
+def test_gemm_needs_dense_copy(be):
+    raw = S.random_weight(1, N.W_Q8_0, 64, 2048)
+    w = be.weight_upload(N.W_Q8_0, 64, 2048, raw)
+    d = be.alloc(64 * 2048 * 4)
+    try:
+        with pytest.raises(N.InvalidOperationError):
+            be.gemm(w, d, 1, d)
+    finally:
+        be.free(d)
+        be.weight_free(w)
+
+
+CFG = ModelConfig(num_layers=2, hidden_size=2048, ffn_size=6144, num_heads=16, num_kv_heads=4,
+                  head_dim=128, vocab_size=512, rope_base=10000.0, rope_dim=128, eps=1e-5)
+PREFILL_BOUND = 1.5e-2
+
+
+@pytest.mark.parametrize("case", [
+    dict(seed=3, types={"attn": [N.W_Q4_K, N.W_Q8_0], "ffn": [N.W_Q6_K, N.W_Q2_0C],
+                        "embd": N.W_Q6_K, "out": N.W_STQ1_0}, kv=N.BF16, m=40, chunk=16),
+    dict(seed=4, types={"attn": N.W_STQ1_0, "ffn": N.W_Q4_K, "embd": N.W_Q8_0}, kv=N.F16, m=70,
+         chunk=1024, tied=True),
+])
+def test_prefill_forward_matches_oracle(be, monkeypatch, case):
+    monkeypatch.setattr(DeviceModel, "PREFILL_CHUNK", case["chunk"])
+    t = S.random_model(case["seed"], CFG, case["types"], tied=case.get("tied", False))
+    om = OracleModel(CFG, t, 128, case["kv"])
+    be.LoadModel(t, CFG, max_tokens=128, kv_dtype=case["kv"])
+    toks = list(np.random.default_rng(case["seed"]).integers(0, CFG.vocab_size, case["m"]))
+    got = be.ForwardStep(toks, 0)
+    ref = om.forward(toks, 0)
+    err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    print(f"prefill m={case['m']} rel {err:.2e}", flush=True)
+    assert err <= PREFILL_BOUND
+    # the K/V rows the prefill wrote: the next decode step reads all of them
+    got = be.ForwardStep([11], case["m"])
+    ref = om.step(11, case["m"])
+    err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    print(f"decode after prefill rel {err:.2e}", flush=True)
+    assert err <= PREFILL_BOUND
