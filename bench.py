@@ -354,7 +354,7 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
         be.download(out, m.logits)
         assert np.max(np.abs(out - logits)) <= 1e-5 * np.max(np.abs(logits)), \
             "recorded step differs from the eager one"
-        # prefill of a prompt_len-token prompt at position 0 (chunks of 1024
+        # prefill of a prompt_len-token prompt at position 0 (chunks of DeviceModel.PREFILL_CHUNK
         # rows, bf16 GEMMs over the dense copies), wall clock per ForwardStep
         prompt = list(np.random.default_rng(9).integers(0, cfg.vocab_size, prompt_len))
         be.ForwardStep(prompt, 0)
@@ -384,7 +384,7 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
                         "frac": round(pf_flops / (pf_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                         "flops": pf_flops,
                         "timing": "wall clock per ForwardStep(prompt, 0), mean of "
-                                  f"{prefill_reps}, chunks of 1024 rows"}}
+                                  f"{prefill_reps}, chunks of 2048 rows"}}
 
 
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):

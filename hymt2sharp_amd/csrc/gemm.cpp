@@ -57,7 +57,52 @@ hipError_t as_hip(hipblasStatus_t st) {
     }
 }
 
-hipError_t make_plan(DeviceState &d, int n, int k, int m, bool y_bf16, bool acc, Plan &p) {
+constexpr int kCandidates = 8;
+
+hipError_t time_candidates(DeviceState &d, const Plan &p, const hipblasLtMatmulHeuristicResult_t *res, int found,
+                           const uint16_t *W, const uint16_t *x, int n, int m, bool y_bf16, bool acc,
+                           hipStream_t s, int &best) {
+    void *scratch = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipMalloc(&scratch, (size_t)n * m * (y_bf16 ? 2 : 4));
+    if (e == hipSuccess) e = hipMemsetAsync(scratch, 0, (size_t)n * m * (y_bf16 ? 2 : 4), s);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    const float alpha = 1.0f, beta = acc ? 1.0f : 0.0f;
+    float best_ms = 0.f;
+    bool have = false;
+    best = 0;
+    for (int i = 0; i < found && e == hipSuccess; i++) {
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspace) continue;
+        auto run = [&]() {
+            return hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.a, x, p.b, &beta, scratch, p.c, scratch, p.c,
+                                   &res[i].algo, d.workspace, res[i].workspaceSize, s);
+        };
+        if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; a candidate that fails is skipped
+        e = hipEventRecord(e0, s);
+        for (int r = 0; r < 3 && e == hipSuccess; r++)
+            if (run() != HIPBLAS_STATUS_SUCCESS) e = hipErrorUnknown;
+        if (e == hipSuccess) e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e == hipSuccess && (!have || ms < best_ms)) {
+            have = true;
+            best_ms = ms;
+            best = i;
+        }
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (scratch) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(scratch);
+    }
+    return e;
+}
+
+hipError_t make_plan(DeviceState &d, int n, int k, int m, bool y_bf16, bool acc, const uint16_t *W,
+                     const uint16_t *x, hipStream_t s, Plan &p) {
     const hipDataType yt = y_bf16 ? HIP_R_16BF : HIP_R_32F;
     hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
     const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
@@ -74,19 +119,29 @@ hipError_t make_plan(DeviceState &d, int n, int k, int m, bool y_bf16, bool acc,
     if (st == HIPBLAS_STATUS_SUCCESS)
         st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
                                                    sizeof(wsmax));
-    hipblasLtMatmulHeuristicResult_t res[1];
+    hipblasLtMatmulHeuristicResult_t res[kCandidates];
     int found = 0;
     if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulAlgoGetHeuristic(d.handle, p.desc, p.a, p.b, p.c, p.c, pref, 1, res, &found);
+        st = hipblasLtMatmulAlgoGetHeuristic(d.handle, p.desc, p.a, p.b, p.c, p.c, pref, kCandidates, res, &found);
     if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    (void)acc;
     if (st == HIPBLAS_STATUS_SUCCESS && found < 1) st = HIPBLAS_STATUS_NOT_SUPPORTED;
     if (st != HIPBLAS_STATUS_SUCCESS) {
         destroy_plan(p);
         return as_hip(st);
     }
-    p.algo = res[0].algo;
-    p.ws = res[0].workspaceSize;
+    int best = 0;
+    if (found > 1) {
+        // The heuristic's first choice is not always the fastest at these
+        // shapes: time each candidate once on the call's operands, writing a
+        // scratch output (beta = 0 or 1 alike), and keep the fastest.
+        hipError_t e = time_candidates(d, p, res, found, W, x, n, m, y_bf16, acc, s, best);
+        if (e != hipSuccess) {
+            destroy_plan(p);
+            return e;
+        }
+    }
+    p.algo = res[best].algo;
+    p.ws = res[best].workspaceSize;
     return hipSuccess;
 }
 
@@ -117,7 +172,7 @@ hipError_t gemm_bf16(hipStream_t s, const uint16_t *W, int n, int k, const uint1
     auto it = d.plans.find(key);
     if (it == d.plans.end()) {
         Plan p;
-        e = make_plan(d, n, k, m, y_bf16, accumulate, p);
+        e = make_plan(d, n, k, m, y_bf16, accumulate, W, x, s, p);
         if (e != hipSuccess) return e;
         it = d.plans.emplace(key, p).first;
     }

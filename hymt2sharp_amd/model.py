@@ -17,8 +17,10 @@ q, k and v (and gate and up) of a layer are uploaded as one matrix when
 their types agree (rows concatenated), so each takes one GEMV.  Everything
 stays on the device; only the logits come back.
 
-A call with several tokens runs them as a prefill, in chunks of up to 1024
-rows as Forward chunks a prompt (HunyuanDenseModel.cs:342-355), over bf16
+A call with several tokens runs them as a prefill, in chunks of up to 2048
+rows (Forward chunks a prompt by 1024, HunyuanDenseModel.cs:342-355; the
+result does not depend on the chunking, and 2048-row GEMMs fill the chip
+better), over bf16
 dense copies of the layer weights (the Vulkan prefill's 16-bit weight
 copies, VulkanBackend.cs:760-880):
     X = token_embd[tokens]                                  hymt_embed_rows
@@ -66,7 +68,7 @@ class Tensor:
 
 
 class DeviceModel:
-    PREFILL_CHUNK = 1024
+    PREFILL_CHUNK = 2048
 
     def __init__(self, be, cfg: ModelConfig, tensors: dict, max_tokens: int, kv_dtype: int = N.BF16,
                  prefill: bool = True):
