@@ -22,8 +22,10 @@ decode call (its split kernel and its merge kernel, back to back) against
 8 TB/s with the same events; `traffic` is read from profiles/traffic.json
 (rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when present.  `prefill`
 carries the prefill TFLOP/s with its own MFMA roofline; `config1`, `config4`
-and `config5` are the other configurations; `cpu_baseline` is the C oracle
-(port of Ops.cs) on this host's cores.
+and `config5` are the other configurations; `gemv` times the weight GEMVs at
+the decode step's shapes; `model` is the whole 32-layer hunyuan-dense model
+(decode tokens/s at position 4096, prompt prefill tokens/s); `cpu_baseline`
+is the C oracle (port of Ops.cs) on this host's cores.
 """
 from __future__ import annotations
 
