@@ -84,6 +84,7 @@ SIGNATURES = {
     "hymt_kv_read": [_vp, _i, _i, _i, _vp, _vp],
     "hymt_attn_decode": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_attn_prefill": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, ctypes.c_uint],
+    "hymt_attn_prefill_ld": [_vp, _i, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_sync": [_vp],
     "hymt_get_stream": [_vp, ctypes.POINTER(_vp)],
     "hymt_dev_alloc": [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)],

@@ -156,6 +156,11 @@ class HipBackend:
         N.check(self._lib.hymt_attn_prefill(self._h, layer, pos, seq, q, k, v, io_dtype, qnw, knw,
                                             out, N.FLAG_DEVICE_PTRS))
 
+    def prefill_dev_ld(self, layer, pos, seq, q, q_ld, k, v, kv_ld, io_dtype, qnw, knw, out):
+        """prefill_dev over rows q_ld (k, v: kv_ld) elements apart."""
+        N.check(self._lib.hymt_attn_prefill_ld(self._h, layer, pos, seq, q, q_ld, k, v, kv_ld, io_dtype,
+                                               qnw, knw, out, N.FLAG_DEVICE_PTRS))
+
     def alloc(self, nbytes: int) -> int:
         p = ctypes.c_void_p()
         N.check(self._lib.hymt_dev_alloc(self._h, nbytes, ctypes.byref(p)))

@@ -97,6 +97,7 @@ struct PrepArgs {
     int rope_half, rope_dim;
     int io_bf16;
     float eps;
+    int kv_ld;          // elements from one k (and v) row to the next, >= Hkv*D
 };
 
 struct FlashArgs {
@@ -117,6 +118,7 @@ struct FlashArgs {
     int npairs;         // block pairs (b, nb16-1-b), b < npairs
     int cap;            // max kv tiles per work item
     int items_per_kvh;  // work items per kv head
+    int q_ld;           // elements from one q row to the next, >= Hq*D
 };
 
 // Number of kv tiles (pages) the 16-row q block b attends to.

@@ -554,9 +554,10 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
     return HYMT_OK;
 }
 
-int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, const void *k,
-                      const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
-                      unsigned flags) {
+// q_ld / kv_ld: elements from one q (k, v) row to the next; 0 = packed rows
+static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q, int q_ld, const void *k,
+                        const void *v, int kv_ld, int io_dtype, const float *qnw, const float *knw, float *out,
+                        unsigned flags) {
     if (int r = check_ctx(c, true, false)) return r;
     if (layer < 0 || layer >= c->layers || pos < 0 || seq <= 0 || !q || !k || !v || !out ||
         (io_dtype != HYMT_F32 && io_dtype != HYMT_BF16))
@@ -602,6 +603,7 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         p.rope_dim = c->rope_dim;
         p.io_bf16 = io_dtype == HYMT_BF16;
         p.eps = c->eps;
+        p.kv_ld = kv_ld ? kv_ld : c->kv_heads * (int)D;
         HIP_TRY(launch_prefill_prep(c->kv_dtype, p, c->stream));
 
         FlashArgs f;
@@ -622,6 +624,7 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         f.io_bf16 = io_dtype == HYMT_BF16;
         f.eps = c->eps;
         f.qscale = 1.4426950408889634f / sqrtf((float)D);
+        f.q_ld = q_ld ? q_ld : c->heads * (int)D;
         f.nb16 = (seq + 15) / 16;
         f.npairs = (f.nb16 + 1) / 2;
         // Work items: split the kv range of block pairs only when there are
@@ -663,6 +666,23 @@ int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, c
         return fail(HYMT_E_CAPACITY, e.what());
     }
     return HYMT_OK;
+}
+
+int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, const void *k,
+                      const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
+                      unsigned flags) {
+    return prefill_impl(c, layer, pos, seq, q, 0, k, v, 0, io_dtype, qnw, knw, out, flags);
+}
+
+int hymt_attn_prefill_ld(hymt_ctx *c, int layer, int pos, int seq, const void *q, int q_ld, const void *k,
+                         const void *v, int kv_ld, int io_dtype, const float *qnw, const float *knw,
+                         float *out, unsigned flags) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (!(flags & HYMT_FLAG_DEVICE_PTRS))
+        return fail(HYMT_E_ARG, "hymt_attn_prefill_ld takes device pointers (HYMT_FLAG_DEVICE_PTRS)");
+    if (q_ld < c->heads * c->head_dim || kv_ld < c->kv_heads * c->head_dim || q_ld % 8 || kv_ld % 8)
+        return fail(HYMT_E_ARG, "row strides must cover a row and be multiples of 8 elements");
+    return prefill_impl(c, layer, pos, seq, q, q_ld, k, v, kv_ld, io_dtype, qnw, knw, out, flags);
 }
 
 int hymt_sync(hymt_ctx *c) {

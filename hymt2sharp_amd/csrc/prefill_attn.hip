@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     const int phys = a.tab[pstart / P];
     const size_t page_base = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
     const int d0 = 8 * c, rh = a.rope_half;
-    const size_t src = (size_t)mc * Hkv * D + (size_t)kvh * D + d0;
+    const size_t src = (size_t)mc * a.kv_ld + (size_t)kvh * D + d0;
 
     float x[8], v[8], cs[8], sn[8], gw[8];
     load8_in(a.k, src, a.io_bf16, x);
@@ -331,7 +331,7 @@ __device__ __forceinline__ void q_load(const FlashArgs &a, int h, const int (&ro
         const int row0 = rowq[qq] + c;
         ok[qq] = okq[qq] && row0 < a.seq;
         const int row = min(row0, a.seq - 1);
-        const size_t base = (size_t)row * a.heads * D + (size_t)h * D + 8 * grp;
+        const size_t base = (size_t)row * a.q_ld + (size_t)h * D + 8 * grp;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             if (IN_BF16) {

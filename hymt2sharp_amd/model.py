@@ -26,8 +26,8 @@ copies, VulkanBackend.cs:760-880):
     X = token_embd[tokens]                                  hymt_embed_rows
     per layer l:
         XN = bf16 RMSNorm(X, attn_norm)                     hymt_rows_rmsnorm
-        Q, K, V = XN . Wq^T, XN . Wk^T, XN . Wv^T (bf16)    hymt_gemm OUT_BF16
-        AO = causal attention (RoPE, QK norm, append)       hymt_attn_prefill
+        [Q|K|V] = XN . [Wq; Wk; Wv]^T (bf16)                hymt_gemm OUT_BF16
+        AO = causal attention (RoPE, QK norm, append)       hymt_attn_prefill_ld
         X += bf16(AO) . Wo^T                                hymt_to_bf16, hymt_gemm ACCUMULATE
         GU = bf16 RMSNorm(X, ffn_norm) . [Wgate; Wup]^T     hymt_rows_rmsnorm, hymt_gemm
         X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu, hymt_gemm ACCUMULATE
@@ -167,6 +167,7 @@ class DeviceModel:
             c, C = self.cfg, self.PREFILL_CHUNK
             H, F, qd, kd = c.hidden_size, c.ffn_size, self.qd, self.kd
             self._pf = {"x": self._buf(C * H), "xn": self._buf(C * H // 2),
+                        "qkv": self._buf(C * (qd + 2 * kd) // 2),
                         "q": self._buf(C * qd // 2), "k": self._buf(C * kd // 2),
                         "v": self._buf(C * kd // 2), "ao": self._buf(C * qd),
                         "ao16": self._buf(C * qd // 2), "gu": self._buf(C * 2 * F),
@@ -183,14 +184,17 @@ class DeviceModel:
         for l, L in enumerate(self.layers):
             be.rows_rmsnorm(B["x"], m, H, L["attn_norm"], c.eps, B["xn"])
             qkv = L["qkv"]
-            outs = (B["q"], B["k"], B["v"])
             if len(qkv) == 1:
-                for (r0, n), y in zip(((0, qd), (qd, kd), (qd + kd, kd)), outs):
-                    be.gemm(qkv[0], B["xn"], m, y, row0=r0, nrows=n, out_bf16=True)
+                # one GEMM into [m][q|k|v]; the attention reads the column ranges
+                ld = qd + 2 * kd
+                be.gemm(qkv[0], B["xn"], m, B["qkv"], out_bf16=True)
+                be.prefill_dev_ld(l, pos, m, B["qkv"], ld, B["qkv"] + 2 * qd, B["qkv"] + 2 * (qd + kd),
+                                  ld, N.BF16, L["q_norm"], L["k_norm"], B["ao"])
             else:
-                for w, y in zip(qkv, outs):
+                for w, y in zip(qkv, (B["q"], B["k"], B["v"])):
                     be.gemm(w, B["xn"], m, y, out_bf16=True)
-            be.prefill_dev(l, pos, m, B["q"], B["k"], B["v"], N.BF16, L["q_norm"], L["k_norm"], B["ao"])
+                be.prefill_dev(l, pos, m, B["q"], B["k"], B["v"], N.BF16, L["q_norm"], L["k_norm"],
+                               B["ao"])
             be.to_bf16(B["ao"], m * qd, B["ao16"])
             be.gemm(L["o"], B["ao16"], m, B["x"], accumulate=True)
             be.rows_rmsnorm(B["x"], m, H, L["ffn_norm"], c.eps, B["xn"])

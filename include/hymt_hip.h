@@ -184,6 +184,16 @@ int hymt_attn_prefill(hymt_ctx *ctx, int layer, int pos, int seq, const void *q,
                       const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
                       unsigned flags);
 
+/* hymt_attn_prefill over rows that are not packed: row j of q starts at
+ * q + j*q_ld elements, of k and v at k + j*kv_ld and v + j*kv_ld (q_ld >=
+ * heads*head_dim, kv_ld >= kv_heads*head_dim, both multiples of 8).  Lets
+ * q, k and v be column ranges of one fused [seq][q|k|v] projection output,
+ * as the Vulkan prefill reads its qkv buffer (pf_kvprep / pf_fa32 over
+ * _pfQkv, VulkanBackend.cs:786-802).  Device pointers only. */
+int hymt_attn_prefill_ld(hymt_ctx *ctx, int layer, int pos, int seq, const void *q, int q_ld, const void *k,
+                         const void *v, int kv_ld, int io_dtype, const float *qnw, const float *knw,
+                         float *out, unsigned flags);
+
 /* Wait for all work on the context's stream. */
 int hymt_sync(hymt_ctx *ctx);
 

@@ -17,7 +17,7 @@ import pytest
 from hymt2sharp_amd import HipBackend
 from hymt2sharp_amd import _native as N
 from hymt2sharp_amd import synth as S
-from hymt2sharp_amd.model import DeviceModel, ModelConfig
+from hymt2sharp_amd.model import DeviceModel, ModelConfig, Tensor
 from oracle import oracle as O
 from oracle.model import OracleModel
 
@@ -165,13 +165,18 @@ PREFILL_BOUND = 1.5e-2
 
 @pytest.mark.parametrize("case", [
     dict(seed=3, types={"attn": [N.W_Q4_K, N.W_Q8_0], "ffn": [N.W_Q6_K, N.W_Q2_0C],
-                        "embd": N.W_Q6_K, "out": N.W_STQ1_0}, kv=N.BF16, m=40, chunk=16),
+                        "embd": N.W_Q6_K, "out": N.W_STQ1_0}, kv=N.BF16, m=40, chunk=16,
+         v_override=N.W_F16),
     dict(seed=4, types={"attn": N.W_STQ1_0, "ffn": N.W_Q4_K, "embd": N.W_Q8_0}, kv=N.F16, m=70,
          chunk=1024, tied=True),
 ])
 def test_prefill_forward_matches_oracle(be, monkeypatch, case):
     monkeypatch.setattr(DeviceModel, "PREFILL_CHUNK", case["chunk"])
     t = S.random_model(case["seed"], CFG, case["types"], tied=case.get("tied", False))
+    if "v_override" in case:  # layer 1's q/k/v types differ: three GEMMs, packed prefill
+        name = "blk.1.attn_v.weight"
+        r, c = t[name].rows, t[name].cols
+        t[name] = Tensor(case["v_override"], r, c, S.random_weight(77, case["v_override"], r, c))
     om = OracleModel(CFG, t, 128, case["kv"])
     be.LoadModel(t, CFG, max_tokens=128, kv_dtype=case["kv"])
     toks = list(np.random.default_rng(case["seed"]).integers(0, CFG.vocab_size, case["m"]))
@@ -186,3 +191,38 @@ def test_prefill_forward_matches_oracle(be, monkeypatch, case):
     err = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
     print(f"decode after prefill rel {err:.2e}", flush=True)
     assert err <= PREFILL_BOUND
+
+
+def test_strided_prefill_equals_packed(be):
+    """q, k, v as column ranges of one [seq][q|k|v] buffer give the same
+    outputs and cache rows as packed arrays."""
+    H, KV, D, seq = 16, 4, 128, 70
+    ld = (H + 2 * KV) * D
+    rng = np.random.default_rng(5)
+    qkv = bf16_bits((rng.standard_normal((seq, ld)) / np.sqrt(D)).astype(np.float32))
+    q = np.ascontiguousarray(qkv[:, :H * D])
+    k = np.ascontiguousarray(qkv[:, H * D:(H + KV) * D])
+    v = np.ascontiguousarray(qkv[:, (H + KV) * D:])
+    g = rng.uniform(0.9, 1.1, D).astype(np.float32)
+    be.configure(H, KV, D, D, 10000.0, 1e-6).create_cache(2, 128, N.BF16)
+    dq, dk, dv, dqkv, dg = dev(be, q), dev(be, k), dev(be, v), dev(be, qkv), dev(be, g)
+    o1, o2 = be.alloc(seq * H * D * 4), be.alloc(seq * H * D * 4)
+    try:
+        be.prefill_dev(0, 0, seq, dq, dk, dv, N.BF16, dg, dg, o1)
+        be.prefill_dev_ld(1, 0, seq, dqkv, ld, dqkv + 2 * H * D, dqkv + 2 * (H + KV) * D, ld, N.BF16,
+                          dg, dg, o2)
+        be.sync()
+        a = be.download(np.empty((seq, H * D), np.float32), o1)
+        b = be.download(np.empty((seq, H * D), np.float32), o2)
+        assert np.array_equal(a, b)
+        k0, v0 = be.ReadKv(0, 0, seq)
+        k1, v1 = be.ReadKv(1, 0, seq)
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+        with pytest.raises(N.ArgumentError):
+            be.prefill_dev_ld(1, 0, seq, dqkv, H * D - 8, dqkv, dqkv, ld, N.BF16, None, None, o2)
+        with pytest.raises(N.ArgumentError):
+            N.check(be._lib.hymt_attn_prefill_ld(be._h, 1, 0, seq, dqkv, ld, dqkv, dqkv, ld, N.BF16,
+                                                 None, None, o2, 0))
+    finally:
+        for p in (dq, dk, dv, dqkv, dg, o1, o2):
+            be.free(p)
