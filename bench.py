@@ -296,7 +296,8 @@ def time_gemv(reps=200, min_bytes=320 << 20):
     return out
 
 
-def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefill_reps=5):
+def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefill_reps=5,
+               cpu_tokens=0):
     """Whole decode step of the 32-layer hunyuan-dense model (synthetic Q4_K
     layers, Q6_K embedding and output as in a Q4_K_M file, fp16 KV) at
     position `ctx` over a resident ctx-row cache: embedding row, per layer the
@@ -319,6 +320,23 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
     wbytes = sum(len(x.data) for n, x in t.items() if n != "token_embd.weight") + \
         len(emb.data) // emb.rows
     kvbytes = cfg.num_layers * decode_bytes_per_layer(ctx + 1, 4 if kv_dtype == F32 else 2)
+    cpu = None
+    if cpu_tokens:
+        # the oracle's decode step (C restatement, one thread, double sums) on
+        # the same weights at the same position; the cache rows are zeros,
+        # which costs the same
+        from oracle.model import OracleModel
+        om = OracleModel(cfg, t, ctx + 1, kv_dtype)
+        om.step(4242, ctx)
+        t0 = time.perf_counter()
+        for _ in range(cpu_tokens):
+            om.step(4242, ctx)
+        sec = (time.perf_counter() - t0) / cpu_tokens
+        del om
+        cpu = {"value": round(1.0 / sec, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"{cpu_tokens} decode steps of the same model at position {ctx} after one "
+                         f"warm-up ({sec:.2f} s per token), oracle/model.py over the C "
+                         f"restatement (oracle/hymt_quant.c, oracle/hymt_oracle.c)"}
     be = HipBackend(0)
     try:
         be.LoadModel(t, cfg, max_tokens=ctx + 1, kv_dtype=kv_dtype)
@@ -386,7 +404,8 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
                         "frac": round(pf_flops / (pf_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                         "flops": pf_flops,
                         "timing": "wall clock per ForwardStep(prompt, 0), mean of "
-                                  f"{prefill_reps}, chunks of 2048 rows"}}
+                                  f"{prefill_reps}, chunks of 2048 rows"},
+            "cpu_baseline": cpu}
 
 
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
@@ -582,7 +601,8 @@ def main():
                                      "decode step's shapes, W streamed from HBM",
                          "unit": "GB/s of GGUF weight bytes", "cases": time_gemv()}
     if args.only in (None, "model"):
-        extra["model"] = time_model(steps=max(5, args.steps // 2), warmup=args.warmup)
+        extra["model"] = time_model(steps=max(5, args.steps // 2), warmup=args.warmup,
+                                    cpu_tokens=0 if args.no_cpu else 2)
 
     cpu = None
     if not args.no_cpu and dec is not None:
