@@ -637,7 +637,6 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
             const int per = (256 + pairs - 1) / pairs;
             cap = std::max(4, (max_tiles + per - 1) / per);
         }
-        if (const char *s = std::getenv("HYMT_HIP_PREFILL_CAP")) cap = std::max(1, atoi(s));
         cap = std::min(cap, kItemTiles);
         f.cap = cap;
         int items = 0;
