@@ -801,6 +801,11 @@ int hymt_graph_destroy(hymt_ctx *c, hymt_graph *g) {
 
 // ---- quantized weights ------------------------------------------------------
 
+namespace {
+// The GEMV and row kernels read activations and norm weights as float4.
+bool misaligned16(const void *p) { return p && ((uintptr_t)p & 15u) != 0; }
+}  // namespace
+
 struct hymt_weight {
     hymt::WeightDev dev;
     void *mem = nullptr;
@@ -885,6 +890,8 @@ int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int f
     if ((flags & HYMT_GEMV_IN_RMSNORM) && (flags & HYMT_GEMV_IN_SWIGLU))
         return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM and HYMT_GEMV_IN_SWIGLU exclude each other");
     if ((flags & HYMT_GEMV_IN_RMSNORM) && !norm_w) return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM needs norm_w");
+    if (misaligned16(x) || ((flags & HYMT_GEMV_IN_RMSNORM) && misaligned16(norm_w)))
+        return fail(HYMT_E_ARG, "x and norm_w must be 16-byte aligned");
     try {
         HIP_TRY(hipSetDevice(c->device));
         HIP_TRY(hymt::launch_gemv(w->dev, x, y, flags, norm_w, eps, c->stream));
@@ -987,6 +994,8 @@ int hymt_rows_rmsnorm(hymt_ctx *c, const float *x, int m, int n, const float *no
     if (int r = check_ctx(c, false, true)) return r;
     if (!x || !norm_w || !out) return fail(HYMT_E_ARG, "null input, weight or output");
     if (m < 0 || n < 4 || n > 8192 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4 up to 8192");
+    if (misaligned16(x) || misaligned16(norm_w) || ((uintptr_t)out & 7u))
+        return fail(HYMT_E_ARG, "x and norm_w must be 16-byte aligned, out 8-byte aligned");
     try {
         HIP_TRY(hipSetDevice(c->device));
         HIP_TRY(hymt::launch_rows_rmsnorm(x, m, n, norm_w, eps, (uint16_t *)out, c->stream));
@@ -1000,6 +1009,8 @@ int hymt_rows_swiglu(hymt_ctx *c, const float *gate_up, int m, int n, void *out)
     if (int r = check_ctx(c, false, true)) return r;
     if (!gate_up || !out) return fail(HYMT_E_ARG, "null input or output");
     if (m < 0 || n < 4 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4");
+    if (misaligned16(gate_up) || ((uintptr_t)out & 7u))
+        return fail(HYMT_E_ARG, "gate_up must be 16-byte aligned, out 8-byte aligned");
     try {
         HIP_TRY(hipSetDevice(c->device));
         HIP_TRY(hymt::launch_rows_swiglu(gate_up, m, n, (uint16_t *)out, c->stream));
@@ -1013,6 +1024,7 @@ int hymt_to_bf16(hymt_ctx *c, const float *x, size_t count, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!x || !out) return fail(HYMT_E_ARG, "null input or output");
     if (count % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "count must be a multiple of 4");
+    if (misaligned16(x) || ((uintptr_t)out & 7u)) return fail(HYMT_E_ARG, "x must be 16-byte aligned, out 8-byte aligned");
     try {
         HIP_TRY(hipSetDevice(c->device));
         HIP_TRY(hymt::launch_to_bf16(x, count, (uint16_t *)out, c->stream));

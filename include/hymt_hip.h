@@ -262,8 +262,8 @@ int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size
  *   HYMT_GEMV_IN_SWIGLU   x holds gate[cols] then up[cols];
  *                         x' = gate / (1 + exp(-gate)) * up (Ops.SiLUMul,
  *                         Ops.cs:999-1052: the FFN's down projection input)
- * x, y and norm_w are device pointers; the call only enqueues work and may be
- * recorded.  fp32 activations and accumulation. */
+ * x, y and norm_w are device pointers (x and norm_w 16-byte aligned); the call
+ * only enqueues work and may be recorded.  fp32 activations and accumulation. */
 #define HYMT_GEMV_ACCUMULATE 1
 #define HYMT_GEMV_IN_RMSNORM 2
 #define HYMT_GEMV_IN_SWIGLU 4
@@ -303,7 +303,9 @@ int hymt_gemm(hymt_ctx *ctx, const hymt_weight *w, int row0, int nrows, const vo
 int hymt_embed_rows(hymt_ctx *ctx, const hymt_weight *w, const int32_t *rows, int n, float *out);
 
 /* out[i] = bf16(x[i] / sqrt(mean(x[i]^2) + eps) * norm_w) for m rows of n
- * fp32 values (Ops.RmsNorm, Ops.cs:12-90).  n a multiple of 4 up to 8192. */
+ * fp32 values (Ops.RmsNorm, Ops.cs:12-90).  n a multiple of 4 up to 8192.
+ * For this and the two calls below: fp32 inputs 16-byte aligned, bf16
+ * outputs 8-byte aligned (vector loads and stores). */
 int hymt_rows_rmsnorm(hymt_ctx *ctx, const float *x, int m, int n, const float *norm_w, float eps, void *out);
 
 /* out[i][j] = bf16(g / (1 + exp(-g)) * u), g = gate_up[i][j], u =

@@ -160,3 +160,25 @@ def test_forward_step_requires_model(hip_available):
             be.ForwardStep([1], 0)
     finally:
         be.Dispose()
+
+
+def test_misaligned_vectors_are_refused(hip_available):
+    be = HipBackend(0)
+    try:
+        raw = S.random_weight(3, N.W_Q8_0, 16, 2048)
+        w = be.weight_upload(N.W_Q8_0, 16, 2048, raw)
+        d = be.alloc(4 * 4096)
+        try:
+            with pytest.raises(N.ArgumentError):
+                be.gemv(w, d + 4, d)
+            with pytest.raises(N.ArgumentError):
+                be.gemv(w, d, d, rmsnorm=d + 8)
+            with pytest.raises(N.ArgumentError):
+                be.rows_rmsnorm(d + 4, 1, 2048, d, 1e-5, d)
+            with pytest.raises(N.ArgumentError):
+                be.to_bf16(d, 8, d + 2)
+        finally:
+            be.free(d)
+            be.weight_free(w)
+    finally:
+        be.Dispose()
