@@ -1033,3 +1033,155 @@ int hymt_to_bf16(hymt_ctx *c, const float *x, size_t count, void *out) {
     }
     return HYMT_OK;
 }
+
+// ---- the decode step of the model, enqueued natively -------------------------
+
+struct hymt_model {
+    hymt_ctx *ctx = nullptr;
+    int layers = 0, hidden = 0, ffn = 0, vocab = 0;
+    float eps = 1e-5f;
+    struct Layer {
+        const hymt_weight *w[6] = {};  // q|k|v (or q), k, v, o, gate|up (or gate), up; down below
+        const hymt_weight *down = nullptr;
+        const float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+        bool set = false;
+    };
+    std::vector<Layer> L;
+    const hymt_weight *embd = nullptr, *out = nullptr;
+    const float *out_norm = nullptr;
+    DevBuf h, qkv, ao, gu;
+};
+
+int hymt_model_create(hymt_ctx *c, int layers, int hidden, int ffn, int vocab, float eps, hymt_model **out) {
+    if (int r = check_ctx(c, true, true)) return r;
+    if (!out) return fail(HYMT_E_ARG, "null output pointer");
+    *out = nullptr;
+    if (layers != c->layers || hidden < 2048 || hidden % 2048 || ffn < 2048 || ffn % 2048 || vocab < 1)
+        return fail(HYMT_E_ARG, "model shape does not match the cache or the GEMV limits");
+    if (int r = refuse_in_capture(c, "hymt_model_create")) return r;
+    hymt_model *m = new (std::nothrow) hymt_model();
+    if (!m) return fail(HYMT_E_OOM, "host allocation failed");
+    m->ctx = c;
+    m->layers = layers;
+    m->hidden = hidden;
+    m->ffn = ffn;
+    m->vocab = vocab;
+    m->eps = eps;
+    m->L.resize(layers);
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        const size_t qd = (size_t)c->heads * c->head_dim, kd = (size_t)c->kv_heads * c->head_dim;
+        m->h.reserve((size_t)hidden * 4);
+        m->qkv.reserve((qd + 2 * kd) * 4);
+        m->ao.reserve(qd * 4);
+        m->gu.reserve((size_t)2 * ffn * 4);
+    } catch (const HipError &e) {
+        for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu}) b->release();
+        delete m;
+        return map_hip(e);
+    }
+    *out = m;
+    return HYMT_OK;
+}
+
+int hymt_model_set_layer(hymt_model *m, int layer, const hymt_weight *q_or_qkv, const hymt_weight *k,
+                         const hymt_weight *v, const hymt_weight *o, const hymt_weight *gate_or_gate_up,
+                         const hymt_weight *up, const hymt_weight *down, const float *attn_norm,
+                         const float *ffn_norm, const float *q_norm, const float *k_norm) {
+    if (!m) return fail(HYMT_E_ARG, "null model");
+    if (layer < 0 || layer >= m->layers) return fail(HYMT_E_ARG, "layer out of range");
+    hymt_ctx *c = m->ctx;
+    const int qd = c->heads * c->head_dim, kd = c->kv_heads * c->head_dim;
+    auto shape = [](const hymt_weight *w, int rows, int cols) {
+        return w && w->dev.rows == rows && w->dev.cols == cols;
+    };
+    const bool fused_qkv = !k && !v;
+    const bool fused_gu = !up;
+    bool ok = fused_qkv ? shape(q_or_qkv, qd + 2 * kd, m->hidden)
+                        : shape(q_or_qkv, qd, m->hidden) && shape(k, kd, m->hidden) && shape(v, kd, m->hidden);
+    ok = ok && shape(o, m->hidden, qd) && shape(down, m->hidden, m->ffn);
+    ok = ok && (fused_gu ? shape(gate_or_gate_up, 2 * m->ffn, m->hidden)
+                         : shape(gate_or_gate_up, m->ffn, m->hidden) && shape(up, m->ffn, m->hidden));
+    if (!ok) return fail(HYMT_E_ARG, "layer weights do not have the model's shapes");
+    if (!attn_norm || !ffn_norm || misaligned16(attn_norm) || misaligned16(ffn_norm))
+        return fail(HYMT_E_ARG, "attn_norm and ffn_norm must be 16-byte aligned device vectors");
+    hymt_model::Layer &Ly = m->L[layer];
+    Ly.w[0] = q_or_qkv;
+    Ly.w[1] = k;
+    Ly.w[2] = v;
+    Ly.w[3] = o;
+    Ly.w[4] = gate_or_gate_up;
+    Ly.w[5] = up;
+    Ly.down = down;
+    Ly.attn_norm = attn_norm;
+    Ly.ffn_norm = ffn_norm;
+    Ly.q_norm = q_norm;
+    Ly.k_norm = k_norm;
+    Ly.set = true;
+    return HYMT_OK;
+}
+
+int hymt_model_set_io(hymt_model *m, const hymt_weight *embd, const hymt_weight *out, const float *out_norm) {
+    if (!m) return fail(HYMT_E_ARG, "null model");
+    if (!embd || embd->dev.cols != m->hidden || embd->dev.rows != m->vocab)
+        return fail(HYMT_E_ARG, "token_embd must be vocab x hidden");
+    if (out && (out->dev.cols != m->hidden || out->dev.rows != m->vocab))
+        return fail(HYMT_E_ARG, "output must be vocab x hidden");
+    if (!out_norm || misaligned16(out_norm)) return fail(HYMT_E_ARG, "out_norm must be a 16-byte aligned device vector");
+    m->embd = embd;
+    m->out = out ? out : embd;  // the tied embedding (HunyuanDenseModel.cs:419)
+    m->out_norm = out_norm;
+    return HYMT_OK;
+}
+
+int hymt_model_decode(hymt_model *m, int token, int pos, float *logits) {
+    if (!m) return fail(HYMT_E_ARG, "null model");
+    hymt_ctx *c = m->ctx;
+    if (int r = check_ctx(c, true, true)) return r;
+    if (!m->embd || !logits) return fail(HYMT_E_STATE, "hymt_model_set_io first (and a logits buffer)");
+    for (const auto &Ly : m->L)
+        if (!Ly.set) return fail(HYMT_E_STATE, "every layer needs hymt_model_set_layer");
+    if (token < 0 || token >= m->vocab) return fail(HYMT_E_ARG, "token out of range");
+    const int qd = c->heads * c->head_dim, kd = c->kv_heads * c->head_dim;
+    float *h = (float *)m->h.p, *qkv = (float *)m->qkv.p, *ao = (float *)m->ao.p, *gu = (float *)m->gu.p;
+    const int norm_in = HYMT_GEMV_IN_RMSNORM;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_embed(m->embd->dev, token, h, c->stream));
+        for (int l = 0; l < m->layers; l++) {
+            const hymt_model::Layer &Ly = m->L[l];
+            if (!Ly.w[1]) {
+                HIP_TRY(hymt::launch_gemv(Ly.w[0]->dev, h, qkv, norm_in, Ly.attn_norm, m->eps, c->stream));
+            } else {
+                HIP_TRY(hymt::launch_gemv(Ly.w[0]->dev, h, qkv, norm_in, Ly.attn_norm, m->eps, c->stream));
+                HIP_TRY(hymt::launch_gemv(Ly.w[1]->dev, h, qkv + qd, norm_in, Ly.attn_norm, m->eps, c->stream));
+                HIP_TRY(hymt::launch_gemv(Ly.w[2]->dev, h, qkv + qd + kd, norm_in, Ly.attn_norm, m->eps, c->stream));
+            }
+            if (int r = hymt_attn_decode(c, l, pos, qkv, qkv + qd, qkv + qd + kd, Ly.q_norm, Ly.k_norm, ao,
+                                         HYMT_FLAG_DEVICE_PTRS))
+                return r;
+            HIP_TRY(hymt::launch_gemv(Ly.w[3]->dev, ao, h, HYMT_GEMV_ACCUMULATE, nullptr, m->eps, c->stream));
+            HIP_TRY(hymt::launch_gemv(Ly.w[4]->dev, h, gu, norm_in, Ly.ffn_norm, m->eps, c->stream));
+            if (Ly.w[5])
+                HIP_TRY(hymt::launch_gemv(Ly.w[5]->dev, h, gu + m->ffn, norm_in, Ly.ffn_norm, m->eps, c->stream));
+            HIP_TRY(hymt::launch_gemv(Ly.down->dev, gu, h, HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_SWIGLU, nullptr,
+                                      m->eps, c->stream));
+        }
+        HIP_TRY(hymt::launch_gemv(m->out->dev, h, logits, norm_in, m->out_norm, m->eps, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
+int hymt_model_destroy(hymt_model *m) {
+    if (!m) return HYMT_OK;
+    hymt_ctx *c = m->ctx;
+    if (c && c->has_device()) {
+        (void)hipSetDevice(c->device);
+        (void)hipStreamSynchronize(c->stream);
+    }
+    for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu}) b->release();
+    delete m;
+    return HYMT_OK;
+}

@@ -35,6 +35,7 @@ copies, VulkanBackend.cs:760-880):
 """
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import numpy as np
@@ -127,6 +128,18 @@ class DeviceModel:
         self.gu = self._buf(2 * c.ffn_size)
         self.logits = self._buf(c.vocab_size)
         self._pf = None  # prefill activations, allocated on the first prefill
+        # the decode step runs natively: one hymt_model_decode per token
+        lib, h = be._lib, ctypes.c_void_p()
+        N.check(lib.hymt_model_create(be._h, c.num_layers, c.hidden_size, c.ffn_size, c.vocab_size,
+                                      c.eps, ctypes.byref(h)))
+        self._native = h.value
+        for l, L in enumerate(self.layers):
+            qkv, gu = L["qkv"] + [None, None], L["gate_up"] + [None]
+            N.check(lib.hymt_model_set_layer(self._native, l, qkv[0], qkv[1], qkv[2], L["o"], gu[0],
+                                             gu[1], L["down"], L["attn_norm"], L["ffn_norm"],
+                                             L["q_norm"], L["k_norm"]))
+        N.check(lib.hymt_model_set_io(self._native, self.embd,
+                                      None if self.out is self.embd else self.out, self.out_norm))
         # the SwiGLU row kernel reads gate and up from one [m][2F] GEMM output,
         # so prompts of a model whose gate and up types differ (two matrices)
         # run as decode steps; so do those of an fp32 cache (the prefill
@@ -140,7 +153,13 @@ class DeviceModel:
         return p
 
     def step(self, token: int, pos: int):
-        """Enqueue one decode step; the logits land in self.logits."""
+        """Enqueue one decode step; the logits land in self.logits
+        (hymt_model_decode runs the sequence of step_composed in C++)."""
+        N.check(self.be._lib.hymt_model_decode(self._native, token, pos, self.logits))
+
+    def step_composed(self, token: int, pos: int):
+        """The same decode step as separate C ABI calls (the sequence a host
+        without hymt_model_decode would issue)."""
         be, c = self.be, self.cfg
         be.embed(self.embd, token, self.h)
         for l, L in enumerate(self.layers):
@@ -221,6 +240,9 @@ class DeviceModel:
         return out
 
     def free(self):
+        if getattr(self, "_native", None):
+            N.check(self.be._lib.hymt_model_destroy(self._native))
+            self._native = None
         for w in self._weights:
             self.be.weight_free(w)
         for p in self._bufs:

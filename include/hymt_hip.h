@@ -315,6 +315,36 @@ int hymt_rows_swiglu(hymt_ctx *ctx, const float *gate_up, int m, int n, void *ou
 /* out[i] = bf16(x[i]) for count fp32 values (count a multiple of 4). */
 int hymt_to_bf16(hymt_ctx *ctx, const float *x, size_t count, void *out);
 
+/* ---- the model's decode step, enqueued natively ---------------------------------
+ * IComputeBackend.ForwardStep for one token (IComputeBackend.cs:40-47) in one
+ * call: the sequence of HunyuanDenseModel.DecodeBlock
+ * (HunyuanDenseModel.Decode.cs:30-101) over weights already uploaded --
+ *   h = token_embd[token]
+ *   per layer: qkv = W_qkv RMSNorm(h, attn_norm); ao = decode attention at pos
+ *              (RoPE, QK norm, append); h += W_o ao;
+ *              gu = W_gate|up RMSNorm(h, ffn_norm); h += W_down (silu(gate) * up)
+ *   logits = W_out RMSNorm(h, output_norm)
+ * -- i.e. hymt_embed, hymt_gemv and hymt_attn_decode with device pointers, on the
+ * context's stream (recordable).  The model borrows the weights and norm
+ * vectors (device pointers, 16-byte aligned) and owns its activation
+ * buffers; destroy it before its weights and the context.  The context's KV
+ * cache must have `layers` layers. */
+typedef struct hymt_model hymt_model;
+int hymt_model_create(hymt_ctx *ctx, int layers, int hidden, int ffn, int vocab, float eps, hymt_model **model);
+/* q_or_qkv: [q; k; v] rows (k = v = NULL) or q alone with k and v;
+ * gate_or_gate_up: [gate; up] rows (up = NULL) or gate alone with up.
+ * q_norm / k_norm may be NULL (no QK norm). */
+int hymt_model_set_layer(hymt_model *model, int layer, const hymt_weight *q_or_qkv, const hymt_weight *k,
+                         const hymt_weight *v, const hymt_weight *o, const hymt_weight *gate_or_gate_up,
+                         const hymt_weight *up, const hymt_weight *down, const float *attn_norm,
+                         const float *ffn_norm, const float *q_norm, const float *k_norm);
+/* out NULL: the output projection uses the tied embedding (HunyuanDenseModel.cs:419). */
+int hymt_model_set_io(hymt_model *model, const hymt_weight *token_embd, const hymt_weight *out,
+                      const float *out_norm);
+/* Enqueue the decode step of `token` at `pos`; logits: device pointer, vocab floats. */
+int hymt_model_decode(hymt_model *model, int token, int pos, float *logits);
+int hymt_model_destroy(hymt_model *model);
+
 #ifdef __cplusplus
 }
 #endif

@@ -182,3 +182,23 @@ def test_misaligned_vectors_are_refused(hip_available):
             be.weight_free(w)
     finally:
         be.Dispose()
+
+
+def test_native_step_equals_composed_calls(hip_available):
+    """hymt_model_decode enqueues exactly the composed sequence of C ABI calls."""
+    t = _model(5, {"attn": N.W_Q4_K, "ffn": [N.W_Q8_0, N.W_Q6_K], "embd": N.W_Q6_K}, tied=True,
+               v_override=N.W_Q8_0)
+    be = HipBackend(0)
+    try:
+        be.LoadModel(t, CFG, max_tokens=16, kv_dtype=N.BF16, prefill=False)
+        m = be._model
+        for pos, tok in enumerate([1, 400, 22, 3]):
+            m.step_composed(tok, pos)
+            a = be.download(np.empty(CFG.vocab_size, np.float32), m.logits)
+            m.step(tok, pos)  # rewrites the same cache row with the same values
+            b = be.download(np.empty(CFG.vocab_size, np.float32), m.logits)
+            assert np.array_equal(a, b), pos
+        with pytest.raises(N.ArgumentError):
+            N.check(be._lib.hymt_model_decode(m._native, CFG.vocab_size, 4, m.logits))
+    finally:
+        be.Dispose()
