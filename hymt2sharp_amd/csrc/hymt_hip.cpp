@@ -1103,8 +1103,9 @@ int hymt_model_set_layer(hymt_model *m, int layer, const hymt_weight *q_or_qkv, 
     ok = ok && (fused_gu ? shape(gate_or_gate_up, 2 * m->ffn, m->hidden)
                          : shape(gate_or_gate_up, m->ffn, m->hidden) && shape(up, m->ffn, m->hidden));
     if (!ok) return fail(HYMT_E_ARG, "layer weights do not have the model's shapes");
-    if (!attn_norm || !ffn_norm || misaligned16(attn_norm) || misaligned16(ffn_norm))
-        return fail(HYMT_E_ARG, "attn_norm and ffn_norm must be 16-byte aligned device vectors");
+    if (!attn_norm || !ffn_norm || misaligned16(attn_norm) || misaligned16(ffn_norm) || misaligned16(q_norm) ||
+        misaligned16(k_norm))
+        return fail(HYMT_E_ARG, "norm vectors must be 16-byte aligned device pointers");
     hymt_model::Layer &Ly = m->L[layer];
     Ly.w[0] = q_or_qkv;
     Ly.w[1] = k;
@@ -1142,6 +1143,13 @@ int hymt_model_decode(hymt_model *m, int token, int pos, float *logits) {
     for (const auto &Ly : m->L)
         if (!Ly.set) return fail(HYMT_E_STATE, "every layer needs hymt_model_set_layer");
     if (token < 0 || token >= m->vocab) return fail(HYMT_E_ARG, "token out of range");
+    // checked here as well as by each attention call, so that a bad position
+    // enqueues nothing
+    if (pos < 0) return fail(HYMT_E_ARG, "negative position");
+    if ((long)pos + 1 > c->pages.max_tokens())
+        return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) + " exceeded at " +
+                                         std::to_string((long)pos + 1));
+    if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before decode");
     const int qd = c->heads * c->head_dim, kd = c->kv_heads * c->head_dim;
     float *h = (float *)m->h.p, *qkv = (float *)m->qkv.p, *ao = (float *)m->ao.p, *gu = (float *)m->gu.p;
     const int norm_in = HYMT_GEMV_IN_RMSNORM;

@@ -200,5 +200,11 @@ def test_native_step_equals_composed_calls(hip_available):
             assert np.array_equal(a, b), pos
         with pytest.raises(N.ArgumentError):
             N.check(be._lib.hymt_model_decode(m._native, CFG.vocab_size, 4, m.logits))
+        with pytest.raises(N.NotSupportedError):  # beyond the cache's capacity
+            N.check(be._lib.hymt_model_decode(m._native, 1, 1000, m.logits))
+        with pytest.raises(N.ArgumentError):
+            N.check(be._lib.hymt_model_decode(m._native, 1, -1, m.logits))
+        m.step(2, 4)  # the model still steps after the refusals
+        be.sync()
     finally:
         be.Dispose()
