@@ -255,6 +255,9 @@ class HipBackend:
     def rows_swiglu(self, gu_dev, m: int, n: int, out_dev):
         N.check(self._lib.hymt_rows_swiglu(self._h, gu_dev, m, n, out_dev))
 
+    def rows_swiglu_bf16(self, gu_dev, m: int, n: int, out_dev):
+        N.check(self._lib.hymt_rows_swiglu_bf16(self._h, gu_dev, m, n, out_dev))
+
     def to_bf16(self, x_dev, count: int, out_dev):
         N.check(self._lib.hymt_to_bf16(self._h, x_dev, count, out_dev))
 

@@ -1020,6 +1020,21 @@ int hymt_rows_swiglu(hymt_ctx *c, const float *gate_up, int m, int n, void *out)
     return HYMT_OK;
 }
 
+int hymt_rows_swiglu_bf16(hymt_ctx *c, const void *gate_up, int m, int n, void *out) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!gate_up || !out) return fail(HYMT_E_ARG, "null input or output");
+    if (m < 0 || n < 4 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4");
+    if (((uintptr_t)gate_up & 7u) || ((uintptr_t)out & 7u))
+        return fail(HYMT_E_ARG, "gate_up and out must be 8-byte aligned");
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        HIP_TRY(hymt::launch_rows_swiglu_bf16((const uint16_t *)gate_up, m, n, (uint16_t *)out, c->stream));
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
 int hymt_to_bf16(hymt_ctx *c, const float *x, size_t count, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!x || !out) return fail(HYMT_E_ARG, "null input or output");

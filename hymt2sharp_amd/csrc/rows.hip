@@ -67,6 +67,23 @@ __global__ __launch_bounds__(256) void rows_swiglu_kernel(const float *__restric
     }
 }
 
+// As rows_swiglu_kernel over a bf16 gate/up GEMM output (half the bytes).
+__global__ __launch_bounds__(256) void rows_swiglu_bf16_kernel(const uint16_t *__restrict__ gu, int m, int n,
+                                                               uint16_t *__restrict__ out) {
+    const int n4 = n / 4;
+    const size_t total = (size_t)m * n4;
+    for (size_t e = (size_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (size_t)gridDim.x * 256) {
+        const size_t r = e / n4, i = e % n4;
+        const uint2 gb = ((const uint2 *)(gu + r * 2 * n))[i], ub = ((const uint2 *)(gu + r * 2 * n + n))[i];
+        const float g[4] = {bf16_to_f32(gb.x & 0xFFFF), bf16_to_f32(gb.x >> 16), bf16_to_f32(gb.y & 0xFFFF),
+                            bf16_to_f32(gb.y >> 16)};
+        const float u[4] = {bf16_to_f32(ub.x & 0xFFFF), bf16_to_f32(ub.x >> 16), bf16_to_f32(ub.y & 0xFFFF),
+                            bf16_to_f32(ub.y >> 16)};
+        ((uint2 *)(out + r * n))[i] = pack4(g[0] / (1.f + expf(-g[0])) * u[0], g[1] / (1.f + expf(-g[1])) * u[1],
+                                            g[2] / (1.f + expf(-g[2])) * u[2], g[3] / (1.f + expf(-g[3])) * u[3]);
+    }
+}
+
 __global__ __launch_bounds__(256) void to_bf16_kernel(const float *__restrict__ x, size_t n4,
                                                       uint16_t *__restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
@@ -94,6 +111,13 @@ hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipS
     if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     hipLaunchKernelGGL(rows_swiglu_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *out, hipStream_t s) {
+    if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
+    if (m == 0) return hipSuccess;
+    hipLaunchKernelGGL(rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
     return hipGetLastError();
 }
 

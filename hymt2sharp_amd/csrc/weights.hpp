@@ -55,6 +55,7 @@ hipError_t launch_rows(const WeightDev &w, const int *rows, int row0, int n, flo
 hipError_t launch_rows_rmsnorm(const float *x, int m, int n, const float *w, float eps, uint16_t *out,
                                hipStream_t s);
 hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipStream_t s);
+hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *out, hipStream_t s);
 hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s);
 // y[m][n] (+)= x[m][k] . W[n][k]^T, bf16 operands, fp32 accumulation
 // (gemm.cpp, hipBLASLt); y is fp32 or, with y_bf16, bf16

@@ -29,8 +29,8 @@ copies, VulkanBackend.cs:760-880):
         [Q|K|V] = XN . [Wq; Wk; Wv]^T (bf16)                hymt_gemm OUT_BF16
         AO = causal attention (RoPE, QK norm, append)       hymt_attn_prefill_ld
         X += bf16(AO) . Wo^T                                hymt_to_bf16, hymt_gemm ACCUMULATE
-        GU = bf16 RMSNorm(X, ffn_norm) . [Wgate; Wup]^T     hymt_rows_rmsnorm, hymt_gemm
-        X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu, hymt_gemm ACCUMULATE
+        GU = bf16 RMSNorm(X, ffn_norm) . [Wgate; Wup]^T     hymt_rows_rmsnorm, hymt_gemm OUT_BF16
+        X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu_bf16, hymt_gemm ACCUMULATE
     logits = Wout RMSNorm(X[last], output_norm)             hymt_gemv IN_RMSNORM
 """
 from __future__ import annotations
@@ -217,8 +217,8 @@ class DeviceModel:
             be.to_bf16(B["ao"], m * qd, B["ao16"])
             be.gemm(L["o"], B["ao16"], m, B["x"], accumulate=True)
             be.rows_rmsnorm(B["x"], m, H, L["ffn_norm"], c.eps, B["xn"])
-            be.gemm(L["gate_up"][0], B["xn"], m, B["gu"])
-            be.rows_swiglu(B["gu"], m, F, B["act"])
+            be.gemm(L["gate_up"][0], B["xn"], m, B["gu"], out_bf16=True)
+            be.rows_swiglu_bf16(B["gu"], m, F, B["act"])
             be.gemm(L["down"], B["act"], m, B["x"], accumulate=True)
         be.gemv(self.out, B["x"] + 4 * (m - 1) * H, self.logits, rmsnorm=self.out_norm, eps=c.eps)
 

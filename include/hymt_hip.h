@@ -312,6 +312,10 @@ int hymt_rows_rmsnorm(hymt_ctx *ctx, const float *x, int m, int n, const float *
  * gate_up[i][n + j] (Ops.SiLUMul, Ops.cs:999-1052). */
 int hymt_rows_swiglu(hymt_ctx *ctx, const float *gate_up, int m, int n, void *out);
 
+/* hymt_rows_swiglu over a bf16 gate_up (a HYMT_GEMM_OUT_BF16 GEMM output);
+ * gate_up and out 8-byte aligned. */
+int hymt_rows_swiglu_bf16(hymt_ctx *ctx, const void *gate_up, int m, int n, void *out);
+
 /* out[i] = bf16(x[i]) for count fp32 values (count a multiple of 4). */
 int hymt_to_bf16(hymt_ctx *ctx, const float *x, size_t count, void *out);
 

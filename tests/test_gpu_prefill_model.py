@@ -72,6 +72,17 @@ def test_rows_rmsnorm_swiglu_and_rounding(be):
     g, u = gu[:, :F].astype(np.float64), gu[:, F:].astype(np.float64)
     ref = bf16_bits((g / (1 + np.exp(-g)) * u).astype(np.float32))
     assert ulp_diff(got, ref).max() <= 1 and np.mean(got == ref) > 0.99
+    # the same over a bf16 gate/up (a bf16 GEMM output)
+    gub = bf16_bits(gu)
+    dgub = dev(be, gub)
+    be.rows_swiglu_bf16(dgub, m, F, dact)
+    be.sync()
+    got = be.download(np.empty((m, F), np.uint16), dact)
+    gv = bf16_val(gub).astype(np.float64)
+    g, u = gv[:, :F], gv[:, F:]
+    ref = bf16_bits((g / (1 + np.exp(-g)) * u).astype(np.float32))
+    assert ulp_diff(got, ref).max() <= 1 and np.mean(got == ref) > 0.99
+    be.free(dgub)
     # rounding: bit-exact RNE (Ops.cs:664-665)
     be.to_bf16(dx, m * n, do)
     be.sync()
