@@ -111,6 +111,7 @@ SIGNATURES = {
     "hymt_model_set_layer": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],
     "hymt_model_set_io": [_vp, _vp, _vp, _vp],
     "hymt_model_decode": [_vp, _i, _i, _vp],
+    "hymt_model_prefill": [_vp, _vp, _i, _i, _vp, ctypes.c_uint],
     "hymt_model_destroy": [_vp],
 }
 
@@ -118,6 +119,7 @@ SIGNATURES = {
 W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
 GEMV_ACCUMULATE, GEMV_IN_RMSNORM, GEMV_IN_SWIGLU = 1, 2, 4
 GEMM_ACCUMULATE, GEMM_OUT_BF16 = 1, 2
+PREFILL_GATE_UP_F32 = 1
 
 _lib = None
 _synth = None

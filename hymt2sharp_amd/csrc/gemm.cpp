@@ -4,45 +4,54 @@
 //
 // hipBLASLt is column-major.  The row-major buffers map onto it without
 // copies: W [n][k] is a k x n column-major matrix (ld k) used transposed,
-// x [m][k] is k x m (ld k), and y [m][n] is the n x m result (ld n).  An
-// accumulating call passes y as C with beta = 1 (the residual add of the
+// x [m][k] is k x m (ld k), and y [m][n] is the n x m result (ld ldy >= n).
+// An accumulating call passes y as C with beta = 1 (the residual add of the
 // reference's Gemm(..., accumulate) calls, VulkanBackend.cs:782-856).
+//
+// All state -- the hipBLASLt handle, the split-K workspace, the chosen
+// algorithms -- belongs to one GemmState, which a context owns: two contexts
+// on one device never share a workspace, and no lock is needed (calls on one
+// context come from one thread, in stream order).
+//
+// Algorithm choice.  hipBLASLt's first heuristic choice is not always its
+// fastest at the prefill shapes, so the first call of a shape in an m bucket
+// (m rounded up to a power of two, at least 256) times up to kCandidates
+// candidates on the call's operands and keeps the fastest.  A later m in the
+// same bucket reuses that algorithm when the heuristic offers it for the new
+// m (else its first choice): no timing runs and no scratch allocation for
+// each new prompt length.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstring>
 #include <map>
-#include <mutex>
 #include <tuple>
 
 #include "weights.hpp"
 
 namespace hymt {
+
 namespace {
 
 constexpr size_t kWorkspace = 64u << 20;
+constexpr int kCandidates = 8;
 
-struct Plan {
-    hipblasLtMatmulDesc_t desc = nullptr;
+struct Layouts {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
     size_t ws = 0;
 };
 
-struct DeviceState {
-    hipblasLtHandle_t handle = nullptr;
-    void *workspace = nullptr;
-    std::map<std::tuple<int, int, int, bool, bool>, Plan> plans;
+struct Choice {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatmulAlgo_t algo{};  // the timed algorithm of the bucket
 };
 
-std::mutex g_mu;
-std::map<int, DeviceState> g_dev;
-
-void destroy_plan(Plan &p) {
-    if (p.a) hipblasLtMatrixLayoutDestroy(p.a);
-    if (p.b) hipblasLtMatrixLayoutDestroy(p.b);
-    if (p.c) hipblasLtMatrixLayoutDestroy(p.c);
-    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
-    p = Plan{};
+void destroy_layouts(Layouts &l) {
+    if (l.a) hipblasLtMatrixLayoutDestroy(l.a);
+    if (l.b) hipblasLtMatrixLayoutDestroy(l.b);
+    if (l.c) hipblasLtMatrixLayoutDestroy(l.c);
+    l = Layouts{};
 }
 
 // hipBLASLt status -> a HIP error code the C ABI maps (no device, bad shape,
@@ -57,26 +66,106 @@ hipError_t as_hip(hipblasStatus_t st) {
     }
 }
 
-constexpr int kCandidates = 8;
+int bucket_of(int m) {
+    int b = 256;
+    while (b < m) b *= 2;
+    return b;
+}
 
-hipError_t time_candidates(DeviceState &d, const Plan &p, const hipblasLtMatmulHeuristicResult_t *res, int found,
-                           const uint16_t *W, const uint16_t *x, int n, int m, bool y_bf16, bool acc,
-                           hipStream_t s, int &best) {
-    void *scratch = nullptr;
+bool same_algo(const hipblasLtMatmulAlgo_t &x, const hipblasLtMatmulAlgo_t &y) {
+    return std::memcmp(&x, &y, sizeof(x)) == 0;
+}
+
+}  // namespace
+
+struct GemmState {
+    hipblasLtHandle_t handle = nullptr;
+    void *workspace = nullptr;
+    void *scratch = nullptr;  // timing output of the candidate runs
+    size_t scratch_bytes = 0;
+    // (n, k, m bucket, y_bf16, accumulate) -> descriptor and timed algorithm
+    std::map<std::tuple<int, int, int, bool, bool>, Choice> choices;
+    // (n, k, m, ldy, y_bf16, accumulate) -> layouts and the algorithm used
+    std::map<std::tuple<int, int, int, int, bool, bool>, Layouts> layouts;
+};
+
+GemmState *gemm_state_create() { return new (std::nothrow) GemmState(); }
+
+void gemm_state_destroy(GemmState *g) {
+    if (!g) return;
+    for (auto &kv : g->layouts) destroy_layouts(kv.second);
+    for (auto &kv : g->choices)
+        if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
+    if (g->workspace) (void)hipFree(g->workspace);
+    if (g->scratch) (void)hipFree(g->scratch);
+    if (g->handle) hipblasLtDestroy(g->handle);
+    delete g;
+}
+
+namespace {
+
+hipblasStatus_t make_desc(hipblasLtMatmulDesc_t &desc) {
+    hipblasStatus_t st = hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
+    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulDescSetAttribute(desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
+    return st;
+}
+
+hipblasStatus_t make_layouts(int n, int k, int m, int ldy, bool y_bf16, Layouts &l) {
+    hipblasStatus_t st = hipblasLtMatrixLayoutCreate(&l.a, HIP_R_16BF, k, n, k);
+    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&l.b, HIP_R_16BF, k, m, k);
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatrixLayoutCreate(&l.c, y_bf16 ? HIP_R_16BF : HIP_R_32F, n, m, ldy);
+    return st;
+}
+
+hipblasStatus_t heuristic(GemmState &g, hipblasLtMatmulDesc_t desc, const Layouts &l,
+                          hipblasLtMatmulHeuristicResult_t *res, int &found) {
+    hipblasLtMatmulPreference_t pref = nullptr;
+    hipblasStatus_t st = hipblasLtMatmulPreferenceCreate(&pref);
+    const uint64_t wsmax = kWorkspace;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
+                                                   sizeof(wsmax));
+    found = 0;
+    if (st == HIPBLAS_STATUS_SUCCESS)
+        st = hipblasLtMatmulAlgoGetHeuristic(g.handle, desc, l.a, l.b, l.c, l.c, pref, kCandidates, res, &found);
+    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+    if (st == HIPBLAS_STATUS_SUCCESS && found < 1) st = HIPBLAS_STATUS_NOT_SUPPORTED;
+    return st;
+}
+
+// Time each usable candidate once on the call's operands (writing the
+// state's scratch output, beta = 0 or 1 alike) and return the fastest.
+hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layouts &l,
+                           const hipblasLtMatmulHeuristicResult_t *res, int found, const uint16_t *W,
+                           const uint16_t *x, size_t ybytes, bool acc, hipStream_t s, int &best) {
+    best = 0;
+    hipError_t e = hipSuccess;
+    if (ybytes > g.scratch_bytes) {
+        e = hipStreamSynchronize(s);
+        if (e == hipSuccess && g.scratch) e = hipFree(g.scratch);
+        g.scratch = nullptr;
+        g.scratch_bytes = 0;
+        if (e == hipSuccess) e = hipMalloc(&g.scratch, ybytes);
+        if (e != hipSuccess) return e;
+        g.scratch_bytes = ybytes;
+    }
+    e = hipMemsetAsync(g.scratch, 0, ybytes, s);
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    hipError_t e = hipMalloc(&scratch, (size_t)n * m * (y_bf16 ? 2 : 4));
-    if (e == hipSuccess) e = hipMemsetAsync(scratch, 0, (size_t)n * m * (y_bf16 ? 2 : 4), s);
     if (e == hipSuccess) e = hipEventCreate(&e0);
     if (e == hipSuccess) e = hipEventCreate(&e1);
     const float alpha = 1.0f, beta = acc ? 1.0f : 0.0f;
     float best_ms = 0.f;
     bool have = false;
-    best = 0;
     for (int i = 0; i < found && e == hipSuccess; i++) {
         if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspace) continue;
         auto run = [&]() {
-            return hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.a, x, p.b, &beta, scratch, p.c, scratch, p.c,
-                                   &res[i].algo, d.workspace, res[i].workspaceSize, s);
+            return hipblasLtMatmul(g.handle, desc, &alpha, W, l.a, x, l.b, &beta, g.scratch, l.c, g.scratch, l.c,
+                                   &res[i].algo, g.workspace, res[i].workspaceSize, s);
         };
         if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; a candidate that fails is skipped
         e = hipEventRecord(e0, s);
@@ -94,92 +183,87 @@ hipError_t time_candidates(DeviceState &d, const Plan &p, const hipblasLtMatmulH
     }
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
-    if (scratch) {
-        (void)hipStreamSynchronize(s);
-        (void)hipFree(scratch);
-    }
     return e;
-}
-
-hipError_t make_plan(DeviceState &d, int n, int k, int m, bool y_bf16, bool acc, const uint16_t *W,
-                     const uint16_t *x, hipStream_t s, Plan &p) {
-    const hipDataType yt = y_bf16 ? HIP_R_16BF : HIP_R_32F;
-    hipblasStatus_t st = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
-    const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta));
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb));
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.a, HIP_R_16BF, k, n, k);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.b, HIP_R_16BF, k, m, k);
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatrixLayoutCreate(&p.c, yt, n, m, n);
-    hipblasLtMatmulPreference_t pref = nullptr;
-    if (st == HIPBLAS_STATUS_SUCCESS) st = hipblasLtMatmulPreferenceCreate(&pref);
-    const uint64_t wsmax = kWorkspace;
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsmax,
-                                                   sizeof(wsmax));
-    hipblasLtMatmulHeuristicResult_t res[kCandidates];
-    int found = 0;
-    if (st == HIPBLAS_STATUS_SUCCESS)
-        st = hipblasLtMatmulAlgoGetHeuristic(d.handle, p.desc, p.a, p.b, p.c, p.c, pref, kCandidates, res, &found);
-    if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-    if (st == HIPBLAS_STATUS_SUCCESS && found < 1) st = HIPBLAS_STATUS_NOT_SUPPORTED;
-    if (st != HIPBLAS_STATUS_SUCCESS) {
-        destroy_plan(p);
-        return as_hip(st);
-    }
-    int best = 0;
-    if (found > 1) {
-        // The heuristic's first choice is not always the fastest at these
-        // shapes: time each candidate once on the call's operands, writing a
-        // scratch output (beta = 0 or 1 alike), and keep the fastest.
-        hipError_t e = time_candidates(d, p, res, found, W, x, n, m, y_bf16, acc, s, best);
-        if (e != hipSuccess) {
-            destroy_plan(p);
-            return e;
-        }
-    }
-    p.algo = res[best].algo;
-    p.ws = res[best].workspaceSize;
-    return hipSuccess;
 }
 
 }  // namespace
 
-hipError_t gemm_bf16(hipStream_t s, const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y,
-                     bool y_bf16, bool accumulate) {
-    if (n < 1 || k < 1 || m < 0 || (accumulate && y_bf16)) return hipErrorInvalidValue;
+hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int k, const uint16_t *x, int m,
+                     void *y, int ldy, bool y_bf16, bool accumulate) {
+    if (!g || n < 1 || k < 1 || m < 0 || ldy < n || (accumulate && y_bf16)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    std::lock_guard<std::mutex> lk(g_mu);
-    DeviceState &d = g_dev[dev];
-    if (!d.handle) {
-        hipblasStatus_t st = hipblasLtCreate(&d.handle);
+    hipError_t e = hipSuccess;
+    if (!g->handle) {
+        hipblasStatus_t st = hipblasLtCreate(&g->handle);
         if (st != HIPBLAS_STATUS_SUCCESS) {
-            d.handle = nullptr;
+            g->handle = nullptr;
             return as_hip(st);
         }
-        e = hipMalloc(&d.workspace, kWorkspace);
+    }
+    if (!g->workspace) {
+        e = hipMalloc(&g->workspace, kWorkspace);
         if (e != hipSuccess) {
-            d.workspace = nullptr;
+            g->workspace = nullptr;
             return e;
         }
     }
-    const auto key = std::make_tuple(n, k, m, y_bf16, accumulate);
-    auto it = d.plans.find(key);
-    if (it == d.plans.end()) {
-        Plan p;
-        e = make_plan(d, n, k, m, y_bf16, accumulate, W, x, s, p);
-        if (e != hipSuccess) return e;
-        it = d.plans.emplace(key, p).first;
+    const auto ckey = std::make_tuple(n, k, bucket_of(m), y_bf16, accumulate);
+    auto cit = g->choices.find(ckey);
+    const bool first_in_bucket = cit == g->choices.end();
+    if (first_in_bucket) {
+        Choice ch;
+        hipblasStatus_t st = make_desc(ch.desc);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            if (ch.desc) hipblasLtMatmulDescDestroy(ch.desc);
+            return as_hip(st);
+        }
+        cit = g->choices.emplace(ckey, ch).first;
     }
-    const Plan &p = it->second;
+    Choice &ch = cit->second;
+    const auto lkey = std::make_tuple(n, k, m, ldy, y_bf16, accumulate);
+    auto lit = g->layouts.find(lkey);
+    if (lit == g->layouts.end()) {
+        Layouts l;
+        hipblasLtMatmulHeuristicResult_t res[kCandidates];
+        int found = 0;
+        hipblasStatus_t st = make_layouts(n, k, m, ldy, y_bf16, l);
+        if (st == HIPBLAS_STATUS_SUCCESS) st = heuristic(*g, ch.desc, l, res, found);
+        if (st != HIPBLAS_STATUS_SUCCESS) {
+            destroy_layouts(l);
+            if (first_in_bucket) {
+                hipblasLtMatmulDescDestroy(ch.desc);
+                g->choices.erase(cit);
+            }
+            return as_hip(st);
+        }
+        int pick = 0;
+        if (first_in_bucket) {
+            if (found > 1) {
+                const size_t ybytes = ((size_t)(m - 1) * ldy + n) * (y_bf16 ? 2 : 4);
+                e = time_candidates(*g, ch.desc, l, res, found, W, x, ybytes, accumulate, s, pick);
+                if (e != hipSuccess) {
+                    destroy_layouts(l);
+                    hipblasLtMatmulDescDestroy(ch.desc);
+                    g->choices.erase(cit);
+                    return e;
+                }
+            }
+            ch.algo = res[pick].algo;
+        } else {
+            for (int i = 0; i < found; i++)
+                if (res[i].state == HIPBLAS_STATUS_SUCCESS && same_algo(res[i].algo, ch.algo)) {
+                    pick = i;
+                    break;
+                }
+        }
+        l.algo = res[pick].algo;
+        l.ws = res[pick].workspaceSize;
+        lit = g->layouts.emplace(lkey, l).first;
+    }
+    const Layouts &l = lit->second;
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
-    hipblasStatus_t st = hipblasLtMatmul(d.handle, p.desc, &alpha, W, p.a, x, p.b, &beta, y, p.c, y, p.c, &p.algo,
-                                         d.workspace, p.ws, s);
+    hipblasStatus_t st = hipblasLtMatmul(g->handle, ch.desc, &alpha, W, l.a, x, l.b, &beta, y, l.c, y, l.c, &l.algo,
+                                         g->workspace, l.ws, s);
     return as_hip(st);
 }
 

@@ -43,15 +43,19 @@ struct HipError {
         if (e_ != hipSuccess) throw HipError{e_, #call};     \
     } while (0)
 
-// A device buffer that grows on demand and never shrinks.
+// A device buffer that grows on demand and never shrinks.  A buffer that
+// belongs to a context bumps the context's generation when it moves, so that
+// recordings holding its old address can be refused (hymt_graph_launch).
 struct DevBuf {
     void *p = nullptr;
     size_t bytes = 0;
+    uint64_t *gen = nullptr;
     void reserve(size_t n) {
         if (n <= bytes) return;
         if (p) HIP_TRY(hipFree(p));
         p = nullptr;
         bytes = 0;
+        if (gen) ++*gen;
         HIP_TRY(hipMalloc(&p, n));
         bytes = n;
     }
@@ -113,10 +117,22 @@ struct hymt_ctx {
     DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
     DevBuf rows_idx;  // token ids of hymt_embed_rows
     HostBuf h_in, h_out;
+    // the prefill GEMMs' hipBLASLt state (created on the first GEMM)
+    GemmState *gemm = nullptr;
 
     // stream capture (hymt_graph_begin .. hymt_graph_end)
     bool capturing = false;
     bool capture_failed = false;
+    // bumped whenever a buffer above is reallocated: a recording replays the
+    // addresses it captured, so it is only valid for the generation it was
+    // recorded in
+    uint64_t gen = 0;
+
+    hymt_ctx() {
+        for (DevBuf *b : {&kpool, &vpool, &tab, &rope_cos, &rope_sin, &dec_ml, &dec_acc, &part_o, &part_ml, &in_q,
+                          &in_k, &in_v, &in_qnw, &in_knw, &out_o, &up_k, &up_v, &rows_idx})
+            b->gen = &gen;
+    }
 
     bool has_device() const { return device >= 0; }
     void *klayer(int l) const { return (char *)kpool.p + (size_t)l * layer_elems * dtype_bytes(kv_dtype); }
@@ -126,6 +142,7 @@ struct hymt_ctx {
 struct hymt_graph {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    uint64_t gen = 0;  // the context's buffer generation at recording
 };
 
 namespace {
@@ -167,6 +184,10 @@ void ensure_rope(hymt_ctx *c, int needed) {
     int cap = std::max(needed, 4096);
     if (c->rope_cap > 0) cap = std::max(cap, 2 * c->rope_cap);
     const int half = c->rope_dim / 2;
+    if (half == 0) {  // rope_dim 0: nothing rotates, the kernels read no table
+        c->rope_cap = cap;
+        return;
+    }
     std::vector<float> freqs(half), cs((size_t)cap * half), sn((size_t)cap * half);
     for (int i = 0; i < half; i++) freqs[i] = 1.0f / powf(c->rope_base, (float)i / (float)half);
     for (int pos = 0; pos < cap; pos++)
@@ -304,6 +325,8 @@ int hymt_destroy(hymt_ctx *c) {
             b->release();
         c->h_in.release();
         c->h_out.release();
+        gemm_state_destroy(c->gemm);
+        c->gemm = nullptr;
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -499,10 +522,10 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
                                          " exceeded at " + std::to_string(pos + 1));
     if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before decode");
-    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
     if (dev && !aligned16({q, k, v, qnw, knw, out}))
         return fail(HYMT_E_ARG, "device tensors must be 16-byte aligned");
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer decode")) return r;
     if (c->capturing && pos + 1 > c->rope_cap) return fail_capture(c, "RoPE table growth");
@@ -570,8 +593,12 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) +
                                          " exceeded at " + std::to_string((long)pos + seq));
     if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before prefill");
-    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     const bool dev = flags & HYMT_FLAG_DEVICE_PTRS;
+    // the kernels read q, k, v and the norm vectors and write out as 16-byte
+    // vectors (rows q_ld / kv_ld elements apart stay aligned: multiples of 8)
+    if (dev && !aligned16({q, k, v, qnw, knw, out}))
+        return fail(HYMT_E_ARG, "device tensors must be 16-byte aligned");
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer prefill")) return r;
     if (c->capturing && pos + seq > c->rope_cap) return fail_capture(c, "RoPE table growth");
@@ -766,6 +793,7 @@ int hymt_graph_end(hymt_ctx *c, hymt_graph **out) {
         return fail(HYMT_E_OOM, "host allocation failed");
     }
     hg->graph = g;
+    hg->gen = c->gen;
     e = hipGraphInstantiate(&hg->exec, g, nullptr, nullptr, 0);
     if (e != hipSuccess) {
         (void)hipGraphDestroy(g);
@@ -780,6 +808,9 @@ int hymt_graph_launch(hymt_ctx *c, hymt_graph *g) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!g || !g->exec) return fail(HYMT_E_ARG, "null graph");
     if (c->capturing) return fail(HYMT_E_STATE, "cannot replay while recording");
+    if (g->gen != c->gen)
+        return fail(HYMT_E_STATE, "the recording holds addresses of context buffers that have since been "
+                                  "reallocated (RoPE table or workspace growth); record it again");
     (void)hipSetDevice(c->device);
     hipError_t e = hipGraphLaunch(g->exec, c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipGraphLaunch: ") + hipGetErrorString(e));
@@ -960,8 +991,10 @@ int hymt_gemm(hymt_ctx *c, const hymt_weight *w, int row0, int nrows, const void
     if (int r = refuse_in_capture(c, "hymt_gemm")) return r;
     try {
         HIP_TRY(hipSetDevice(c->device));
-        HIP_TRY(hymt::gemm_bf16(c->stream, w->dense + (size_t)row0 * w->dev.cols, nrows, w->dev.cols,
-                                (const uint16_t *)x, m, y, flags & HYMT_GEMM_OUT_BF16, flags & HYMT_GEMM_ACCUMULATE));
+        if (!c->gemm && !(c->gemm = gemm_state_create())) return fail(HYMT_E_OOM, "host allocation failed");
+        HIP_TRY(hymt::gemm_bf16(c->gemm, c->stream, w->dense + (size_t)row0 * w->dev.cols, nrows, w->dev.cols,
+                                (const uint16_t *)x, m, y, nrows, flags & HYMT_GEMM_OUT_BF16,
+                                flags & HYMT_GEMM_ACCUMULATE));
     } catch (const HipError &e) {
         return map_hip(e);
     }
@@ -1065,7 +1098,38 @@ struct hymt_model {
     const hymt_weight *embd = nullptr, *out = nullptr;
     const float *out_norm = nullptr;
     DevBuf h, qkv, ao, gu;
+    // prefill activations (hymt_model_prefill), allocated on its first call
+    // for kPrefillRows rows: x fp32 [C][H], xn bf16 [C][H], qkv bf16
+    // [C][q|k|v], ao fp32 and ao16 bf16 [C][qd], gu [C][2F] (bf16, or fp32
+    // with HYMT_PREFILL_GATE_UP_F32), act bf16 [C][F]; token ids through a
+    // pinned buffer whose last copy is marked by tok_ev
+    DevBuf px, pxn, pqkv, pao, pao16, pgu, pact, ptok;
+    HostBuf htok;
+    hipEvent_t tok_ev = nullptr;
 };
+
+namespace {
+constexpr int kPrefillRows = 2048;
+
+// The prefill GEMM path needs a bf16 dense copy of every layer weight and a
+// 16-bit cache (the prefill kernels read 16-bit pages).
+bool prefill_ready(const hymt_model *m) {
+    if (m->ctx->kv_dtype == HYMT_F32) return false;
+    for (const auto &Ly : m->L) {
+        for (const hymt_weight *w : Ly.w)
+            if (w && !w->dense) return false;
+        if (!Ly.down->dense) return false;
+    }
+    return true;
+}
+
+// y (+)= x . W^T over the weight's dense copy, rows ldy elements apart
+void model_gemm(hymt_ctx *c, const hymt_weight *w, const void *x, int m, void *y, int ldy, bool y_bf16, bool acc) {
+    if (!c->gemm && !(c->gemm = gemm_state_create())) throw HipError{hipErrorOutOfMemory, "gemm_state_create"};
+    HIP_TRY(gemm_bf16(c->gemm, c->stream, w->dense, w->dev.rows, w->dev.cols, (const uint16_t *)x, m, y, ldy, y_bf16,
+                      acc));
+}
+}  // namespace
 
 int hymt_model_create(hymt_ctx *c, int layers, int hidden, int ffn, int vocab, float eps, hymt_model **out) {
     if (int r = check_ctx(c, true, true)) return r;
@@ -1197,6 +1261,100 @@ int hymt_model_decode(hymt_model *m, int token, int pos, float *logits) {
     return HYMT_OK;
 }
 
+int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, float *logits, unsigned flags) {
+    if (!m) return fail(HYMT_E_ARG, "null model");
+    hymt_ctx *c = m->ctx;
+    if (int r = check_ctx(c, true, true)) return r;
+    if (!m->embd || !logits) return fail(HYMT_E_STATE, "hymt_model_set_io first (and a logits buffer)");
+    for (const auto &Ly : m->L)
+        if (!Ly.set) return fail(HYMT_E_STATE, "every layer needs hymt_model_set_layer");
+    if (flags & ~HYMT_PREFILL_GATE_UP_F32) return fail(HYMT_E_ARG, "unknown prefill flags");
+    if (n < 1 || !tokens) return fail(HYMT_E_ARG, "empty token list");
+    for (int i = 0; i < n; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->vocab) return fail(HYMT_E_ARG, "token out of range");
+    if (pos < 0) return fail(HYMT_E_ARG, "negative position");
+    if ((long)pos + n > c->pages.max_tokens())
+        return fail(HYMT_E_CAPACITY, "KV capacity " + std::to_string(c->pages.max_tokens()) + " exceeded at " +
+                                         std::to_string((long)pos + n));
+    if (!c->pages.resident(pos)) return fail(HYMT_E_STATE, "device KV must hold [0, pos) before prefill");
+    if (int r = refuse_in_capture(c, "hymt_model_prefill")) return r;
+    if (n == 1 || !prefill_ready(m)) {
+        // one token, an fp32 cache or no dense copies: the tokens run as
+        // decode steps, as ForwardStep does without a prefill path
+        for (int i = 0; i < n; i++)
+            if (int r = hymt_model_decode(m, tokens[i], pos + i, logits)) return r;
+        return HYMT_OK;
+    }
+    const int H = m->hidden, F = m->ffn, qd = c->heads * c->head_dim, kd = c->kv_heads * c->head_dim;
+    const int ld = qd + 2 * kd;
+    const bool gu32 = flags & HYMT_PREFILL_GATE_UP_F32;
+    const size_t C = kPrefillRows;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        m->px.reserve(C * H * 4);
+        m->pxn.reserve(C * H * 2);
+        m->pqkv.reserve(C * ld * 2);
+        m->pao.reserve(C * qd * 4);
+        m->pao16.reserve(C * qd * 2);
+        m->pgu.reserve(C * 2 * F * 4);
+        m->pact.reserve(C * F * 2);
+        m->ptok.reserve(C * 4);
+        if (!m->htok.p) {
+            m->htok.reserve(C * 4);
+            HIP_TRY(hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming));
+        }
+        float *x = (float *)m->px.p, *ao = (float *)m->pao.p;
+        uint16_t *xn = (uint16_t *)m->pxn.p, *qkv = (uint16_t *)m->pqkv.p, *ao16 = (uint16_t *)m->pao16.p;
+        uint16_t *act = (uint16_t *)m->pact.p;
+        void *gu = m->pgu.p;
+        for (int r0 = 0; r0 < n; r0 += kPrefillRows) {
+            const int rows = std::min(kPrefillRows, n - r0), p0 = pos + r0;
+            // token ids: host -> pinned -> device, the pinned buffer reused
+            // once the previous chunk's copy has read it
+            HIP_TRY(hipEventSynchronize(m->tok_ev));
+            std::memcpy(m->htok.p, tokens + r0, (size_t)rows * 4);
+            HIP_TRY(hipMemcpyAsync(m->ptok.p, m->htok.p, (size_t)rows * 4, hipMemcpyHostToDevice, c->stream));
+            HIP_TRY(hipEventRecord(m->tok_ev, c->stream));
+            HIP_TRY(launch_rows(m->embd->dev, (const int *)m->ptok.p, 0, rows, x, c->stream));
+            for (int l = 0; l < m->layers; l++) {
+                const hymt_model::Layer &Ly = m->L[l];
+                HIP_TRY(launch_rows_rmsnorm(x, rows, H, Ly.attn_norm, m->eps, xn, c->stream));
+                if (!Ly.w[1]) {
+                    model_gemm(c, Ly.w[0], xn, rows, qkv, ld, true, false);
+                } else {  // q, k, v as three matrices into the column ranges of one buffer
+                    model_gemm(c, Ly.w[0], xn, rows, qkv, ld, true, false);
+                    model_gemm(c, Ly.w[1], xn, rows, qkv + qd, ld, true, false);
+                    model_gemm(c, Ly.w[2], xn, rows, qkv + qd + kd, ld, true, false);
+                }
+                if (int r = prefill_impl(c, l, p0, rows, qkv, ld, qkv + qd, qkv + qd + kd, ld, HYMT_BF16, Ly.q_norm,
+                                         Ly.k_norm, ao, HYMT_FLAG_DEVICE_PTRS))
+                    return r;
+                HIP_TRY(launch_to_bf16(ao, (size_t)rows * qd, ao16, c->stream));
+                model_gemm(c, Ly.w[3], ao16, rows, x, H, false, true);
+                HIP_TRY(launch_rows_rmsnorm(x, rows, H, Ly.ffn_norm, m->eps, xn, c->stream));
+                if (!Ly.w[5]) {
+                    model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
+                } else {  // gate and up as two matrices into the halves of one row
+                    const size_t es = gu32 ? 4 : 2;
+                    model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
+                    model_gemm(c, Ly.w[5], xn, rows, (char *)gu + F * es, 2 * F, !gu32, false);
+                }
+                if (gu32)
+                    HIP_TRY(launch_rows_swiglu((const float *)gu, rows, F, act, c->stream));
+                else
+                    HIP_TRY(launch_rows_swiglu_bf16((const uint16_t *)gu, rows, F, act, c->stream));
+                model_gemm(c, Ly.down, act, rows, x, H, false, true);
+            }
+            if (r0 + rows == n)
+                HIP_TRY(launch_gemv(m->out->dev, x + (size_t)(rows - 1) * H, logits, HYMT_GEMV_IN_RMSNORM,
+                                    m->out_norm, m->eps, c->stream));
+        }
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
 int hymt_model_destroy(hymt_model *m) {
     if (!m) return HYMT_OK;
     hymt_ctx *c = m->ctx;
@@ -1204,7 +1362,11 @@ int hymt_model_destroy(hymt_model *m) {
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
     }
-    for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu}) b->release();
+    for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu, &m->px, &m->pxn, &m->pqkv, &m->pao, &m->pao16, &m->pgu,
+                      &m->pact, &m->ptok})
+        b->release();
+    m->htok.release();
+    if (m->tok_ev) (void)hipEventDestroy(m->tok_ev);
     delete m;
     return HYMT_OK;
 }

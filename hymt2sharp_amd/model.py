@@ -22,7 +22,9 @@ rows (Forward chunks a prompt by 1024, HunyuanDenseModel.cs:342-355; the
 result does not depend on the chunking, and 2048-row GEMMs fill the chip
 better), over bf16
 dense copies of the layer weights (the Vulkan prefill's 16-bit weight
-copies, VulkanBackend.cs:760-880):
+copies, VulkanBackend.cs:760-880).  hymt_model_prefill enqueues the whole
+prompt natively in one call; prefill_composed issues the same sequence as
+separate C ABI calls:
     X = token_embd[tokens]                                  hymt_embed_rows
     per layer l:
         XN = bf16 RMSNorm(X, attn_norm)                     hymt_rows_rmsnorm
@@ -140,12 +142,9 @@ class DeviceModel:
                                              L["q_norm"], L["k_norm"]))
         N.check(lib.hymt_model_set_io(self._native, self.embd,
                                       None if self.out is self.embd else self.out, self.out_norm))
-        # the SwiGLU row kernel reads gate and up from one [m][2F] GEMM output,
-        # so prompts of a model whose gate and up types differ (two matrices)
-        # run as decode steps; so do those of an fp32 cache (the prefill
-        # kernels read 16-bit pages)
-        self.prefill_enabled = prefill and kv_dtype != N.F32 and \
-            all(len(L["gate_up"]) == 1 for L in self.layers)
+        # prompts of an fp32 cache run as decode steps (the prefill kernels
+        # read 16-bit pages), as do prompts without dense weight copies
+        self.prefill_enabled = prefill and kv_dtype != N.F32
 
     def _buf(self, n):
         p = self.be.alloc(4 * n)
@@ -181,6 +180,17 @@ class DeviceModel:
             be.gemv(L["down"], self.gu, self.h, accumulate=True, swiglu=True)
         be.gemv(self.out, self.h, self.logits, rmsnorm=self.out_norm, eps=c.eps)
 
+    def prefill(self, tokens, pos: int, gate_up_f32: bool = False):
+        """Enqueue the prompt `tokens` at positions [pos, pos + len) with one
+        hymt_model_prefill call (chunks of 2048 rows, or decode steps without
+        dense copies or with an fp32 cache); the last row's logits land in
+        self.logits.  gate_up_f32 keeps the gate/up GEMM output in fp32, as
+        the reference's prefill does."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        flags = N.PREFILL_GATE_UP_F32 if gate_up_f32 else 0
+        N.check(self.be._lib.hymt_model_prefill(self._native, t.ctypes.data_as(ctypes.c_void_p), t.size, pos,
+                                                self.logits, flags))
+
     def _prefill_bufs(self):
         if self._pf is None:
             c, C = self.cfg, self.PREFILL_CHUNK
@@ -193,9 +203,11 @@ class DeviceModel:
                         "act": self._buf(C * F // 2)}
         return self._pf
 
-    def prefill(self, tokens, pos: int):
-        """Enqueue one prefill chunk (len(tokens) <= PREFILL_CHUNK) at
-        positions [pos, pos + len); the last row's logits land in self.logits."""
+    def prefill_composed(self, tokens, pos: int):
+        """The sequence of hymt_model_prefill for one chunk (len(tokens) <=
+        PREFILL_CHUNK) at positions [pos, pos + len), as separate C ABI calls
+        (a model with fused q/k/v and gate/up matrices); the last row's logits
+        land in self.logits."""
         be, c, B = self.be, self.cfg, self._prefill_bufs()
         m, H, F, qd, kd = len(tokens), c.hidden_size, c.ffn_size, self.qd, self.kd
         assert 0 < m <= self.PREFILL_CHUNK
@@ -228,13 +240,10 @@ class DeviceModel:
         decode step; several run as prefill chunks when the dense copies were
         made (LoadModel(prefill=True)), else as decode steps one by one."""
         tokens = [int(t) for t in tokens]
-        if len(tokens) > 1 and self.prefill_enabled:
-            for i in range(0, len(tokens), self.PREFILL_CHUNK):
-                chunk = tokens[i:i + self.PREFILL_CHUNK]
-                self.prefill(chunk, pos + i)
+        if len(tokens) > 1:
+            self.prefill(tokens, pos)
         else:
-            for i, t in enumerate(tokens):
-                self.step(t, pos + i)
+            self.step(tokens[0], pos)
         out = np.empty(self.cfg.vocab_size, np.float32)
         self.be.download(out, self.logits)
         return out

@@ -347,6 +347,30 @@ int hymt_model_set_io(hymt_model *model, const hymt_weight *token_embd, const hy
                       const float *out_norm);
 /* Enqueue the decode step of `token` at `pos`; logits: device pointer, vocab floats. */
 int hymt_model_decode(hymt_model *model, int token, int pos, float *logits);
+
+/* IComputeBackend.ForwardStep for n >= 1 tokens at positions [pos, pos+n)
+ * (IComputeBackend.cs:40-47) in one call: the prompt runs as prefill chunks
+ * of up to 2048 rows (Forward chunks by 1024, HunyuanDenseModel.cs:342-355;
+ * the result does not depend on the chunking), the Vulkan backend's recorded
+ * prefill (VulkanBackend.cs:760-880, 1017-1062) as native calls --
+ *   X = token_embd[tokens]
+ *   per layer: XN = bf16 RMSNorm(X, attn_norm); [Q|K|V] = XN W_qkv^T (bf16)
+ *              AO = causal prefill attention (RoPE, QK norm, append)
+ *              X += bf16(AO) W_o^T
+ *              GU = bf16 RMSNorm(X, ffn_norm) W_gate|up^T
+ *              X += bf16(silu(gate) * up) W_down^T
+ *   logits = W_out RMSNorm(X[n-1], output_norm)
+ * -- over the layer weights' bf16 dense copies (hymt_weight_dense), bf16 GEMM
+ * operands with fp32 accumulation.  GU is bf16 unless
+ * HYMT_PREFILL_GATE_UP_F32 keeps it fp32 as the reference's prefill does
+ * (its _pfGu buffer, VulkanBackend.cs:595,604); bf16 GU adds two bf16
+ * roundings per FFN element.  With n = 1, an fp32 cache, or a layer weight
+ * without a dense copy, the tokens run as decode steps (hymt_model_decode).
+ * tokens is a host array (read before the call returns); logits a device
+ * pointer (vocab floats, the last token's).  Not recordable. */
+#define HYMT_PREFILL_GATE_UP_F32 1u
+int hymt_model_prefill(hymt_model *model, const int32_t *tokens, int n, int pos, float *logits,
+                       unsigned flags);
 int hymt_model_destroy(hymt_model *model);
 
 #ifdef __cplusplus

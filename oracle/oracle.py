@@ -148,7 +148,7 @@ def neox_rope(x, start_pos: int, base: float, rope_dim: int | None = None) -> np
     """Ops.NeoXRoPE (Ops.cs:98-168) on x[tokens][heads][head_dim]; returns a copy."""
     x = _c32(x).copy()
     tokens, heads, head_dim = x.shape
-    lib().orc_neox_rope(_p(x), tokens, heads, head_dim, rope_dim or head_dim, start_pos, base)
+    lib().orc_neox_rope(_p(x), tokens, heads, head_dim, head_dim if rope_dim is None else rope_dim, start_pos, base)
     return x
 
 
@@ -224,7 +224,7 @@ def decode_attention(q, k, v, qnw, knw, cache_k, cache_v, kv_dtype, heads, kv_he
     out = np.zeros(heads * head_dim, dtype=np.float32)
     assert cache_k.flags.c_contiguous and cache_v.flags.c_contiguous
     lib().orc_decode_attention(_p(q), _p(k), _p(v), _p(qnw), _p(knw), _p(cache_k), _p(cache_v),
-                               kv_dtype, heads, kv_heads, head_dim, rope_dim or head_dim,
+                               kv_dtype, heads, kv_heads, head_dim, head_dim if rope_dim is None else rope_dim,
                                rope_base, eps, start, _p(out), threads)
     return out
 
@@ -242,7 +242,7 @@ def prefill_attention(q, k, v, qnw, knw, cache_k, cache_v, kv_dtype, heads, kv_h
     out = np.zeros((seq, heads * head_dim), dtype=np.float32)
     fn = lib().orc_forward_prefill_attention if chunked else lib().orc_prefill_attention
     fn(_p(q), _p(k), _p(v), _p(qnw), _p(knw), _p(cache_k), _p(cache_v), kv_dtype, heads, kv_heads,
-       head_dim, rope_dim or head_dim, rope_base, eps, start, seq, _p(out), threads)
+       head_dim, head_dim if rope_dim is None else rope_dim, rope_base, eps, start, seq, _p(out), threads)
     return out
 
 

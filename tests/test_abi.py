@@ -191,3 +191,62 @@ def test_backend_factory_names(monkeypatch):
         create_backend("metal")
     monkeypatch.setenv("HYMT_BACKEND", "cpu")
     assert create_backend() is None
+
+
+def test_misaligned_device_pointers_are_refused():
+    """Device-pointer decode and prefill (packed and strided) refuse tensors
+    that are not 16-byte aligned (the kernels load and store 16-byte vectors)
+    before they look for a device, so the refusal shows on a host-only
+    context; the pointers are never dereferenced."""
+    L, h = host_ctx(256)
+    try:
+        ok, bad = 1 << 20, (1 << 20) + 8  # addresses only
+        dev = N.FLAG_DEVICE_PTRS
+        N.check(L.hymt_kv_map(h, 0, 64))
+        # decode: every tensor argument, one at a time
+        for i in range(6):
+            args = [ok] * 6
+            args[i] = bad
+            q, k, v, qnw, knw, out = args
+            assert L.hymt_attn_decode(h, 0, 10, q, k, v, qnw, knw, out, dev) == N.HYMT_E_ARG
+            assert b"aligned" in L.hymt_last_error()
+        assert L.hymt_attn_decode(h, 0, 10, ok, ok, ok, None, None, ok, dev) == N.HYMT_E_NO_DEVICE
+        # packed prefill
+        for i in range(6):
+            args = [ok] * 6
+            args[i] = bad
+            q, k, v, qnw, knw, out = args
+            assert L.hymt_attn_prefill(h, 0, 0, 16, q, k, v, N.BF16, qnw, knw, out, dev) == N.HYMT_E_ARG
+            assert b"aligned" in L.hymt_last_error()
+        assert L.hymt_attn_prefill(h, 0, 0, 16, ok, ok, ok, N.BF16, None, None, ok, dev) == N.HYMT_E_NO_DEVICE
+        # strided prefill: base pointers checked, strides already multiples of 8
+        ld = 3072
+        for i in range(6):
+            args = [ok] * 6
+            args[i] = bad
+            q, k, v, qnw, knw, out = args
+            assert L.hymt_attn_prefill_ld(h, 0, 0, 16, q, ld, k, v, ld, N.BF16, qnw, knw, out, dev) == \
+                N.HYMT_E_ARG
+        assert L.hymt_attn_prefill_ld(h, 0, 0, 16, ok, ld, ok, ok, ld, N.BF16, None, None, ok, dev) == \
+            N.HYMT_E_NO_DEVICE
+        # host pointers are staged into aligned buffers: no refusal
+        q = np.zeros(4096, np.float32)
+        p = ctypes.c_void_p(q.ctypes.data + 4)
+        assert L.hymt_attn_decode(h, 0, 10, p, p, p, None, None, p, 0) == N.HYMT_E_NO_DEVICE
+    finally:
+        L.hymt_destroy(h)
+
+
+def test_model_prefill_refusals_without_device():
+    """hymt_model_prefill needs a model; its argument checks come back as
+    status codes."""
+    L = N.lib()
+    toks = np.zeros(4, np.int32)
+    assert L.hymt_model_prefill(None, toks.ctypes.data_as(ctypes.c_void_p), 4, 0, None, 0) == N.HYMT_E_ARG
+    L2, h = host_ctx(64)
+    try:
+        m = ctypes.c_void_p()
+        # a model needs a device
+        assert L2.hymt_model_create(h, 2, 2048, 6144, 512, 1e-5, ctypes.byref(m)) == N.HYMT_E_NO_DEVICE
+    finally:
+        L2.hymt_destroy(h)

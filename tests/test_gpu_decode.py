@@ -19,16 +19,16 @@ TOL = 1e-3
 DT = {"f32": F32, "f16": F16, "bf16": BF16}
 
 
-def make_backend(layers, cap, dtype):
-    return HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, cap, dtype)
+def make_backend(layers, cap, dtype, rope_dim=D):
+    return HipBackend(0).configure(HQ, HKV, D, rope_dim, BASE, EPS).create_cache(layers, cap, dtype)
 
 
 def run_case(oracle, dtype, pos, norm, config=1, salt=0, outlier_frac=0.0, kscale=None, layer=0,
-             layers=1):
+             layers=1, rope_dim=D):
     cap = pos + 1
     kb, vb = cache_rows(config, pos, dtype_scale=kscale, salt=salt, outlier_frac=outlier_frac)
     q, k, v, qnw, knw = new_token(config, salt, norm)
-    be = make_backend(layers, cap, dtype)
+    be = make_backend(layers, cap, dtype, rope_dim)
     try:
         if pos:
             be.UploadKv(layer, 0, pos, kb, vb)
@@ -38,7 +38,7 @@ def run_case(oracle, dtype, pos, norm, config=1, salt=0, outlier_frac=0.0, kscal
         be.Dispose()
     ck, cv = oracle_cache(kb, vb, cap, dtype)
     ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, dtype, HQ, HKV, D, BASE,
-                                  EPS, pos)
+                                  EPS, pos, rope_dim=rope_dim)
     return got, ref, (krow[0], vrow[0]), (oracle.from_storage(ck[pos], dtype),
                                           oracle.from_storage(cv[pos], dtype))
 
@@ -129,3 +129,17 @@ def test_decode_repeat_is_deterministic(hip_available):
     finally:
         be.Dispose()
     assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("rope_dim", [64, 32, 2, 0])
+@pytest.mark.parametrize("dtype,pos", [("f16", 4096), ("bf16", 700), ("f32", 513), ("f16", 9000)])
+def test_decode_partial_rotary(oracle, hip_available, rope_dim, dtype, pos):
+    """rope_dim < head_dim (ModelConfig.RopeDim, ModelConfig.cs:30): dims at
+    or past rope_dim pass through the rotation (Ops.cs:100, 157); rope_dim 0
+    rotates nothing.  These run the kernels' partial-rotary path (partner and
+    table index per element), single- and multi-page splits."""
+    dt = DT[dtype]
+    got, ref, (kr, vr), (kr_ref, vr_ref) = run_case(oracle, dt, pos, "gamma", config=9,
+                                                    salt=rope_dim + pos, rope_dim=rope_dim)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+    assert ulp_close(kr, kr_ref, dt) and ulp_close(vr, vr_ref, dt)

@@ -142,3 +142,46 @@ def test_unrecordable_calls_are_refused(hip_available):
             be.free(p)
     finally:
         be.Dispose()
+
+
+def test_recording_refused_after_buffer_growth(hip_available):
+    """A recording replays the addresses of the context buffers it captured.
+    Growing one of them afterwards (here the RoPE table, by an eager decode
+    past its 4096 rows) makes hymt_graph_launch refuse the old recording
+    instead of replaying reads of freed memory; a new recording runs."""
+    pos = 64
+    be = backend(1, 5000, F16)
+    L = N.lib()
+    try:
+        kb, vb = cache_rows(14, pos)
+        be.UploadKv(0, 0, pos, kb, vb)
+        q, k, v, qnw, knw = new_token(14, 0, "gamma")
+        dq, dk, dv = dev_inputs(be, [q, k, v])
+        dout = be.alloc(q.nbytes)
+        be.MapRange(0, 5000)
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
+        be.sync()
+        be.graph_begin()
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
+        g = be.graph_end()
+        be.graph_launch(g)
+        be.sync()
+        ref = be.download(np.empty(HQ * D, np.float32), dout)
+        be.decode_dev(0, 4999, dq, dk, dv, None, None, dout)  # the RoPE table grows
+        be.sync()
+        assert L.hymt_graph_launch(be.handle, g) == N.HYMT_E_STATE
+        assert b"record it again" in L.hymt_last_error()
+        be.graph_destroy(g)
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)  # row pos rewritten as before
+        be.graph_begin()
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
+        g = be.graph_end()
+        be.upload(dout, np.zeros_like(q))
+        be.graph_launch(g)
+        be.sync()
+        assert np.array_equal(be.download(np.empty(HQ * D, np.float32), dout), ref)
+        be.graph_destroy(g)
+        for p in (dq, dk, dv, dout):
+            be.free(p)
+    finally:
+        be.Dispose()

@@ -21,6 +21,7 @@ import numpy as np
 import pytest
 
 from hymt2sharp_amd import BF16, F16, HipBackend
+from hymt2sharp_amd.backend import NotSupportedError
 from hymt2sharp_amd import synth as S
 from tests.attn_cases import (BASE, D, EPS, HKV, HQ, cache_rows, max_rel, new_token,
                               oracle_cache)
@@ -31,8 +32,8 @@ pytestmark = pytest.mark.gpu
 U = {BF16: 2.0 ** -9, F16: 2.0 ** -11}
 
 
-def make_backend(layers, cap, dtype):
-    return HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(layers, cap, dtype)
+def make_backend(layers, cap, dtype, rope_dim=D):
+    return HipBackend(0).configure(HQ, HKV, D, rope_dim, BASE, EPS).create_cache(layers, cap, dtype)
 
 
 def check(got, ref, vals_v, dtype, model=None):
@@ -48,13 +49,14 @@ def check(got, ref, vals_v, dtype, model=None):
     return max_rel(got, ref), d.max()
 
 
-def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, with_model=True):
+def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, with_model=True,
+                rope_dim=D):
     kb, vb = cache_rows(config, pos, salt=salt)
     q, k, v, qnw, knw = new_token(config, salt, norm, seq=seq)
     if io_bf16:  # bf16 inputs: both sides see the same bf16-representable values
         q, k, v = (S.bf16_bits_to_f32(S.f32_to_bf16_bits(x)).reshape(x.shape) for x in (q, k, v))
     cap = pos + seq
-    be = make_backend(1, cap, dtype)
+    be = make_backend(1, cap, dtype, rope_dim)
     try:
         if pos:
             be.UploadKv(0, 0, pos, kb, vb)
@@ -69,11 +71,11 @@ def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, wi
         be.Dispose()
     ck, cv = oracle_cache(kb, vb, cap, dtype)
     ref = oracle.prefill_attention(q, k, v, qnw, knw, ck, cv, dtype, HQ, HKV, D, BASE, EPS, pos,
-                                   threads=8)
+                                   threads=8, rope_dim=rope_dim)
     kf, vf = oracle.from_storage(ck, dtype), oracle.from_storage(cv, dtype)
     model = None
     if with_model:
-        qh = oracle.neox_rope(q.reshape(seq, HQ, D), pos, BASE)
+        qh = oracle.neox_rope(q.reshape(seq, HQ, D), pos, BASE, rope_dim=rope_dim)
         if qnw is not None:
             qh = oracle.rmsnorm(qh, qnw, EPS)
         model = prefill_model(qh.reshape(seq, HQ * D), kf, vf, HQ, HKV, D, pos, seq, dtype)
@@ -166,3 +168,29 @@ def test_back_to_back_launches_on_one_context(hip_available):
     finally:
         fresh.Dispose()
     assert np.array_equal(got, again)
+
+
+@pytest.mark.parametrize("rope_dim", [64, 0])
+@pytest.mark.parametrize("dtype,pos,seq", [(BF16, 0, 300), (F16, 100, 190), (BF16, 8192, 256)])
+def test_prefill_partial_rotary(oracle, hip_available, rope_dim, dtype, pos, seq):
+    """rope_dim 64 (half the head rotated) and 0 (no rotation): the prefill
+    kernels' partial-rotary instances (k/v kernel and the flash kernel's q
+    prologue), against the oracle with the same rope_dim."""
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, dtype, pos, seq, "gamma", 13,
+                                                              salt=rope_dim + seq, rope_dim=rope_dim)
+    check(got, ref, vf, dtype, model)
+    assert np.array_equal(vd, vref)
+    assert max_rel(kd, kref) <= 2.0 ** -7
+
+
+def test_prefill_refuses_other_rope_dims(hip_available):
+    """The prefill kernels are built for rope_dim 0, 64 and 128; other widths
+    are refused (decode accepts any even width)."""
+    be = make_backend(1, 64, BF16, rope_dim=32)
+    try:
+        q = np.zeros((4, HQ * D), np.float32)
+        k = np.zeros((4, HKV * D), np.float32)
+        with pytest.raises(NotSupportedError):
+            be.PrefillAttention(0, 0, q, k, k)
+    finally:
+        be.Dispose()

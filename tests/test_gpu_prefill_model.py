@@ -237,3 +237,60 @@ def test_strided_prefill_equals_packed(be):
     finally:
         for p in (dq, dk, dv, dqkv, dg, o1, o2):
             be.free(p)
+
+
+def _read_logits(be, m):
+    return be.download(np.empty(CFG.vocab_size, np.float32), m.logits)
+
+
+@pytest.mark.parametrize("n", [70, 2100])
+def test_native_prefill_equals_composed_calls(be, n):
+    """hymt_model_prefill (one C ABI call, 2048-row chunks) gives the same
+    logits and cache rows, bit for bit, as the same sequence issued as
+    separate C ABI calls (DeviceModel.prefill_composed), on one context (so
+    both use the same GEMM algorithms).  n = 2100 runs two chunks."""
+    cfg = ModelConfig(num_layers=2, vocab_size=512)
+    t = S.random_model(8, cfg, {"attn": N.W_Q4_K, "ffn": N.W_Q8_0, "embd": N.W_Q6_K, "out": N.W_Q6_K})
+    be.LoadModel(t, cfg, max_tokens=n + 64, kv_dtype=N.BF16)
+    m = be._model
+    toks = [int(x) for x in np.random.default_rng(n).integers(0, cfg.vocab_size, n)]
+    m.prefill(toks, 0)
+    be.sync()
+    native = _read_logits(be, m)
+    kv_native = [be.ReadKv(l, 0, n) for l in range(cfg.num_layers)]
+    for i in range(0, n, DeviceModel.PREFILL_CHUNK):
+        m.prefill_composed(toks[i:i + DeviceModel.PREFILL_CHUNK], i)
+    be.sync()
+    composed = _read_logits(be, m)
+    assert np.array_equal(native, composed)
+    for l in range(cfg.num_layers):
+        k, v = be.ReadKv(l, 0, n)
+        assert np.array_equal(k, kv_native[l][0]) and np.array_equal(v, kv_native[l][1]), l
+    # an argument error enqueues nothing
+    with pytest.raises(N.ArgumentError):
+        m.prefill([0, cfg.vocab_size], n)
+    with pytest.raises(N.NotSupportedError):
+        m.prefill([1] * 200, n)  # past the capacity
+
+
+def test_deep_prefill_gate_up_rounding(be):
+    """The bf16 gate/up GEMM output (two extra bf16 roundings per FFN element
+    against the reference's fp32 _pfGu, VulkanBackend.cs:595,604) over a
+    6-layer model: logits of both forms within the prefill bound of the
+    oracle's fp32/double decode steps; their distances are printed."""
+    cfg = ModelConfig(num_layers=6, vocab_size=512)
+    t = S.random_model(12, cfg, {"attn": N.W_Q4_K, "ffn": N.W_Q4_K, "embd": N.W_Q6_K, "out": N.W_Q6_K})
+    toks = [int(x) for x in np.random.default_rng(12).integers(0, cfg.vocab_size, 24)]
+    om = OracleModel(cfg, t, 64, N.BF16)
+    ref = om.forward(toks, 0)
+    be.LoadModel(t, cfg, max_tokens=64, kv_dtype=N.BF16)
+    m = be._model
+    errs = {}
+    for f32 in (False, True):
+        m.prefill(toks, 0, gate_up_f32=f32)
+        be.sync()
+        got = _read_logits(be, m)
+        errs[f32] = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
+    print(f"6-layer prefill logits rel: bf16 gate/up {errs[False]:.2e}, fp32 gate/up {errs[True]:.2e}",
+          flush=True)
+    assert errs[False] <= PREFILL_BOUND and errs[True] <= PREFILL_BOUND

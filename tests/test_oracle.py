@@ -122,6 +122,12 @@ def test_rope_partial_rotary_dims(oracle):
     want = np_ref.rope(x, 17, 10000.0, rope_dim=64)
     assert np.max(np.abs(got - want)) < 1e-5
     assert np.array_equal(got[..., 64:], x[..., 64:])
+    # rope_dim 0 (a GGUF rope.dimension_count of 0, ModelConfig.cs:30): no rotation
+    assert np.array_equal(oracle.neox_rope(x, 17, 10000.0, rope_dim=0), x)
+    # rope_dim 2: one rotated pair per head
+    got = oracle.neox_rope(x, 17, 10000.0, rope_dim=2)
+    want = np_ref.rope(x, 17, 10000.0, rope_dim=2)
+    assert np.max(np.abs(got - want)) < 1e-5 and np.array_equal(got[..., 2:], x[..., 2:])
 
 
 def test_rmsnorm_closed_form(oracle):
