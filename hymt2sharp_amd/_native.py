@@ -83,6 +83,7 @@ SIGNATURES = {
     "hymt_kv_upload": [_vp, _i, _i, _i, _vp, _vp],
     "hymt_kv_read": [_vp, _i, _i, _i, _vp, _vp],
     "hymt_attn_decode": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_uint],
+    "hymt_attn_decode_noalloc": [_vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp],
     "hymt_attn_prefill": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_attn_prefill_ld": [_vp, _i, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_sync": [_vp],

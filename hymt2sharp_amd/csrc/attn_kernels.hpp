@@ -139,6 +139,10 @@ __host__ __device__ inline int pair_tiles(int pos0, int pair, int nb16, int seq)
 
 // kv dtype codes as in hymt_dtype.
 hipError_t launch_decode(int kv_dtype, const DecodeArgs &a, hipStream_t s);
+// The static decode workspace (decode_attn.hip): resolve its address on
+// `device` (call with that device current, once per device), then fetch it.
+hipError_t decode_scratch_init(int device);
+hipError_t decode_scratch(int device, float **part_ml, float **part_acc, int *max_heads);
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s);
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s);
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s);

@@ -21,6 +21,7 @@
 //   q rows, then the K/V stream; no workgroup barrier before the final
 //   combine of the 4 wave partials.  Splits are merged by a second launch.
 #include <algorithm>
+#include <mutex>
 
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
@@ -592,6 +593,48 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
         ((float4 *)(a.out + (size_t)h * D))[d4] = make_float4(Ot.x * inv, Ot.y * inv, Ot.z * inv, Ot.w * inv);
     }
+}
+
+// ---- the decode workspace of hymt_attn_decode_noalloc ------------------------
+// A file-scope device array holds the split partials -- (m, l) then acc, laid
+// out as DecodeArgs.part_ml / part_acc for up to kScratchHeads q heads -- so
+// that a decode call needs no device allocation.  Every GPU that loads the
+// library holds its own copy until the process ends; its address on a
+// device comes from hipGetSymbolAddress with that device current (in host
+// code the array's name is not a device address).  Every call on one GPU
+// shares the array: the splits overwrite every partial the merge reads, so
+// nothing needs clearing, and calls that overlap on one GPU race.
+constexpr int kScratchHeads = 32;
+constexpr size_t kScratchMl = (size_t)kScratchHeads * kMaxSplits * 2;        // floats
+constexpr size_t kScratchAcc = (size_t)kScratchHeads * kMaxSplits * kHeadDim;  // floats
+static __device__ __align__(256) float scratch[kScratchMl + kScratchAcc];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch[kScratchDevices] = {};
+}  // namespace
+
+hipError_t decode_scratch_init(int device) {
+    if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch[device]) return hipSuccess;
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));  // the current device's copy
+    if (e != hipSuccess) return e;
+    g_scratch[device] = (float *)ptr;
+    return hipSuccess;
+}
+
+hipError_t decode_scratch(int device, float **part_ml, float **part_acc, int *max_heads) {
+    if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    float *p = g_scratch[device];
+    if (!p) return hipErrorNotInitialized;
+    *part_ml = p;
+    *part_acc = p + kScratchMl;
+    *max_heads = kScratchHeads;
+    return hipSuccess;
 }
 
 using DecodeKernel = void (*)(DecodeArgs);

@@ -177,8 +177,11 @@ void map_write(hymt_ctx *c, int pos, int len) {
     flush_table(c);
 }
 
-// Ops.EnsureRopeTable (Ops.cs:170-195): capacity max(needed, 4096), grown by
-// doubling; freq_i = 1 / base^(i/half), angle = pos * freq in fp32.
+// Ops.EnsureRopeTable (Ops.cs:170-195): freq_i = 1 / base^(i/half), angle =
+// pos * freq in fp32; rows [0, max(needed, 4096)).  The reference grows its
+// table on demand; here it is built once for the cache's capacity when the
+// cache is created (a row's values do not depend on the table's size), so
+// no attention call ever reallocates it.
 void ensure_rope(hymt_ctx *c, int needed) {
     if (needed <= c->rope_cap) return;
     int cap = std::max(needed, 4096);
@@ -300,6 +303,9 @@ int hymt_create(int device, hymt_ctx **out) {
         }
         HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
         c->device = device;
+        // the no-allocation decode's static workspace: its address on this
+        // device, resolved once per device while the device is current
+        HIP_TRY(decode_scratch_init(device));
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -374,6 +380,7 @@ int hymt_kv_create(hymt_ctx *c, int layers, int max_tokens, int kv_dtype) {
             HIP_TRY(hipMemset(c->tab.p, 0xFF, (size_t)P * 4));
             c->dec_ml.reserve((size_t)c->heads * kMaxSplits * 2 * 4);
             c->dec_acc.reserve((size_t)c->heads * kMaxSplits * kHeadDim * 4);
+            ensure_rope(c, c->pages.max_tokens());
         } catch (const HipError &e) {
             c->kpool.release();
             c->vpool.release();
@@ -512,9 +519,11 @@ int hymt_kv_read(hymt_ctx *c, int layer, int pos, int len, float *k_out, float *
     return HYMT_OK;
 }
 
-int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const float *k,
-                     const float *v, const float *qnw, const float *knw, float *out,
-                     unsigned flags) {
+// scratch_ml / scratch_acc: the split partials of a no-allocation call (the
+// static device workspace), or null for the context's own buffers
+static int decode_impl(hymt_ctx *c, int layer, int pos, const float *q, const float *k, const float *v,
+                       const float *qnw, const float *knw, float *out, unsigned flags, float *scratch_ml,
+                       float *scratch_acc) {
     if (int r = check_ctx(c, true, false)) return r;
     if (layer < 0 || layer >= c->layers || pos < 0 || !q || !k || !v || !out)
         return fail(HYMT_E_ARG, "invalid decode arguments");
@@ -528,12 +537,10 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer decode")) return r;
-    if (c->capturing && pos + 1 > c->rope_cap) return fail_capture(c, "RoPE table growth");
     if (c->capturing && c->pages.needs_copy(pos, 1)) return fail_capture(c, "a write into a harvested block");
     try {
         HIP_TRY(hipSetDevice(c->device));
-        map_write(c, pos, 1);
-        ensure_rope(c, pos + 1);
+        map_write(c, pos, 1);  // the RoPE table already covers the capacity
         const size_t D = c->head_dim, qn = (size_t)c->heads * D, kn = (size_t)c->kv_heads * D;
         if (!dev) {
             stage_in(c, {{q, qn * 4, &c->in_q}, {k, kn * 4, &c->in_k}, {v, kn * 4, &c->in_v},
@@ -552,8 +559,8 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         a.tab = (const int32_t *)c->tab.p;
         a.kpool = c->klayer(layer);
         a.vpool = c->vlayer(layer);
-        a.part_ml = (float *)c->dec_ml.p;
-        a.part_acc = (float *)c->dec_acc.p;
+        a.part_ml = scratch_ml ? scratch_ml : (float *)c->dec_ml.p;
+        a.part_acc = scratch_acc ? scratch_acc : (float *)c->dec_acc.p;
         a.out = dev ? out : (float *)c->out_o.p;
         a.L = pos + 1;
         a.kv_heads = c->kv_heads;
@@ -575,6 +582,26 @@ int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const floa
         return fail(HYMT_E_CAPACITY, e.what());
     }
     return HYMT_OK;
+}
+
+int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const float *k, const float *v,
+                     const float *qnw, const float *knw, float *out, unsigned flags) {
+    return decode_impl(c, layer, pos, q, k, v, qnw, knw, out, flags, nullptr, nullptr);
+}
+
+int hymt_attn_decode_noalloc(hymt_ctx *c, int layer, int pos, const float *q, const float *k, const float *v,
+                             const float *qnw, const float *knw, float *out) {
+    if (int r = check_ctx(c, true, false)) return r;
+    if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
+    float *ml = nullptr, *acc = nullptr;
+    int max_heads = 0;
+    const hipError_t e = decode_scratch(c->device, &ml, &acc, &max_heads);
+    if (e != hipSuccess)
+        return fail(HYMT_E_DEVICE, std::string("decode workspace not resolved on this device: ") + hipGetErrorString(e));
+    if (c->heads > max_heads)
+        return fail(HYMT_E_UNSUPPORTED, "the static decode workspace holds " + std::to_string(max_heads) +
+                                            " q heads; the context has " + std::to_string(c->heads));
+    return decode_impl(c, layer, pos, q, k, v, qnw, knw, out, HYMT_FLAG_DEVICE_PTRS, ml, acc);
 }
 
 // q_ld / kv_ld: elements from one q (k, v) row to the next; 0 = packed rows
@@ -601,12 +628,10 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer prefill")) return r;
-    if (c->capturing && pos + seq > c->rope_cap) return fail_capture(c, "RoPE table growth");
     if (c->capturing && c->pages.needs_copy(pos, seq)) return fail_capture(c, "a write into a harvested block");
     try {
         HIP_TRY(hipSetDevice(c->device));
-        map_write(c, pos, seq);
-        ensure_rope(c, pos + seq);
+        map_write(c, pos, seq);  // the RoPE table already covers the capacity
         const size_t D = c->head_dim, es = dtype_bytes(io_dtype);
         const size_t qn = (size_t)seq * c->heads * D, kn = (size_t)seq * c->kv_heads * D;
         if (!dev) {

@@ -165,6 +165,21 @@ int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const fl
                      unsigned flags);
 
 /*
+ * hymt_attn_decode for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * It has no counterpart in the reference.  Device pointers only (as
+ * HYMT_FLAG_DEVICE_PTRS), same arguments and result as hymt_attn_decode, and
+ * it never calls hipMalloc or hipFree: the split partials live in a static
+ * device array of the library (2.03 MiB per GPU, held until the process
+ * ends; room for 32 q heads, a larger head count is HYMT_E_UNSUPPORTED), and
+ * the RoPE table is built for the whole cache by hymt_kv_create.  All
+ * contexts on one GPU share that array: calls that overlap on one GPU (two
+ * contexts' streams) race, so callers serialise them.
+ */
+int hymt_attn_decode_noalloc(hymt_ctx *ctx, int layer, int pos, const float *q, const float *k,
+                             const float *v, const float *qnw, const float *knw, float *out);
+
+/*
  * Causal prefill attention for one layer: `seq` tokens at positions
  * [pos, pos+seq), attending over [0, pos+row].  Same steps as decode; K/V of
  * the chunk are written into the cache.  q/k/v are fp32 or bf16 as io_dtype;
@@ -207,7 +222,10 @@ int hymt_sync(hymt_ctx *ctx);
  * :400-568) and submits it per token (:677).  Replays repeat the recorded
  * arguments (positions included).  During capture, calls that synchronise,
  * copy host memory or would grow a device workspace return HYMT_E_STATE, so a
- * sequence is warmed up once eagerly before it is recorded.  Such a refusal
+ * sequence is warmed up once eagerly before it is recorded.  A recording
+ * holds the addresses of the context's workspaces: when a later eager call
+ * grows one of them, hymt_graph_launch refuses the recording (HYMT_E_STATE)
+ * and it must be recorded again.  Such a refusal
  * spoils the recording: it stays open, and hymt_graph_end discards it and
  * reports the failure.  A call rejected for its arguments records nothing
  * and leaves the recording intact.

@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from hymt2sharp_amd import BF16, F16, HipBackend
+from hymt2sharp_amd import BF16, F16, F32, HipBackend
 from hymt2sharp_amd import _native as N
 from hymt2sharp_amd import synth as S
 from tests.attn_cases import BASE, D, EPS, HKV, HQ, cache_rows, new_token
@@ -99,12 +99,12 @@ def test_recorded_prefill_replays_exactly(hip_available):
 
 
 def test_unrecordable_calls_are_refused(hip_available):
-    pos = 64
-    be = backend(1, 5000, F16)
+    pos, ctx = 64, 2048
+    be = backend(1, ctx + 64, F16)
     L = N.lib()
     try:
-        kb, vb = cache_rows(13, pos)
-        be.UploadKv(0, 0, pos, kb, vb)
+        kb, vb = cache_rows(13, ctx)
+        be.UploadKv(0, 0, ctx, kb, vb)
         q, k, v, qnw, knw = new_token(13, 0, "gamma")
         be.graph_begin()
         # host pointers synchronise: refused, and the recording is spoiled
@@ -114,18 +114,24 @@ def test_unrecordable_calls_are_refused(hip_available):
         assert L.hymt_graph_begin(be.handle) == N.HYMT_E_STATE  # already open
         with pytest.raises(N.InvalidOperationError):
             be.graph_end()
-        # a device-pointer call whose RoPE table would grow is refused too
+        # a device-pointer call whose workspace would grow is refused too: a
+        # 64-token prefill over 2048 cached positions splits its kv ranges
+        # and needs the split workspace, which no call has allocated yet
         dq, dk, dv = dev_inputs(be, [q, k, v])
         dout = be.alloc(q.nbytes)
-        be.MapRange(0, 5000)
-        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)  # table of 4096 rows
+        qp, kp, vp = new_token(13, 1, None, seq=64)[:3]
+        dqp, dkp, dvp = dev_inputs(be, [qp, kp, vp])
+        doutp = be.alloc(qp.nbytes)
+        be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
         be.sync()
         be.graph_begin()
         with pytest.raises(N.InvalidOperationError) as e:
-            be.decode_dev(0, 4999, dq, dk, dv, None, None, dout)
-        assert "RoPE table growth" in str(e.value)
+            be.prefill_dev(0, ctx, 64, dqp, dkp, dvp, F32, None, None, doutp)
+        assert "workspace growth" in str(e.value)
         with pytest.raises(N.InvalidOperationError):
             be.graph_end()
+        for p in (dqp, dkp, dvp, doutp):
+            be.free(p)
         # an argument error records nothing and leaves the recording usable
         be.graph_begin()
         with pytest.raises(N.ArgumentError):
@@ -146,19 +152,19 @@ def test_unrecordable_calls_are_refused(hip_available):
 
 def test_recording_refused_after_buffer_growth(hip_available):
     """A recording replays the addresses of the context buffers it captured.
-    Growing one of them afterwards (here the RoPE table, by an eager decode
-    past its 4096 rows) makes hymt_graph_launch refuse the old recording
-    instead of replaying reads of freed memory; a new recording runs."""
-    pos = 64
-    be = backend(1, 5000, F16)
+    Growing one of them afterwards (here the prefill split workspace, by an
+    eager 64-token prefill over 2048 cached positions) makes
+    hymt_graph_launch refuse the old recording instead of replaying accesses
+    of freed memory; a new recording runs."""
+    pos, ctx = 64, 2048
+    be = backend(1, ctx + 64, F16)
     L = N.lib()
     try:
-        kb, vb = cache_rows(14, pos)
-        be.UploadKv(0, 0, pos, kb, vb)
+        kb, vb = cache_rows(14, ctx)
+        be.UploadKv(0, 0, ctx, kb, vb)
         q, k, v, qnw, knw = new_token(14, 0, "gamma")
         dq, dk, dv = dev_inputs(be, [q, k, v])
         dout = be.alloc(q.nbytes)
-        be.MapRange(0, 5000)
         be.decode_dev(0, pos, dq, dk, dv, None, None, dout)
         be.sync()
         be.graph_begin()
@@ -167,8 +173,13 @@ def test_recording_refused_after_buffer_growth(hip_available):
         be.graph_launch(g)
         be.sync()
         ref = be.download(np.empty(HQ * D, np.float32), dout)
-        be.decode_dev(0, 4999, dq, dk, dv, None, None, dout)  # the RoPE table grows
+        qp, kp, vp = new_token(14, 1, None, seq=64)[:3]
+        dqp, dkp, dvp = dev_inputs(be, [qp, kp, vp])
+        doutp = be.alloc(qp.nbytes)
+        be.prefill_dev(0, ctx, 64, dqp, dkp, dvp, F32, None, None, doutp)  # the workspace grows
         be.sync()
+        for p in (dqp, dkp, dvp, doutp):
+            be.free(p)
         assert L.hymt_graph_launch(be.handle, g) == N.HYMT_E_STATE
         assert b"record it again" in L.hymt_last_error()
         be.graph_destroy(g)
