@@ -453,6 +453,57 @@ def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
             "cow_note": "GPU time of one copy-on-write: the page-copy kernel and the table update"}
 
 
+def measure_ceilings():
+    """Ceilings measured on this GPU (libhymt_ceilings.so, HIP events): the
+    cost of a dependent launch, the time to stream the decode call's bytes
+    (and a 32k-context layer's, and 1 GiB) from HBM with the decode kernel's
+    access pattern, the dense bf16 MFMA rate and the LDS read rate."""
+    from hymt2sharp_amd import build as B
+    L = ctypes.CDLL(B.CEIL_LIB)
+    d = ctypes.c_double()
+    i = ctypes.c_int()
+
+    def ck(rc):
+        if rc != 0:
+            raise RuntimeError(f"libhymt_ceilings call failed: hipError {rc}")
+
+    out = {}
+    for graph, name in ((1, "graph"), (0, "eager")):
+        ck(L.hc_launch_gap(graph, ctypes.byref(d)))
+        out[f"launch_gap_us_{name}"] = round(d.value, 3)
+    stream = {}
+    for label, nbytes in (("config2_layer", decode_bytes_per_layer(CTX + 1)),
+                          ("ctx32k_layer", decode_bytes_per_layer(32768)), ("1GiB", 1 << 30)):
+        row = {"bytes": nbytes}
+        for per in (4, 8, 16, 32):  # 16, 32, 64, 128 KiB per workgroup
+            for graph, name in ((1, "graph"), (0, "eager")):
+                if per != 8 and not graph:
+                    continue
+                ck(L.hc_stream_read(ctypes.c_size_t(nbytes), per, graph, ctypes.byref(d), ctypes.byref(i)))
+                row[f"{16 * per}k_us_{name}"] = round(d.value, 3)
+                row[f"{16 * per}k_gbs_{name}"] = round(nbytes / (d.value * 1e-6) / 1e9, 1)
+            row[f"{16 * per}k_workgroups"] = i.value
+        stream[label] = row
+    out["stream_read"] = stream
+    mf = {}
+    for w in (1, 2, 4):
+        ck(L.hc_mfma_bf16(w, ctypes.byref(d)))
+        mf[f"waves_per_simd_{w}"] = round(d.value, 1)
+    out["mfma_bf16_tflops"] = mf
+    lds = {}
+    for w in (1, 2):
+        ck(L.hc_lds_read(w, ctypes.byref(d)))
+        lds[f"wgs_per_cu_{w}"] = round(d.value, 2)
+    out["lds_read_tbs"] = lds
+    cu, clk, mclk, bus = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    ck(L.hc_device_info(ctypes.byref(cu), ctypes.byref(clk), ctypes.byref(mclk), ctypes.byref(bus)))
+    out["device"] = {"cus": cu.value, "clock_mhz": clk.value // 1000, "mem_clock_mhz": mclk.value // 1000,
+                     "bus_bits": bus.value}
+    out["note"] = ("per-launch times of back-to-back launches on one stream: a graph of them replayed, "
+                   "or enqueued one by one; stream reads rotate over > 1 GiB of buffers")
+    return out
+
+
 def cpu_threads():
     try:
         n = len(os.sched_getaffinity(0))
@@ -551,11 +602,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv", "model"],
+    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv", "model", "ceilings"],
                     default=None,
                     help="run one leg: the config-2 decode step, the config-3 prefill, "
-                         "the other configurations (1, 4, 5), the weight GEMVs or the "
-                         "whole-model decode step")
+                         "the other configurations (1, 4, 5), the weight GEMVs, the "
+                         "whole-model decode step or the measured ceilings")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
     ap.add_argument("--no-graph", action="store_true",
@@ -600,6 +651,8 @@ def main():
         extra["gemv"] = {"workload": "decode weight GEMV y += W x (batch 1, fp32 x/y) at the "
                                      "decode step's shapes, W streamed from HBM",
                          "unit": "GB/s of GGUF weight bytes", "cases": time_gemv()}
+    if args.only in (None, "ceilings"):
+        extra["ceilings"] = measure_ceilings()
     if args.only in (None, "model"):
         extra["model"] = time_model(steps=max(5, args.steps // 2), warmup=args.warmup,
                                     cpu_tokens=0 if args.no_cpu else 2)

@@ -1,7 +1,9 @@
 """Build the native pieces of hymt2sharp_amd in-tree.
 
-libhymt_hip.so   C ABI (include/hymt_hip.h) + gfx950 kernels, via hipcc
-libhymt_synth.so seeded input generator (plain C), via gcc
+libhymt_hip.so      C ABI (include/hymt_hip.h) + gfx950 kernels, via hipcc
+libhymt_synth.so    seeded input generator (plain C), via gcc
+libhymt_ceilings.so the benchmark's measured ceilings (launch gap, HBM stream
+                    read, MFMA and LDS rates), via hipcc
 
 Run `python -m hymt2sharp_amd.build` or call build_all().
 """
@@ -16,6 +18,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 HIP_LIB = os.path.join(PKG, "libhymt_hip.so")
 SYNTH_LIB = os.path.join(PKG, "libhymt_synth.so")
+CEIL_LIB = os.path.join(PKG, "libhymt_ceilings.so")
 
 # Sources of libhymt_hip.so and the extra compiler flags of each.
 HIP_SOURCES = {
@@ -72,6 +75,13 @@ def build_hip(extra=()):
     return HIP_LIB
 
 
+def build_ceilings():
+    tmp = CEIL_LIB + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "ceilings.hip"), "-o", tmp])
+    os.replace(tmp, CEIL_LIB)
+    return CEIL_LIB
+
+
 def build_synth():
     tmp = SYNTH_LIB + ".tmp"
     _run(["gcc", "-O2", "-fPIC", "-shared", "-std=c11", os.path.join(CSRC, "synth.c"), "-lm",
@@ -82,6 +92,7 @@ def build_synth():
 
 def build_all():
     build_synth()
+    build_ceilings()
     build_hip()
 
 

@@ -11,7 +11,7 @@ namespace hymt {
 constexpr int kHeadDim = 128;   // built head_dim (Hy-MT2-1.8B)
 constexpr int kGroup = 4;       // q heads per kv head (16 / 4)
 constexpr int kPage = 64;       // tokens per KV page
-constexpr int kMaxSplits = 128; // decode KV splits per kv head (merge width)
+constexpr int kMaxSplits = 256; // decode KV splits per kv head (merge width)
 constexpr int kArgPages = 256;  // decode page lists passed in kernel arguments
 constexpr int kItemTiles = 1024; // prefill kv tiles per work item (page ids staged in LDS)
 
@@ -55,33 +55,35 @@ template <int BYTES> __host__ __device__ inline size_t v_off(int t, int d) {
 }
 
 struct DecodeArgs {
-    // Ordered by first use in the kernels: the scalars that place a
-    // workgroup, then the pointers its first loads need.
-    int L;              // positions attended = pos + 1
-    int kv_heads;
-    int kv_shift;       // log2(kv_heads)
-    int ppw;            // pages per split (set by launch_decode)
-    int nsplit;         // splits per kv head (set by launch_decode)
-    int rope_half;
-    int rope_dim;
-    int pages_in_args;  // 1: pages[] below holds tab[0, npages) (npages <= kArgPages)
-    const float *q;     // [Hq*D]
-    const float *qnw;   // [D] or null
+    // Ordered for the kernel's prologue, which is one batch of scalar
+    // argument loads: the page ids (the K/V addresses hang on them), then the
+    // pointers and scalars of the first vector loads.  Every pointer is
+    // valid: an absent gamma or RoPE table is a ones vector.
+    int32_t pages[kArgPages];  // physical page of each logical block (when
+                               // pages_in_args), saving a dependent table load
+    const void *kpool;      // this layer's K pool
+    const void *vpool;      // this layer's V pool
+    const float *q;         // [Hq*D]
+    const float *knew;      // [Hkv*D]
+    const float *vnew;      // [Hkv*D]
+    const float *qnw;       // [D] gamma of q
+    const float *knw;       // [D] gamma of k
     const float *rope_cos;  // row `pos` of the cos table, [rope_half]
     const float *rope_sin;
-    const float *knew;  // [Hkv*D]
-    const float *knw;   // [D] or null
-    const float *vnew;  // [Hkv*D]
-    const int32_t *tab; // logical block -> physical page
-    void *kpool;        // this layer's K pool
-    void *vpool;        // this layer's V pool
+    int L;                  // positions attended = pos + 1
+    int kv_heads;
+    int ppw;                // pages per split (set by launch_decode)
+    int nsplit;             // splits per kv head (set by launch_decode)
+    int rope_half;
+    int rope_dim;
+    int norm_q, norm_k;     // apply the q / k RMSNorm
     float eps;
-    float qscale;       // log2(e) / sqrt(D)
-    float *out;         // [Hq*D]
-    float *part_ml;     // [Hq][kMaxSplits][2]
-    float *part_acc;    // [Hq][kMaxSplits][D]
-    int32_t pages[kArgPages];  // physical page of each logical block, saving a
-                               // dependent table load before the K/V stream
+    float qscale;           // log2(e) / sqrt(D)
+    int pages_in_args;      // 1: pages[] holds tab[0, ceil(L/64)) (<= kArgPages)
+    const int32_t *tab;     // logical block -> physical page
+    float *out;             // [Hq*D]
+    float *part_ml;         // [Hq][kMaxSplits][2]
+    float *part_acc;        // [Hq][kMaxSplits][D]
 };
 
 struct PrepArgs {

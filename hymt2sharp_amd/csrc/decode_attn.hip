@@ -149,9 +149,11 @@ __device__ __forceinline__ float wave_sum64(float v) { return xrow32_sum(xrow16_
 
 // NR consecutive head rows (q heads of one GQA group, or one k row) held as
 // lanes (d, d+64).  All loads -- rows, rotation partners, cos/sin, gamma --
-// are issued by load() before any use, in straight-line code, so they share
-// one memory round trip and can be issued ahead of the K/V stream; finish()
-// applies RoPE then RMSNorm (HunyuanDenseModel.Decode.cs:80-85).
+// are issued by load() before any use, unconditionally (the host passes a
+// ones vector for an absent gamma or RoPE table), so the kernel's prologue is
+// straight-line code: one batch of scalar argument loads, then every vector
+// load in one memory round trip.  finish() applies RoPE then RMSNorm
+// (HunyuanDenseModel.Decode.cs:80-85).
 // FULL: rotary width 128 (half 64), the partner of d is d^64 in the same
 // lane and no partner loads are needed.
 template <int NR, bool FULL> struct RowsIn {
@@ -163,26 +165,29 @@ template <int NR, bool FULL> struct RowsIn {
             x[r][0] = rows[r * kHeadDim + lane];
             x[r][1] = rows[r * kHeadDim + lane + 64];
         }
-        w[0] = gamma ? gamma[lane] : 1.0f;
-        w[1] = gamma ? gamma[lane + 64] : 1.0f;
+        w[0] = gamma[lane];
+        w[1] = gamma[lane + 64];
         if constexpr (FULL) {
             c[0] = c[1] = cosr[lane];
             s[0] = s[1] = sinr[lane];
         } else {
-            // partner index d when d is not rotated; table index 0 then (the
-            // table has at least one column whenever rdim > 0)
+            // partner index d and table index 0 when d is not rotated (the
+            // values are then unused)
 #pragma unroll
             for (int e = 0; e < 2; e++) {
                 const int d = lane + 64 * e;
 #pragma unroll
                 for (int r = 0; r < NR; r++) xp[r][e] = rows[r * kHeadDim + rope_partner(d, half, rdim)];
-                c[e] = rdim > 0 ? cosr[rope_index(d, half, rdim)] : 1.0f;
-                s[e] = rdim > 0 ? sinr[rope_index(d, half, rdim)] : 0.0f;
+                c[e] = cosr[rope_index(d, half, rdim)];
+                s[e] = sinr[rope_index(d, half, rdim)];
             }
         }
     }
     // Row r: RoPE (Ops.cs:157-165) then y = x * (1/sqrt(sum x^2/D + eps)) * gamma
-    // (Ops.cs:62-88), times `scale`.
+    // (Ops.cs:62-88), times `scale`.  Without the norm the factor is 1 and
+    // gamma the ones vector, so y = x exactly; gamma is used on both paths so
+    // that its loads stay ahead of the K/V stream (a load used only under a
+    // branch is sunk behind it, and vmcnt retires in order).
     __device__ __forceinline__ void finish(int r, float (&y)[2], int lane, int half, int rdim, bool norm,
                                            float eps, float scale) const {
 #pragma unroll
@@ -191,35 +196,77 @@ template <int NR, bool FULL> struct RowsIn {
             y[e] = FULL ? (e == 0 ? x[r][0] * c[0] - p * s[0] : p * s[1] + x[r][1] * c[1])
                         : rope_elem(lane + 64 * e, x[r][e], p, c[e], s[e], half, rdim);
         }
-        if (norm) {
-            const float ss = wave_sum64(y[0] * y[0] + y[1] * y[1]);
-            const float rr = 1.0f / sqrtf(ss / (float)kHeadDim + eps);
-            y[0] = y[0] * rr * w[0];
-            y[1] = y[1] * rr * w[1];
-        }
+        const float ss = wave_sum64(y[0] * y[0] + y[1] * y[1]);
+        const float rr = norm ? 1.0f / sqrtf(ss / (float)kHeadDim + eps) : 1.0f;
+        y[0] = y[0] * rr * w[0];
+        y[1] = y[1] * rr * w[1];
         y[0] *= scale;
         y[1] *= scale;
     }
 };
 
+// K and V operands of one wave for one page: its 16 positions.
+//   f16/bf16 pages: wave w takes the 16 positions of V chunks 2w and 2w+1, so
+//   that its V loads are whole 16-byte chunks; S row / P.V index 4 grp + i
+//   of the wave is page position posw(i).
+//   K A-operand: lane (grp, c) = K row c (position posw of index c), dims
+//     32*ks + 8*grp + [0, 8): two 128-byte segments per 16 lanes.
+//   V B-operand: lane (grp, c) = V^T row 16*db + c, indices 4*grp + [0, 4):
+//     half (grp & 1) of V chunk (2 w + (grp >> 1), 16 db + c).
+//   f32 pages (row-major K, V^T sub-tiles [16w, 16w+16)): the same operands
+//   as fp32, two 16-byte K loads per ks and one 16-byte V load per db.
+template <typename S> struct PageOps {
+    static constexpr bool W4 = sizeof(S) == 4;
+    static constexpr int KL = W4 ? 8 : 4;
+    using VL = typename std::conditional<W4, uint4, uint2>::type;
+    uint4 k[KL];
+    VL v[8];
+    __device__ __forceinline__ void load(const S *kpool, const S *vpool, size_t pb, int wave, int grp, int c) {
+        constexpr int D = kHeadDim, SUB = 16;
+        if constexpr (W4) {
+            const S *kp = kpool + pb + (size_t)(SUB * wave + c) * D + 8 * grp;
+            const S *vp = vpool + pb + (size_t)(wave * D + c) * SUB + 4 * grp;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                k[2 * ks] = *(const uint4 *)(kp + 32 * ks);
+                k[2 * ks + 1] = *(const uint4 *)(kp + 32 * ks + 4);
+            }
+#pragma unroll
+            for (int db = 0; db < 8; db++) v[db] = *(const VL *)(vp + 256 * db);
+        } else {
+            const S *kp = kpool + pb + 2048 * (2 * (wave >> 1) + ((c >> 2) & 1)) + 128 * grp +
+                          8 * (8 * (wave & 1) + 4 * (c >> 3) + (c & 3));
+            const S *vp = vpool + pb + (size_t)(2 * wave + (grp >> 1)) * 1024 + 8 * c + 4 * (grp & 1);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) k[ks] = *(const uint4 *)(kp + 512 * ks);
+#pragma unroll
+            for (int db = 0; db < 8; db++) v[db] = *(const VL *)(vp + 128 * db);
+        }
+    }
+};
+
 // Decode for every cache type.
 //   The cached positions [0, pos) are split by pages: workgroup (split, kv
-//   head), 4 waves; wave w streams the 16-position sub-tile [16w, 16w+16) of
-//   each of the split's pages.
+//   head), 4 waves, PPW pages per split whose K/V loads are all issued at
+//   once; wave w streams 16 positions of each page (PageOps).  For each page
 //     S = K_sub . Qcat^T, lane (grp, c<4) gets head c at positions 4*grp + i
 //     (its hi part; lanes c+4 hold the lo part).
+//   then one softmax over all the split's positions of the wave, then for
+//   each page
 //     O += Pcat . V_sub, lane (grp, c) gets rows 4*grp + i of dims 16*db + c,
 //     rows 0-3 = hi(P) of the 4 heads, rows 4-7 = lo(P).
-//   The new token (position pos) is one more position.  Wave 3 of the last
-//   split computes it on the VALU from registers -- its K after RoPE + norm,
-//   both rows rounded to the cache type as the reference reads them back from
-//   its cache -- and adds it to the split's combine as a fifth partial; the
-//   same wave appends the row to the cache at the end.  So no workgroup is
-//   spent on a page that holds only the new token (L = 4097 runs exactly 256
-//   workgroups), and no MFMA operand needs patching.
+//   A split of more than PPW pages runs its pages PPW at a time, merging the
+//   runs online.
+//   The new token (position pos) is one more position, handled in the last
+//   split on the VALU from registers while the K/V stream is in flight: wave
+//   w computes the new K row after RoPE + norm and V, both rounded to the
+//   cache type as the reference reads them back from its cache, and head w's
+//   weight for it, a fifth partial of the split's combine; wave 0 appends the
+//   row to the cache at the end.  So no workgroup is spent on a page that
+//   holds only the new token (L = 4097 runs exactly 256 workgroups).
 // PAGES_ARG: page ids come from the kernel arguments, else from the device
 // page table; both are scalar loads issued first.
-template <typename T, bool MULTI, bool PAGES_ARG, bool FULL>
+template <typename T, int PPW, bool RUNS, bool PAGES_ARG, bool FULL>
 __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     constexpr int D = kHeadDim, G = kGroup, P = kPage, SUB = 16;
     // f32 pages: each K and V operand is split on the fly into bf16 hi + lo
@@ -232,103 +279,118 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, c = lane & 15;  // MFMA lane group / row-col index
-    const int Hkv = a.kv_heads;
     const int split = blockIdx.x, kvh = blockIdx.y;  // grid (nsplit, kv heads)
-    const int newpos = a.L - 1;                // cached positions [0, newpos)
-    const int ncp = (newpos + P - 1) / P;      // cached pages
-    // one page per split unless MULTI: the first page id's address then
-    // depends on blockIdx alone and is loaded with the kernel arguments
-    const int page0 = MULTI ? split * a.ppw : split;
-    const int page_end = min(page0 + (MULTI ? a.ppw : 1), ncp);
-    const bool last = split == a.nsplit - 1;
-    const bool extra = last && wave == 3;      // the wave that adds the new token
 
     __shared__ __attribute__((aligned(16))) uint16_t s_qop[2][G][D];  // hi/lo q of the 4 heads
-    __shared__ float s_qf[G][D];                                      // fp32 q, for the new token
-    __shared__ __attribute__((aligned(16))) float s_o[4][2][D][G];       // per wave: hi/lo rows
-    __shared__ __attribute__((aligned(16))) float s_xo[D][G];            // the new token
-    __shared__ float s_m[5][G], s_l[5][G];                                // [4]: the new token
+    __shared__ __attribute__((aligned(16))) float s_o[4][2][D][G];    // per wave: hi/lo rows
+    __shared__ __attribute__((aligned(16))) float s_xo[D][G];         // the new token
+    __shared__ float s_m[5][G], s_l[5][G];                             // [4]: the new token
 
-    const size_t page_elems = (size_t)P * D;
-    const S *kpool = (const S *)a.kpool;
-    const S *vpool = (const S *)a.vpool;
-    const int half = a.rope_half, rdim = a.rope_dim;
+    // ---- 0. the arguments: one batch of scalar loads and one wait ---------
+    // Every argument passes through one empty asm as an output.  The compiler
+    // must then issue all their loads (page ids from the argument list
+    // included: without RUNS a split's pages are PPW consecutive blocks from
+    // split * PPW, an address that hangs on blockIdx alone) before the asm
+    // and cannot move work on any of them above it, nor load one again later;
+    // left to itself it waits on some of them before issuing the rest, and
+    // every such scalar round trip delays the K/V stream.
+    const S *kpool = (const S *)a.kpool, *vpool = (const S *)a.vpool;
+    const float *q_in = a.q, *k_in = a.knew, *v_in = a.vnew, *qnw = a.qnw, *knw = a.knw;
+    const float *rcos = a.rope_cos, *rsin = a.rope_sin;
+    const int32_t *tab = a.tab;
+    float *out_p = a.out, *pml_p = a.part_ml, *pacc_p = a.part_acc;
+    int L = a.L, Hkv = a.kv_heads, ppw = RUNS ? a.ppw : PPW, nsplit = a.nsplit;
+    int half = a.rope_half, rdim = a.rope_dim, norm_q = a.norm_q, norm_k = a.norm_k;
+    float eps = a.eps, qscale = a.qscale;
+    // page ids of the split's first PPW pages from the argument list; past
+    // its end the index is clamped (the host pads the list with a mapped page)
+    int pid[4] = {0, 0, 0, 0};
+    if constexpr (PAGES_ARG) {
+#pragma unroll
+        for (int p = 0; p < PPW; p++) pid[p] = a.pages[min(split * PPW + p, kArgPages - 1)];
+    }
+    // Pointers that vector loads use are inputs only: an asm output would be
+    // a pointer of unknown address space, read by flat loads.  The stores at
+    // the end go through global-address-space copies of their pointers.
+    asm volatile(""
+                 : "+s"(out_p), "+s"(pml_p), "+s"(pacc_p), "+s"(L), "+s"(Hkv), "+s"(ppw), "+s"(nsplit), "+s"(half),
+                   "+s"(rdim), "+s"(norm_q), "+s"(norm_k), "+s"(eps), "+s"(qscale), "+s"(pid[0]), "+s"(pid[1]),
+                   "+s"(pid[2]), "+s"(pid[3])
+                 : "s"(kpool), "s"(vpool), "s"(q_in), "s"(k_in), "s"(v_in), "s"(qnw), "s"(knw), "s"(rcos), "s"(rsin),
+                   "s"(tab));
+    using gfloat = __attribute__((address_space(1))) float;
+    gfloat *out_g = (gfloat *)out_p, *pml_g = (gfloat *)pml_p, *pacc_g = (gfloat *)pacc_p;
 
-    // ---- 1. page ids: the K/V addresses hang on them -----------------------
-    // Loads are never skipped by a branch: after a conditional block of loads
-    // the wait counts must cover the path without them, which makes every
-    // later wait drain the K/V stream.  Look-ahead pages past the split clamp
-    // to its last page (a re-read from L2); with no cached page (pos = 0) the
-    // page of pos is read and ignored.
-    auto page_id = [&](int p) { return PAGES_ARG ? a.pages[p] : a.tab[p]; };
+    const int newpos = L - 1;                // cached positions [0, newpos)
+    const int ncp = (newpos + P - 1) / P;    // cached pages
+    const int page0 = split * ppw;
+    const int page_end = min(page0 + ppw, ncp);
     const int plast = max(page_end - 1, page0);
-    const int phys0 = page_id(page0);
-    const int phys1 = MULTI ? page_id(min(page0 + 1, plast)) : 0;
+    const bool last = split == nsplit - 1;
+    const size_t page_elems = (size_t)P * D;
+    // a page of the device table (wave-uniform), clamped to the split
+    auto tab_page = [&](int p) { return __builtin_amdgcn_readfirstlane(tab[min(p, plast)]); };
+    auto page_base = [&](int phys) { return ((size_t)phys * Hkv + kvh) * page_elems; };
 
-    // ---- 2. q rows and the new k, v rows ------------------------------------
-    // vmcnt retires in order: these small rows are issued ahead of the K/V
-    // stream so the q operand is built while it is in flight.  Wave w loads
-    // q head w of the group; every wave loads the new rows (1.5 KiB, cached)
-    // so that all loads sit in one straight-line block.
-    RowsIn<1, FULL> qin;
-    RowsIn<1, FULL> kin;
-    qin.load(a.q + (size_t)(kvh * G + wave) * D, a.rope_cos, a.rope_sin, a.qnw, lane, half, rdim);
-    kin.load(a.knew + (size_t)kvh * D, a.rope_cos, a.rope_sin, a.knw, lane, half, rdim);
-    const float vnew0 = a.vnew[(size_t)kvh * D + lane];
-    const float vnew1 = a.vnew[(size_t)kvh * D + lane + 64];
+    // ---- 1. every vector load, straight-line: the q row of head kvh*4 +
+    // wave, the new k and v rows, then the K/V of the split's first PPW
+    // pages.  vmcnt retires in order, so the small rows come first: the q
+    // operand is built while the stream is in flight.  Pages past the split
+    // are read and masked out (with no cached page, pos = 0, the page of pos
+    // is read and ignored).
+    RowsIn<1, FULL> qin, kin;
+    qin.load(q_in + (size_t)(kvh * G + wave) * D, rcos, rsin, qnw, lane, half, rdim);
+    kin.load(k_in + (size_t)kvh * D, rcos, rsin, knw, lane, half, rdim);
+    const float vnew0 = v_in[(size_t)kvh * D + lane];
+    const float vnew1 = v_in[(size_t)kvh * D + lane + 64];
+    // the new token's page, whose index hangs on L: from the device table
+    // in the same round trip as the split's page ids, from the argument
+    // list while the stream is in flight
+    int phys_new = 0;
+    if constexpr (!PAGES_ARG) phys_new = __builtin_amdgcn_readfirstlane(tab[newpos / P]);
+    PageOps<S> pg[PPW];
+#pragma unroll
+    for (int p = 0; p < PPW; p++)
+        pg[p].load(kpool, vpool, page_base(PAGES_ARG ? pid[p] : tab_page(page0 + p)), wave, grp, c);
+    if constexpr (PAGES_ARG) {
+        phys_new = a.pages[newpos / P];
+        asm volatile("" : "+s"(phys_new));
+    }
 
-    // ---- 3. the K/V stream --------------------------------------------------
-    // f16/bf16 pages: wave w takes the 16 positions of V chunks 2w and 2w+1,
-    // so that its V loads are whole 16-byte chunks; S row / P.V index
-    // 4 grp + i of the wave is page position posw(i) below.
-    // K A-operand: lane (grp, c) = K row c (position posw of index c), dims
-    //   32*ks + 8*grp + [0, 8): two 128-byte segments per 16 lanes.
-    // V B-operand: lane (grp, c) = V^T row 16*db + c, indices 4*grp + [0, 4):
-    //   half (grp & 1) of V chunk (2 w + (grp >> 1), 16 db + c).
-    // Whole sub-tiles are loaded (pages are fully allocated); rows at or past
-    // pos are masked out of the scores and zeroed in V before use.
-    //   f32 pages (row-major K, V^T sub-tiles): the same operands as fp32,
-    //   two 16-byte K loads per ks and one 16-byte V load per db.
-    constexpr int KL = W4 ? 8 : 4;
-    using VL = typename std::conditional<W4, uint4, uint2>::type;
-    uint4 ka[KL], kn[KL];
-    VL vb[8], vn[8];
-    auto load_sub = [&](int phys, uint4 *kk, VL *vv) {
-        const size_t pb = ((size_t)phys * Hkv + kvh) * page_elems;
-        if constexpr (W4) {
-            const S *kp = kpool + pb + (size_t)(SUB * wave + c) * D + 8 * grp;
-            const S *vp = vpool + pb + (size_t)(wave * D + c) * SUB + 4 * grp;
+    // ---- 2. q operand: wave w applies RoPE + norm to head w and stores its
+    // hi/lo split in LDS; one barrier shares the 4 heads ---------------------
+    float qy[2];
+    qin.finish(0, qy, lane, half, rdim, norm_q != 0, eps, qscale);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                kk[2 * ks] = *(const uint4 *)(kp + 32 * ks);
-                kk[2 * ks + 1] = *(const uint4 *)(kp + 32 * ks + 4);
-            }
-#pragma unroll
-            for (int db = 0; db < 8; db++) vv[db] = *(const VL *)(vp + 256 * db);
-        } else {
-            const S *kp = kpool + pb + 2048 * (2 * (wave >> 1) + ((c >> 2) & 1)) + 128 * grp +
-                          8 * (8 * (wave & 1) + 4 * (c >> 3) + (c & 3));
-            const S *vp = vpool + pb + (size_t)(2 * wave + (grp >> 1)) * 1024 + 8 * c + 4 * (grp & 1);
-#pragma unroll
-            for (int ks = 0; ks < 4; ks++) kk[ks] = *(const uint4 *)(kp + 512 * ks);
-#pragma unroll
-            for (int db = 0; db < 8; db++) vv[db] = *(const VL *)(vp + 128 * db);
-        }
-    };
-    load_sub(phys0, ka, vb);
-    if (MULTI) load_sub(phys1, kn, vn);  // two pages in flight
+    for (int e = 0; e < 2; e++) {
+        const uint32_t pr = split_pair<Op>(qy[e]);
+        s_qop[0][wave][lane + 64 * e] = (uint16_t)pr;
+        s_qop[1][wave][lane + 64 * e] = (uint16_t)(pr >> 16);
+    }
 
-    // ---- 4. q operand: wave w applies RoPE + norm to head w and stores its
-    // hi/lo split (and the fp32 row) in LDS; one barrier shares the 4 heads --
-    {
-        float y[2];
-        qin.finish(0, y, lane, half, rdim, a.qnw != nullptr, a.eps, a.qscale);
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const uint32_t pr = split_pair<Op>(y[e]);
-            s_qop[0][wave][lane + 64 * e] = (uint16_t)pr;
-            s_qop[1][wave][lane + 64 * e] = (uint16_t)(pr >> 16);
-            s_qf[wave][lane + 64 * e] = y[e];
+    // ---- 3. the new token (last split): K after RoPE + norm and V, rounded
+    // to the cache type (Ops.ConvertToBf16, Ops.cs:658-680), then head w's
+    // weight for it in the softmax's base-2 units: m = max(s, floor),
+    // l = exp2(max(s - m, floor)).  Its cache stores are issued at the end:
+    // vmcnt retires in order, so stores issued here would hold up every
+    // later wait on the K/V stream.
+    S knew_st[2] = {}, vnew_st[2] = {};
+    if (last) {
+        float ky[2];
+        kin.finish(0, ky, lane, half, rdim, norm_k != 0, eps, 1.0f);
+        knew_st[0] = to_elem<T>(ky[0]);
+        knew_st[1] = to_elem<T>(ky[1]);
+        vnew_st[0] = to_elem<T>(vnew0);
+        vnew_st[1] = to_elem<T>(vnew1);
+        const float k0 = from_elem<T>(knew_st[0]), k1 = from_elem<T>(knew_st[1]);
+        const float sc = wave_sum64(qy[0] * k0 + qy[1] * k1);
+        const float m = fmaxf(sc, kFloor2);
+        const float l = exp2f(fmaxf(sc - m, kFloor2));
+        s_xo[lane][wave] = l * from_elem<T>(vnew_st[0]);
+        s_xo[lane + 64][wave] = l * from_elem<T>(vnew_st[1]);
+        if (lane == 0) {
+            s_m[4][wave] = m;
+            s_l[4][wave] = l;
         }
     }
     __syncthreads();
@@ -339,134 +401,109 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
     for (int ks = 0; ks < 4; ks++)
         qb[ks] = c < 8 ? *(const uint4 *)&s_qop[c >> 2][c & 3][32 * ks + 8 * grp] : make_uint4(0, 0, 0, 0);
 
-    // ---- 5. the new token: K after RoPE + norm and V, rounded to the cache
-    // type (Ops.ConvertToBf16, Ops.cs:658-680), then its weight for each head
-    // in the softmax's base-2 units: m = max(s, floor), l = exp2(max(s-m, floor)).
-    // Its cache stores are issued at the end: vmcnt retires in order, so
-    // stores issued here would hold up every later wait on the K/V stream.
-    S knew_st[2] = {}, vnew_st[2] = {};
-    if (extra) {
-        float ky[2];
-        kin.finish(0, ky, lane, half, rdim, a.knw != nullptr, a.eps, 1.0f);
-        knew_st[0] = to_elem<T>(ky[0]);
-        knew_st[1] = to_elem<T>(ky[1]);
-        vnew_st[0] = to_elem<T>(vnew0);
-        vnew_st[1] = to_elem<T>(vnew1);
-        const float k0 = from_elem<T>(knew_st[0]), k1 = from_elem<T>(knew_st[1]);
-        const float v0 = from_elem<T>(vnew_st[0]), v1 = from_elem<T>(vnew_st[1]);
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            const float sc = wave_sum64(s_qf[g][lane] * k0 + s_qf[g][lane + 64] * k1);
-            const float m = fmaxf(sc, kFloor2);
-            const float l = exp2f(fmaxf(sc - m, kFloor2));
-            s_xo[lane][g] = l * v0;
-            s_xo[lane + 64][g] = l * v1;
-            if (lane == 0) {
-                s_m[4][g] = m;
-                s_l[4][g] = l;
-            }
-        }
-    }
-
-    // ---- 6. attention over the split's cached sub-tiles ---------------------
+    // ---- 4. attention over the split's cached pages, PPW at a time ---------
     // page position of S row / P.V index 4 grp + i of this wave, and the
-    // smallest one (f32 pages: the sub-tile [16 w, 16 w + 16))
+    // smallest one
     auto posw = [&](int i) {
         return W4 ? SUB * wave + 4 * grp + i
                   : 32 * (wave >> 1) + 8 * (wave & 1) + 4 * (grp >> 1) + 16 * (grp & 1) + i;
     };
-    const int pmin = W4 ? SUB * wave : 32 * (wave >> 1) + 8 * (wave & 1);
     f32x4 acc[8];
 #pragma unroll
     for (int db = 0; db < 8; db++) acc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = kFloor2, l_run = 0.0f;  // lanes c < 4: head c
 
-    for (int page = page0; page < page_end; page++) {
-        const int nv = newpos - page * P;  // positions of this page below pos
-        if (nv > pmin) {
-            // scores: lane (grp, c<4) <- head c, positions 4*grp + i
+    for (int run0 = page0; run0 < page_end; run0 += PPW) {
+        // scores of the run's pages (positions at or past pos masked out)
+        float sc[PPW][4], mt = kFloor2;
+#pragma unroll
+        for (int p = 0; p < PPW; p++) {
+            const int nv = newpos - (run0 + p) * P;  // positions of page p below pos
             f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 if constexpr (W4) {
                     uint4 hi, lo;
-                    split8(ka[2 * ks], ka[2 * ks + 1], hi, lo);
+                    split8(pg[p].k[2 * ks], pg[p].k[2 * ks + 1], hi, lo);
                     sacc = M::qk(hi, qb[ks], sacc);
                     sacc = M::qk(lo, qb[ks], sacc);
                 } else {
-                    sacc = M::qk(ka[ks], qb[ks], sacc);
+                    sacc = M::qk(pg[p].k[ks], qb[ks], sacc);
                 }
             }
-            float sc[4], mt = kFloor2;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                sc[i] = sacc[i] + dpp_from_plus4(sacc[i]);
-                if (posw(i) < nv) mt = fmaxf(mt, sc[i]);
+                sc[p][i] = sacc[i] + dpp_from_plus4(sacc[i]);
+                if (run0 + p < page_end && posw(i) < nv) mt = fmaxf(mt, sc[p][i]);
+                else sc[p][i] = -INFINITY;
             }
-            mt = xrow32_max(xrow16_max(mt));
-            const float mnew = fmaxf(m_run, mt);
-            float p[4], ps = 0.0f;
+        }
+        mt = xrow32_max(xrow16_max(mt));
+        const float mnew = fmaxf(m_run, mt);
+        const float alpha = exp2f(m_run - mnew);
+        float pr[PPW][4], ps = 0.0f;
+#pragma unroll
+        for (int p = 0; p < PPW; p++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                p[i] = posw(i) < nv ? exp2f(fmaxf(sc[i] - mnew, kFloor2)) : 0.0f;
-                ps += p[i];
+                pr[p][i] = sc[p][i] == -INFINITY ? 0.0f : exp2f(fmaxf(sc[p][i] - mnew, kFloor2));
+                ps += pr[p][i];
             }
-            ps = xrow32_sum(xrow16_sum(ps));
+        ps = xrow32_sum(xrow16_sum(ps));
+        l_run = l_run * alpha + ps;
+        m_run = mnew;
+        if (run0 != page0) {  // rescale the running sums of earlier runs
+            float al[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) al[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), i));
+#pragma unroll
+            for (int db = 0; db < 8; db++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) acc[db][i] *= al[i];
+        }
+#pragma unroll
+        for (int p = 0; p < PPW; p++) {
             // Pcat A-operand: lane (grp, r): r<4 hi(p_r), 4<=r<8 lo(p_{r-4})
             uint32_t hp[2], lp[2];
 #pragma unroll
             for (int e = 0; e < 2; e++) {
-                const uint32_t p0 = split_pair<Op>(p[2 * e]), p1 = split_pair<Op>(p[2 * e + 1]);
+                const uint32_t p0 = split_pair<Op>(pr[p][2 * e]), p1 = split_pair<Op>(pr[p][2 * e + 1]);
                 hp[e] = (p0 & 0xFFFFu) | (p1 << 16);
                 lp[e] = dpp_from_minus4((p0 >> 16) | (p1 & 0xFFFF0000u));
             }
             const uint2 pa = c < 4 ? make_uint2(hp[0], hp[1]) : c < 8 ? make_uint2(lp[0], lp[1]) : make_uint2(0u, 0u);
-            if (MULTI) {  // rescale the running sums (a single sub-tile starts from zero)
-                const float alpha = exp2f(m_run - mnew);
-                l_run = l_run * alpha + ps;
-                float al[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) al[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), i));  // head i
-#pragma unroll
-                for (int db = 0; db < 8; db++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) acc[db][i] *= al[i];
-            } else {
-                l_run = ps;
-            }
-            m_run = mnew;
             // V: zero the positions at or past pos (halfword masks of this
             // lane's 4 positions); they may hold stale data
+            const int nv = newpos - (run0 + p) * P;
             uint32_t keep[2] = {0xFFFFFFFFu, 0xFFFFFFFFu};
             if (nv < P) {
 #pragma unroll
                 for (int j = 0; j < 4; j++)
                     if (posw(j) >= nv) keep[j >> 1] &= ~(0xFFFFu << (16 * (j & 1)));
             }
+            if (run0 + p >= page_end) keep[0] = keep[1] = 0u;
             if constexpr (W4) {
 #pragma unroll
                 for (int db = 0; db < 8; db++) {
                     uint2 hi, lo;
-                    split4(vb[db], keep, hi, lo);
+                    split4(pg[p].v[db], keep, hi, lo);
                     acc[db] = M::pv(pa, hi, acc[db]);
                     acc[db] = M::pv(pa, lo, acc[db]);
                 }
             } else {
 #pragma unroll
                 for (int db = 0; db < 8; db++)
-                    acc[db] = M::pv(pa, make_uint2(vb[db].x & keep[0], vb[db].y & keep[1]), acc[db]);
+                    acc[db] = M::pv(pa, make_uint2(pg[p].v[db].x & keep[0], pg[p].v[db].y & keep[1]), acc[db]);
             }
         }
-        if (MULTI) {
+        // the next run's pages (splits of more than PPW pages)
+        if (RUNS && run0 + PPW < page_end) {
 #pragma unroll
-            for (int ks = 0; ks < KL; ks++) ka[ks] = kn[ks];
-#pragma unroll
-            for (int db = 0; db < 8; db++) vb[db] = vn[db];
-            load_sub(page_id(min(page + 2, plast)), kn, vn);
+            for (int p = 0; p < PPW; p++) pg[p].load(kpool, vpool, page_base(tab_page(run0 + PPW + p)), wave, grp, c);
         }
     }
 
-    // ---- 7. combine the wave partials (and the new token) ------------------
+    // ---- 5. combine the wave partials (and the new token) ------------------
     // rows 0-3 (grp 0, hi) and 4-7 (grp 1, lo) of every dim go to LDS as
     // 16-byte vectors [wave][part][dim][head]; (m, l) of head c from lane c.
     if (grp < 2) {
@@ -509,19 +546,23 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const int h = kvh * G + gp + j;
-            if (a.nsplit == 1) {
-                a.out[(size_t)h * D + d] = Lx[j] > 0.0f ? O[j] / Lx[j] : 0.0f;
+            if (nsplit == 1) {
+                out_g[(size_t)h * D + d] = Lx[j] > 0.0f ? O[j] / Lx[j] : 0.0f;
             } else {
-                a.part_acc[((size_t)h * kMaxSplits + split) * D + d] = O[j];
-                if (d == 0) *(float2 *)(a.part_ml + ((size_t)h * kMaxSplits + split) * 2) = make_float2(Mx[j], Lx[j]);
+                pacc_g[((size_t)h * kMaxSplits + split) * D + d] = O[j];
+                if (d == 0) {
+                    gfloat *m = pml_g + ((size_t)h * kMaxSplits + split) * 2;
+                    m[0] = Mx[j];
+                    m[1] = Lx[j];
+                }
             }
         }
     }
-    // ---- 8. append the new row to the cache ---------------------------------
-    if (extra) {
-        const int phys = page_id(newpos / P), t = newpos % P;
-        S *kp = (S *)kpool + ((size_t)phys * Hkv + kvh) * page_elems;
-        S *vp = (S *)vpool + ((size_t)phys * Hkv + kvh) * page_elems;
+    // ---- 6. append the new row to the cache ---------------------------------
+    if (last && wave == 0) {
+        const int t = newpos % P;
+        S *kp = (S *)kpool + ((size_t)phys_new * Hkv + kvh) * page_elems;
+        S *vp = (S *)vpool + ((size_t)phys_new * Hkv + kvh) * page_elems;
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             kp[k_off<sizeof(S)>(t, lane + 64 * e)] = knew_st[e];
@@ -532,34 +573,51 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 
 // Merge of the split partials (the second launch of a multi-split call):
 // out[h] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
-// Workgroup = q head; thread = (split group sg of 8, 4 dims).  Every thread
+// Workgroup = q head, NG x 32 threads; thread = (split group sg of NG, 4
+// dims) over splits sg + NG k, k < PER (NG * PER >= nsplit).  Every thread
 // issues all its loads (float2 (m, l) and float4 acc per split) at once; the
-// 8 split groups are combined through LDS.
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
-    constexpr int D = kHeadDim, NG = 8, PER = kMaxSplits / NG;
+// NG split groups are combined through LDS.
+struct MergeArgs {
+    const float *part_ml;
+    const float *part_acc;
+    float *out;
+    int nsplit;
+};
+template <int NG, int PER>
+__global__ __launch_bounds__(NG * 32) void decode_merge_kernel(MergeArgs a) {
+    constexpr int D = kHeadDim;
+    static_assert(NG * PER <= kMaxSplits, "slots past the workspace");
     const int h = blockIdx.x, d4 = threadIdx.x & 31, sg = threadIdx.x >> 5;
     __shared__ float s_m[NG], s_l[NG];
     __shared__ float4 s_o[NG][32];
     const float2 *ml = (const float2 *)(a.part_ml + (size_t)h * kMaxSplits * 2);
     const float4 *pa = (const float4 *)(a.part_acc + (size_t)h * kMaxSplits * D) + d4;
+    // Every slot is loaded (the workspace holds kMaxSplits per head; slots at
+    // or past nsplit hold stale data) and then masked: a load under a
+    // condition would be followed by a wait before the next one is issued.
     float2 mlv[PER];
     float4 x[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int s = sg + NG * k;
-        const bool ok = s < a.nsplit;
-        mlv[k] = ok ? ml[s] : make_float2(-INFINITY, 0.0f);
-        x[k] = ok ? pa[(size_t)s * (D / 4)] : make_float4(0.f, 0.f, 0.f, 0.f);
+        mlv[k] = ml[s];
+        x[k] = pa[(size_t)s * (D / 4)];
     }
-    float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < PER; k++) M = fmaxf(M, mlv[k].x);
+    for (int k = 0; k < PER; k++) {
+        const bool ok = sg + NG * k < a.nsplit;
+        mlv[k] = ok ? mlv[k] : make_float2(-INFINITY, 0.0f);
+        x[k] = ok ? x[k] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float Mv = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < PER; k++) Mv = fmaxf(Mv, mlv[k].x);
     float L = 0.0f;
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (M != -INFINITY) {
+    if (Mv != -INFINITY) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
-            const float w = exp2f(mlv[k].x - M);
+            const float w = exp2f(mlv[k].x - Mv);
             L = fmaf(w, mlv[k].y, L);
             O.x = fmaf(w, x[k].x, O.x);
             O.y = fmaf(w, x[k].y, O.y);
@@ -568,7 +626,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
         }
     }
     if (d4 == 0) {
-        s_m[sg] = M;
+        s_m[sg] = Mv;
         s_l[sg] = L;
     }
     s_o[sg][d4] = O;
@@ -639,38 +697,62 @@ hipError_t decode_scratch(int device, float **part_ml, float **part_acc, int *ma
 
 using DecodeKernel = void (*)(DecodeArgs);
 
-template <typename T> DecodeKernel pick_mfma(bool multi, bool args, bool full) {
-    const int i = multi * 4 + args * 2 + full;
-    static const DecodeKernel k[8] = {
-        decode_attn_mfma_kernel<T, false, false, false>, decode_attn_mfma_kernel<T, false, false, true>,
-        decode_attn_mfma_kernel<T, false, true, false>,  decode_attn_mfma_kernel<T, false, true, true>,
-        decode_attn_mfma_kernel<T, true, false, false>,  decode_attn_mfma_kernel<T, true, false, true>,
-        decode_attn_mfma_kernel<T, true, true, false>,   decode_attn_mfma_kernel<T, true, true, true>};
-    return k[i];
+template <typename T, int PPW, bool RUNS, bool ARGS> DecodeKernel pick_full(bool full) {
+    return full ? decode_attn_mfma_kernel<T, PPW, RUNS, ARGS, true> : decode_attn_mfma_kernel<T, PPW, RUNS, ARGS, false>;
+}
+// Instances that launch_decode can reach: page lists in the arguments hold at
+// most kArgPages pages, taken one or two per split.
+template <typename T> DecodeKernel pick_mfma(int ppw, bool args, bool full) {
+    if (args) return ppw == 1 ? pick_full<T, 1, false, true>(full) : pick_full<T, 2, false, true>(full);
+    switch (ppw) {
+    case 1: return pick_full<T, 1, false, false>(full);
+    case 2: return pick_full<T, 2, false, false>(full);
+    case 3: return pick_full<T, 3, false, false>(full);
+    case 4: return pick_full<T, 4, false, false>(full);
+    default: return pick_full<T, 4, true, false>(full);
+    }
+}
+
+// Pages per split for `pages` cached pages (at most kMaxSplits splits).
+// Measured at 1k-32k positions: a page per split while there are at most 128
+// (4k positions: 64 workgroups per kv head), then two (fewer partials for
+// the merge to read: 13.7 against 16.1 us per call at 16k).
+int decode_pages_per_split(int pages) {
+    return pages <= 128 ? 1 : pages <= 2 * kMaxSplits ? 2 : (pages + kMaxSplits - 1) / kMaxSplits;
 }
 
 hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     DecodeArgs a = args;
     // Work split: pages of the cached positions [0, L-1), the new token riding
     // with the last split.  One page per split until the split count reaches
-    // kMaxSplits (the merge width).
+    // kMaxSplits (the merge width, so up to 32768 positions take at most two
+    // pages per split); a split's pages are loaded PPW (<= 4) at a time, all
+    // issued at once.
     const int pages = (a.L - 1 + kPage - 1) / kPage;
-    a.ppw = std::max(1, (pages + kMaxSplits - 1) / kMaxSplits);
+    a.ppw = decode_pages_per_split(pages);
     a.nsplit = std::max(1, (pages + a.ppw - 1) / a.ppw);
     dim3 grid(a.nsplit, a.kv_heads), block(256);
-    const bool multi = a.ppw > 1, in_args = a.pages_in_args != 0;
+    const bool in_args = a.pages_in_args != 0;
+    if (in_args && a.ppw > 2) return hipErrorInvalidValue;
     const bool full = a.rope_dim == kHeadDim;
     DecodeKernel k;
     switch (kv_dtype) {
-    case 0: k = pick_mfma<F32>(multi, in_args, full); break;
-    case 1: k = pick_mfma<F16>(multi, in_args, full); break;
-    case 2: k = pick_mfma<BF16>(multi, in_args, full); break;
+    case 0: k = pick_mfma<F32>(a.ppw, in_args, full); break;
+    case 1: k = pick_mfma<F16>(a.ppw, in_args, full); break;
+    case 2: k = pick_mfma<BF16>(a.ppw, in_args, full); break;
     default: return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(k, grid, block, 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
-    hipLaunchKernelGGL(decode_merge_kernel, dim3(a.kv_heads * kGroup), dim3(256), 0, s, a);
+    const MergeArgs m{a.part_ml, a.part_acc, a.out, a.nsplit};
+    const dim3 heads(a.kv_heads * kGroup);
+    if (a.nsplit <= 64)
+        hipLaunchKernelGGL((decode_merge_kernel<8, 8>), heads, dim3(256), 0, s, m);
+    else if (a.nsplit <= 128)
+        hipLaunchKernelGGL((decode_merge_kernel<8, 16>), heads, dim3(256), 0, s, m);
+    else
+        hipLaunchKernelGGL((decode_merge_kernel<16, 16>), heads, dim3(512), 0, s, m);
     return hipGetLastError();
 }
 

@@ -108,6 +108,9 @@ struct hymt_ctx {
     // RoPE table rows [0, rope_cap)
     int rope_cap = 0;
     DevBuf rope_cos, rope_sin;
+    // 128 ones: the gamma of an absent QK norm and the table row of rope_dim
+    // 0, so that the decode kernel's loads never depend on a branch
+    DevBuf ones;
 
     // decode workspace: split partials (m, l) and acc
     DevBuf dec_ml, dec_acc;
@@ -129,7 +132,7 @@ struct hymt_ctx {
     uint64_t gen = 0;
 
     hymt_ctx() {
-        for (DevBuf *b : {&kpool, &vpool, &tab, &rope_cos, &rope_sin, &dec_ml, &dec_acc, &part_o, &part_ml, &in_q,
+        for (DevBuf *b : {&kpool, &vpool, &tab, &rope_cos, &rope_sin, &ones, &dec_ml, &dec_acc, &part_o, &part_ml, &in_q,
                           &in_k, &in_v, &in_qnw, &in_knw, &out_o, &up_k, &up_v, &rows_idx})
             b->gen = &gen;
     }
@@ -325,7 +328,7 @@ int hymt_destroy(hymt_ctx *c) {
             c->capturing = false;
         }
         (void)hipStreamSynchronize(c->stream);
-        for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->dec_ml,
+        for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->ones, &c->dec_ml,
                           &c->dec_acc, &c->part_o, &c->part_ml, &c->in_q,
                           &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v, &c->rows_idx})
             b->release();
@@ -381,6 +384,9 @@ int hymt_kv_create(hymt_ctx *c, int layers, int max_tokens, int kv_dtype) {
             c->dec_ml.reserve((size_t)c->heads * kMaxSplits * 2 * 4);
             c->dec_acc.reserve((size_t)c->heads * kMaxSplits * kHeadDim * 4);
             ensure_rope(c, c->pages.max_tokens());
+            const std::vector<float> ones(kHeadDim, 1.0f);
+            c->ones.reserve(kHeadDim * 4);
+            HIP_TRY(hipMemcpy(c->ones.p, ones.data(), kHeadDim * 4, hipMemcpyHostToDevice));
         } catch (const HipError &e) {
             c->kpool.release();
             c->vpool.release();
@@ -548,14 +554,17 @@ static int decode_impl(hymt_ctx *c, int layer, int pos, const float *q, const fl
             c->out_o.reserve(qn * 4);
         }
         DecodeArgs a;
+        const float *ones = (const float *)c->ones.p;
         a.q = dev ? q : (const float *)c->in_q.p;
         a.knew = dev ? k : (const float *)c->in_k.p;
         a.vnew = dev ? v : (const float *)c->in_v.p;
-        a.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
-        a.knw = !knw ? nullptr : dev ? knw : (const float *)c->in_knw.p;
+        a.qnw = !qnw ? ones : dev ? qnw : (const float *)c->in_qnw.p;
+        a.knw = !knw ? ones : dev ? knw : (const float *)c->in_knw.p;
+        a.norm_q = qnw != nullptr;
+        a.norm_k = knw != nullptr;
         const int half = c->rope_dim / 2;
-        a.rope_cos = (const float *)c->rope_cos.p + (size_t)pos * half;
-        a.rope_sin = (const float *)c->rope_sin.p + (size_t)pos * half;
+        a.rope_cos = half ? (const float *)c->rope_cos.p + (size_t)pos * half : ones;
+        a.rope_sin = half ? (const float *)c->rope_sin.p + (size_t)pos * half : ones;
         a.tab = (const int32_t *)c->tab.p;
         a.kpool = c->klayer(layer);
         a.vpool = c->vlayer(layer);
@@ -564,7 +573,6 @@ static int decode_impl(hymt_ctx *c, int layer, int pos, const float *q, const fl
         a.out = dev ? out : (float *)c->out_o.p;
         a.L = pos + 1;
         a.kv_heads = c->kv_heads;
-        a.kv_shift = __builtin_ctz((unsigned)c->kv_heads);
         a.rope_half = half;
         a.rope_dim = c->rope_dim;
         const int npages = (a.L + kPage - 1) / kPage;
@@ -572,8 +580,12 @@ static int decode_impl(hymt_ctx *c, int layer, int pos, const float *q, const fl
         a.eps = c->eps;
         a.qscale = 1.4426950408889634f / sqrtf((float)D);
         a.pages_in_args = npages <= kArgPages;
-        if (a.pages_in_args)
+        if (a.pages_in_args) {
+            // padded with the last page: the kernel clamps look-ahead page
+            // indices to the list's end, not to L
             for (int b = 0; b < npages; b++) a.pages[b] = c->pages.phys(b);
+            for (int b = npages; b < kArgPages; b++) a.pages[b] = a.pages[npages - 1];
+        }
         HIP_TRY(launch_decode(c->kv_dtype, a, c->stream));
         if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
     } catch (const HipError &e) {

@@ -170,7 +170,7 @@ int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const fl
  * It has no counterpart in the reference.  Device pointers only (as
  * HYMT_FLAG_DEVICE_PTRS), same arguments and result as hymt_attn_decode, and
  * it never calls hipMalloc or hipFree: the split partials live in a static
- * device array of the library (2.03 MiB per GPU, held until the process
+ * device array of the library (4.06 MiB per GPU, held until the process
  * ends; room for 32 q heads, a larger head count is HYMT_E_UNSUPPORTED), and
  * the RoPE table is built for the whole cache by hymt_kv_create.  All
  * contexts on one GPU share that array: calls that overlap on one GPU (two
