@@ -89,7 +89,7 @@ struct DecodeArgs {
 struct PrepArgs {
     const void *k;      // [seq][Hkv*D]   fp32 or bf16 (io_bf16)
     const void *v;
-    const float *knw;   // [D] or null
+    const float *knw;   // [D] gamma of k (a ones vector when the norm is off)
     const float *rope_cos; // table base [cap][rope_half]
     const float *rope_sin;
     const int32_t *tab;
@@ -98,13 +98,14 @@ struct PrepArgs {
     int kv_heads;
     int rope_half, rope_dim;
     int io_bf16;
+    int norm_k;         // apply the k RMSNorm
     float eps;
     int kv_ld;          // elements from one k (and v) row to the next, >= Hkv*D
 };
 
 struct FlashArgs {
     const void *q;      // [seq][Hq*D]    fp32 or bf16 (io_bf16), before RoPE/norm
-    const float *qnw;   // [D] or null
+    const float *qnw;   // [D] gamma of q (a ones vector when the norm is off)
     const float *rope_cos, *rope_sin;  // table base [cap][rope_half]
     const int32_t *tab;
     const void *kpool, *vpool;
@@ -115,6 +116,7 @@ struct FlashArgs {
     int heads, kv_heads;
     int rope_half, rope_dim;  // rope_dim in {0, 64, 128}
     int io_bf16;
+    int norm_q;         // apply the q RMSNorm
     float eps, qscale;  // qscale = log2(e) / sqrt(D)
     int nb16;           // q blocks of 16 rows
     int npairs;         // block pairs (b, nb16-1-b), b < npairs

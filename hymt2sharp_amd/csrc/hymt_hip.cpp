@@ -654,7 +654,8 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         PrepArgs p;
         p.k = dev ? k : c->in_k.p;
         p.v = dev ? v : c->in_v.p;
-        p.knw = !knw ? nullptr : dev ? knw : (const float *)c->in_knw.p;
+        p.knw = !knw ? (const float *)c->ones.p : dev ? knw : (const float *)c->in_knw.p;
+        p.norm_k = knw != nullptr;
         p.rope_cos = (const float *)c->rope_cos.p;
         p.rope_sin = (const float *)c->rope_sin.p;
         p.tab = (const int32_t *)c->tab.p;
@@ -672,7 +673,8 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
 
         FlashArgs f;
         f.q = dev ? q : c->in_q.p;
-        f.qnw = !qnw ? nullptr : dev ? qnw : (const float *)c->in_qnw.p;
+        f.qnw = !qnw ? (const float *)c->ones.p : dev ? qnw : (const float *)c->in_qnw.p;
+        f.norm_q = qnw != nullptr;
         f.rope_cos = (const float *)c->rope_cos.p;
         f.rope_sin = (const float *)c->rope_sin.p;
         f.tab = (const int32_t *)c->tab.p;

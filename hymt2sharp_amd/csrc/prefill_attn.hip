@@ -88,13 +88,26 @@ __device__ __forceinline__ void load8_in(const void *base, size_t i, bool bf16, 
 
 // ------------------------------------------------------------------ k/v
 // Block (16-position block, kv head); thread (row = tid/16, dims 8*(tid%16)..).
-// Every global load (k, v, the row's cos/sin, gamma) is issued before any
-// math.  The RoPE partner of dim d (d +- rope_dim/2) lives in lane
-// c ^ (rope_dim/16) of the same 16-lane row and is fetched by a lane shuffle;
-// the norm's sum of squares is a DPP reduction over the row.  K is written as
-// one 16-byte store per thread; V is transposed through LDS into the page's
-// 16-position V^T sub-tile.
-template <typename T>
+// Straight-line loads, no branch between them (a load under a branch is
+// followed by a wait before the next one): the row's page id first (only
+// the stores need it), then k, v, the row's cos/sin and gamma (the host
+// passes a ones vector when the norm is off).  The RoPE partner of dim d
+// (d +- rope_dim/2) lives in lane c ^ (rope_dim/16) of the same 16-lane row
+// and is fetched by DPP; the norm's sum of squares is a DPP reduction over
+// the row.  K is written as one 16-byte store per thread; V is transposed
+// through LDS into the page's V^T chunks.
+// IN_BF16: k/v rows are bf16 (else fp32); HK = rope_dim / 64 in {0, 1, 2}.
+template <int HK> __device__ __forceinline__ float rope_partner_dpp(float x, int c) {
+    if constexpr (HK == 2) {  // c ^ 8: rotate the 16-lane row by 8
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+    } else {  // c ^ 4: from c + 4 (row_shl:4) or from c - 4 (row_shr:4)
+        const float up = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x104, 0xF, 0xF, false));
+        const float dn = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xF, 0xF, false));
+        return (c & 4) ? dn : up;
+    }
+}
+
+template <typename T, bool IN_BF16, int HK>
 __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     constexpr int D = kHeadDim, P = kPage;
     using S = typename T::storage;
@@ -106,23 +119,38 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     const int m = pstart + r - a.pos0;                    // row within the chunk
     const bool valid = m >= 0 && m < a.seq;
     const int mc = m < 0 ? 0 : (m < a.seq ? m : a.seq - 1);  // clamped for loads
-    const int phys = a.tab[pstart / P];
-    const size_t page_base = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
+    const int phys = __builtin_amdgcn_readfirstlane(a.tab[pstart / P]);
     const int d0 = 8 * c, rh = a.rope_half;
     const size_t src = (size_t)mc * a.kv_ld + (size_t)kvh * D + d0;
 
     float x[8], v[8], cs[8], sn[8], gw[8];
-    load8_in(a.k, src, a.io_bf16, x);
-    load8_in(a.v, src, a.io_bf16, v);
-    const bool rot = d0 < a.rope_dim;
-    if (rot) {
+    if constexpr (IN_BF16) {
+        const uint4 ku = *(const uint4 *)((const uint16_t *)a.k + src);
+        const uint4 vu = *(const uint4 *)((const uint16_t *)a.v + src);
+        const uint32_t kw[4] = {ku.x, ku.y, ku.z, ku.w}, vw[4] = {vu.x, vu.y, vu.z, vu.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[2 * e] = __uint_as_float(kw[e] << 16);
+            x[2 * e + 1] = __uint_as_float(kw[e] & 0xFFFF0000u);
+            v[2 * e] = __uint_as_float(vw[e] << 16);
+            v[2 * e + 1] = __uint_as_float(vw[e] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 k0 = *(const float4 *)((const float *)a.k + src), k1 = *(const float4 *)((const float *)a.k + src + 4);
+        const float4 v0 = *(const float4 *)((const float *)a.v + src), v1 = *(const float4 *)((const float *)a.v + src + 4);
+        x[0] = k0.x; x[1] = k0.y; x[2] = k0.z; x[3] = k0.w; x[4] = k1.x; x[5] = k1.y; x[6] = k1.z; x[7] = k1.w;
+        v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w; v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+    }
+    if constexpr (HK > 0) {
+        // every lane loads a table row (non-rotated dims of rope_dim 64 read
+        // the row of dim d0 % 32 and ignore it)
         const size_t rb = (size_t)(a.pos0 + mc) * rh + (d0 & (rh - 1));
         const float4 c0 = *(const float4 *)(a.rope_cos + rb), c1 = *(const float4 *)(a.rope_cos + rb + 4);
         const float4 s0 = *(const float4 *)(a.rope_sin + rb), s1 = *(const float4 *)(a.rope_sin + rb + 4);
         cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
         sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
     }
-    if (a.knw) {
+    {
         const float4 g0 = *(const float4 *)(a.knw + d0), g1 = *(const float4 *)(a.knw + d0 + 4);
         gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w; gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
     }
@@ -138,30 +166,32 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
         *(uint4 *)&s_v[r][d0] = m < a.seq ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
     }
 
-    // RoPE (Ops.RopeRange, Ops.cs:157-165) then RMSNorm of the k row
-    const int pl = rh >> 3;  // partner lane distance: 8 (rope 128) or 4 (rope 64)
-    const bool lower = (d0 & rh) == 0;
+    // RoPE (Ops.RopeRange, Ops.cs:157-165) then RMSNorm of the k row; without
+    // the norm the factor is 1 and gamma the ones vector
     float y[8], ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const float xp = pl ? __shfl_xor(x[e], pl, 16) : 0.0f;
-        y[e] = !rot ? x[e] : lower ? x[e] * cs[e] - xp * sn[e] : xp * sn[e] + x[e] * cs[e];
-        ss += y[e] * y[e];
+        float yv = x[e];
+        if constexpr (HK > 0) {
+            const float xp = rope_partner_dpp<HK>(x[e], c);
+            const bool rot = d0 < 64 * HK, lower = (d0 & rh) == 0;
+            yv = !rot ? x[e] : lower ? x[e] * cs[e] - xp * sn[e] : xp * sn[e] + x[e] * cs[e];
+        }
+        y[e] = yv;
+        ss += yv * yv;
     }
-    if (a.knw) {
-        ss = dpp_sum16(ss);
-        const float rr = 1.0f / sqrtf(ss / (float)D + a.eps);
+    ss = dpp_sum16(ss);
+    const float rr = a.norm_k ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.0f;
 #pragma unroll
-        for (int e = 0; e < 8; e++) y[e] = y[e] * rr * gw[e];
-    }
-    if (valid) {
-        uint32_t w[4];
+    for (int e = 0; e < 8; e++) y[e] = y[e] * rr * gw[e];
+    uint32_t kw[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            w[e] = (uint32_t)to_elem<T>(y[2 * e]) | ((uint32_t)to_elem<T>(y[2 * e + 1]) << 16);
-        *(uint4 *)((S *)a.kpool + page_base + k_off16(pstart % P + r, d0)) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    for (int e = 0; e < 4; e++) kw[e] = (uint32_t)to_elem<T>(y[2 * e]) | ((uint32_t)to_elem<T>(y[2 * e + 1]) << 16);
+    const size_t page_base = ((size_t)phys * Hkv + kvh) * (size_t)(P * D);
+    // the barrier precedes every global store: a store issued before it
+    // would be waited for at the barrier
     __syncthreads();
+    if (valid) *(uint4 *)((S *)a.kpool + page_base + k_off16(pstart % P + r, d0)) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
     // V: thread -> (d = tid/2, positions h8 + [0, 8) of the block, h8 = 8*(tid%2)),
     // i.e. 4 positions in each of two V chunks (8-byte stores)
     {
@@ -171,9 +201,9 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
         if (m0 >= 0) {
 #pragma unroll
             for (int q4 = 0; q4 < 2; q4++) {
-                const int r = h8 + 4 * q4;
-                const uint32_t w0 = (uint32_t)s_v[r][d] | ((uint32_t)s_v[r + 1][d] << 16);
-                const uint32_t w1 = (uint32_t)s_v[r + 2][d] | ((uint32_t)s_v[r + 3][d] << 16);
+                const int rr4 = h8 + 4 * q4;
+                const uint32_t w0 = (uint32_t)s_v[rr4][d] | ((uint32_t)s_v[rr4 + 1][d] << 16);
+                const uint32_t w1 = (uint32_t)s_v[rr4 + 2][d] | ((uint32_t)s_v[rr4 + 3][d] << 16);
                 *(uint2 *)(vpage + v_off16(t0 + 4 * q4, d)) = make_uint2(w0, w1);
             }
         } else {
@@ -184,14 +214,22 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     }
 }
 
+template <typename T, bool IN_BF16> void launch_kv(const PrepArgs &a, dim3 grid, hipStream_t s) {
+    const int hk = a.rope_half >> 5;
+    if (hk == 2) hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 2>), grid, dim3(256), 0, s, a);
+    else if (hk == 1) hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 1>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 0>), grid, dim3(256), 0, s, a);
+}
+
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
     // blocks of 16 positions from the chunk's first to the end of the page
     // holding its last position (the V rows past the chunk are zeroed)
     const int first = a.pos0 & ~15, last = ((a.pos0 + a.seq + kPage - 1) & ~(kPage - 1)) - 1;
-    dim3 grid((last - first) / 16 + 1, a.kv_heads), block(256);
+    dim3 grid((last - first) / 16 + 1, a.kv_heads);
+    if (a.rope_dim != 0 && a.rope_dim != 64 && a.rope_dim != 128) return hipErrorInvalidValue;
     switch (kv_dtype) {
-    case 1: hipLaunchKernelGGL(prefill_kv_kernel<F16>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(prefill_kv_kernel<BF16>, grid, block, 0, s, a); break;
+    case 1: a.io_bf16 ? launch_kv<F16, true>(a, grid, s) : launch_kv<F16, false>(a, grid, s); break;
+    case 2: a.io_bf16 ? launch_kv<BF16, true>(a, grid, s) : launch_kv<BF16, false>(a, grid, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -320,6 +358,7 @@ constexpr int kRopeF4 = 16;  // float4 per table row (rope_dim / 8 <= 16)
 // absent block use q = 0 (their results are discarded).
 template <bool IN_BF16> struct QRaw {
     uint4 u[2][4][IN_BF16 ? 1 : 2];
+    float4 g[4][2];  // gamma of the lane's dims 32*ks + 8*grp + [0, 8)
 };
 
 template <bool IN_BF16>
@@ -342,6 +381,11 @@ __device__ __forceinline__ void q_load(const FlashArgs &a, int h, const int (&ro
             }
         }
     }
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        raw.g[ks][0] = *(const float4 *)(a.qnw + 32 * ks + 8 * grp);
+        raw.g[ks][1] = *(const float4 *)(a.qnw + 32 * ks + 8 * grp + 4);
+    }
 }
 
 // HK = rope_dim / 64: dim chunk ks rotates with chunk ks ^ HK (HK 0: no RoPE).
@@ -351,20 +395,12 @@ __device__ __forceinline__ void q_finish(const FlashArgs &a, const QRaw<IN_BF16>
     constexpr int D = kHeadDim;
     typedef typename Mfma<T>::vec vec;
     const int rh = a.rope_half;
-    float gw[4][8];
-    if (a.qnw) {
+    float gw[4][8];  // gamma: the host passes a ones vector when the norm is off
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const float4 g0 = *(const float4 *)(a.qnw + 32 * ks + 8 * grp);
-            const float4 g1 = *(const float4 *)(a.qnw + 32 * ks + 8 * grp + 4);
-            gw[ks][0] = g0.x; gw[ks][1] = g0.y; gw[ks][2] = g0.z; gw[ks][3] = g0.w;
-            gw[ks][4] = g1.x; gw[ks][5] = g1.y; gw[ks][6] = g1.z; gw[ks][7] = g1.w;
-        }
-    } else {
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) gw[ks][e] = 1.0f;
+    for (int ks = 0; ks < 4; ks++) {
+        const float4 g0 = raw.g[ks][0], g1 = raw.g[ks][1];
+        gw[ks][0] = g0.x; gw[ks][1] = g0.y; gw[ks][2] = g0.z; gw[ks][3] = g0.w;
+        gw[ks][4] = g1.x; gw[ks][5] = g1.y; gw[ks][6] = g1.z; gw[ks][7] = g1.w;
     }
 #pragma unroll
     for (int qq = 0; qq < 2; qq++) {
@@ -422,8 +458,8 @@ __device__ __forceinline__ void q_finish(const FlashArgs &a, const QRaw<IN_BF16>
                 ss += v * v;
             }
         }
-        float rr = 1.0f;
-        if (a.qnw) rr = 1.0f / sqrtf(pf_xrow_sum(ss) / (float)D + a.eps);
+        const float sum = pf_xrow_sum(ss);
+        const float rr = a.norm_q ? 1.0f / sqrtf(sum / (float)D + a.eps) : 1.0f;
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             uint32_t w[4];
@@ -465,8 +501,20 @@ constexpr float kLazy = 8.0f;
 // the 16 of its long block B (qq = 1); tiles past A's causal range run B
 // alone.  Tile pair j sits in LDS buffer j & 1 (one slot per parity); the
 // two halves' (m, l, O) are combined through LDS at the end.
-template <typename T>
-__global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
+template <typename T, bool IN_BF16, int HK>
+__global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
+    // The arguments pass through one empty asm (scalars as outputs, pointers
+    // as inputs, which keeps their global address space): the compiler then
+    // issues every argument load in one batch with one wait, instead of
+    // waiting on the first few before it issues the rest, and cannot load
+    // one again later.
+    FlashArgs a = args;
+    asm volatile(""
+                 : "+s"(a.pos0), "+s"(a.seq), "+s"(a.heads), "+s"(a.kv_heads), "+s"(a.rope_half), "+s"(a.io_bf16),
+                   "+s"(a.norm_q), "+s"(a.eps), "+s"(a.qscale), "+s"(a.nb16), "+s"(a.npairs), "+s"(a.cap),
+                   "+s"(a.items_per_kvh), "+s"(a.q_ld)
+                 : "s"(a.q), "s"(a.qnw), "s"(a.rope_cos), "s"(a.rope_sin), "s"(a.tab), "s"(a.kpool), "s"(a.vpool),
+                   "s"(a.out), "s"(a.part_o), "s"(a.part_ml));
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
     constexpr int KT = P * D;  // elements of one staged K or V tile (16 KiB)
     typedef typename Mfma<T>::vec vec;
@@ -520,44 +568,56 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
         fetch_page(phys, buf, 1);
     };
 
-    // ---- start: the first tile's loads, the page ids, the pair's RoPE rows
-    // and the q rows are all in flight before the first barrier.  The RoPE
-    // rows sit in the LDS slot of tile pair 1, which is first written after
-    // iteration 0.
+    // ---- start: every prologue load is issued before the first tile's
+    // page copies, in straight-line code -- the item's page ids (up to two
+    // per thread), the page id of this wave's first tile, the q rows and
+    // gamma, the pair's RoPE rows -- so that waiting for the small ones never
+    // waits for the copies (vmcnt retires in order), and they all share one
+    // memory round trip.  The RoPE rows go to the LDS slot of tile pair 1,
+    // which is first written after iteration 0.
     const int nt = it.t1 - it.t0;  // <= kItemTiles (host caps items)
-    const int half_u = __builtin_amdgcn_readfirstlane(half);  // wave-uniform: scalar page-id load
-    if (half_u < nt) fetch(a.tab[it.t0 + half_u], 0);
-    for (int i = tid; i < nt; i += 512) sTab[i] = a.tab[it.t0 + i];
+    static_assert(kItemTiles <= 1024, "two page ids per thread");
+    const int tab0 = a.tab[it.t0 + min(tid, nt - 1)];
+    const int tab1 = a.tab[it.t0 + min(tid + 512, nt - 1)];
+    const int half_u = __builtin_amdgcn_readfirstlane(half);
+    const int phys_first = __builtin_amdgcn_readfirstlane(a.tab[it.t0 + min(half_u, nt - 1)]);
+    QRaw<IN_BF16> raw;
+    bool qok[2];
+    q_load<IN_BF16>(a, h, rowq, okq, grp, c, raw, qok);
+    // RoPE rows: float4 (table, 4 dims, row) i = tid + 512 k of 16 * rope_half
+    // (k = 0, 1; named values, not an array, which the compiler would place
+    // in LDS and store before the tile copies)
+    constexpr int RH = 32 * HK;  // rope_half
+    auto rope_src = [&](int k) {
+        const int i = min(tid + 512 * k, max(16 * RH - 1, 0));
+        const int r = i & 31, f4 = RH ? (i >> 5) % (RH / 4) : 0, tbl = RH ? i / (8 * RH) : 0;
+        const int row = min((r < 16 ? 16 * blkA : 16 * blkB) + (r & 15), a.seq - 1);
+        return (const float4 *)((tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * RH + 4 * f4);
+    };
+    float4 rope_v0 = make_float4(0.f, 0.f, 0.f, 0.f), rope_v1 = rope_v0;
+    if constexpr (HK > 0) {
+        rope_v0 = *rope_src(0);
+        rope_v1 = *rope_src(1);
+    }
+    if (half_u < nt) fetch(phys_first, 0);
+    if (tid < nt) sTab[tid] = tab0;
+    if (tid + 512 < nt) sTab[tid + 512] = tab1;
     // the V slot of buffer 1, parity 0 (16 KiB = 2 * kRopeF4 * 32 float4)
     float *rope_lds = (float *)(sKV + (4 + 2) * KT);
-    {
-        const int rh = a.rope_half;
-        // thread -> (table, 4 dims, row); 2 * 32 * rh / 4 <= 1024 float4
-        for (int i = tid; i < 16 * rh; i += 512) {
-            const int r = i & 31, f4 = (i >> 5) % (rh / 4), tbl = i / (8 * rh);
-            const int row = min((r < 16 ? rowq[0] : rowq[1]) + (r & 15), a.seq - 1);
-            const float *src = (tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * rh + 4 * f4;
-            ((float4 *)rope_lds)[(tbl * kRopeF4 + f4) * 32 + r] = *(const float4 *)src;
-        }
+    if constexpr (HK > 0) {
+        auto rope_put = [&](int k, float4 v) {
+            const int i = tid + 512 * k;
+            if (i < 16 * RH) {
+                const int r = i & 31, f4 = (i >> 5) % (RH / 4), tbl = i / (8 * RH);
+                ((float4 *)rope_lds)[(tbl * kRopeF4 + f4) * 32 + r] = v;
+            }
+        };
+        rope_put(0, rope_v0);
+        rope_put(1, rope_v1);
     }
     vec qf[2][4];
-    bool qok[2];
-    const int hk = a.rope_half >> 5;  // rope_dim / 64
-    if (a.io_bf16) {
-        QRaw<true> raw;
-        q_load<true>(a, h, rowq, okq, grp, c, raw, qok);
-        __syncthreads();
-        if (hk == 2) q_finish<T, true, 2>(a, raw, qok, grp, c, rope_lds, qf);
-        else if (hk == 1) q_finish<T, true, 1>(a, raw, qok, grp, c, rope_lds, qf);
-        else q_finish<T, true, 0>(a, raw, qok, grp, c, rope_lds, qf);
-    } else {
-        QRaw<false> raw;
-        q_load<false>(a, h, rowq, okq, grp, c, raw, qok);
-        __syncthreads();
-        if (hk == 2) q_finish<T, false, 2>(a, raw, qok, grp, c, rope_lds, qf);
-        else if (hk == 1) q_finish<T, false, 1>(a, raw, qok, grp, c, rope_lds, qf);
-        else q_finish<T, false, 0>(a, raw, qok, grp, c, rope_lds, qf);
-    }
+    __syncthreads();
+    q_finish<T, IN_BF16, HK>(a, raw, qok, grp, c, rope_lds, qf);
 
     f32x4 o[8][2];
 #pragma unroll
@@ -779,14 +839,22 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs a) {
     }
 }
 
+template <typename T, bool IN_BF16> void launch_flash(const FlashArgs &a, dim3 grid, hipStream_t s) {
+    const int hk = a.rope_half >> 5;
+    if (hk == 2) hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 2>), grid, dim3(512), 0, s, a);
+    else if (hk == 1) hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 1>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 0>), grid, dim3(512), 0, s, a);
+}
+
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s) {
     (void)total_items;
     const int R = 8 / a.kv_heads;
     const int per_xcd = (a.items_per_kvh + R - 1) / R;
-    dim3 grid(per_xcd * 8), block(512);
+    dim3 grid(per_xcd * 8);
+    if (a.rope_dim != 0 && a.rope_dim != 64 && a.rope_dim != 128) return hipErrorInvalidValue;
     switch (kv_dtype) {
-    case 1: hipLaunchKernelGGL(prefill_flash_kernel<F16>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(prefill_flash_kernel<BF16>, grid, block, 0, s, a); break;
+    case 1: a.io_bf16 ? launch_flash<F16, true>(a, grid, s) : launch_flash<F16, false>(a, grid, s); break;
+    case 2: a.io_bf16 ? launch_flash<BF16, true>(a, grid, s) : launch_flash<BF16, false>(a, grid, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
