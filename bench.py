@@ -17,15 +17,21 @@ K/V written into an empty cache.
 
 Printed: ONE JSON line.  `value` is decode-attention HBM GB/s: algorithmic
 bytes per step / GPU time per step, from HIP events recorded on the
-backend's stream around the whole timed region.  `roofline` prices one
-decode call (its split kernel and its merge kernel, back to back) against
-8 TB/s with the same events; `traffic` is read from profiles/traffic.json
-(rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when present.  `prefill`
-carries the prefill TFLOP/s with its own MFMA roofline; `config1`, `config4`
-and `config5` are the other configurations; `gemv` times the weight GEMVs at
-the decode step's shapes; `model` is the whole 32-layer hunyuan-dense model
-(decode tokens/s at position 4096, prompt prefill tokens/s); `cpu_baseline`
-is the C oracle (port of Ops.cs) on this host's cores.
+backend's stream around the whole timed region.  `roofline` prices the
+dominant kernel, decode_attn: the call's algorithmic bytes over that
+kernel's own mean duration, from HIP events recorded around each of its
+launches on the backend's stream (a second pass over the same calls on a
+context created with HYMT_HIP_TIMING=quiet); `roofline.call` prices the whole
+call (both launches) the same way; `traffic` is read from
+profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when
+present.  `prefill` carries the prefill TFLOP/s with the flash kernel's MFMA
+roofline; `config1`, `config4` and `config5` are the other configurations;
+`gemv` times the weight GEMVs at the decode step's shapes; `ceilings` are
+rates measured on this GPU (launch gap, HBM stream read, MFMA, LDS); `model`
+is the whole 32-layer hunyuan-dense model (decode tokens/s at position 4096,
+prompt prefill tokens/s).  `cpu_baseline` is the C oracle (port of Ops.cs)
+on this host's cores, multi-threaded and on one thread, with the host's CPU
+model and ISA.
 """
 from __future__ import annotations
 
@@ -94,6 +100,34 @@ class HipEvents:
         self.L.hipEventDestroy(e)
 
 
+def new_backend(kernel_timing=False):
+    """A device backend; kernel_timing: created with HYMT_HIP_TIMING=quiet, so
+    that every call records HIP events around each kernel on the launch stream
+    (HipBackend.timing reads the totals)."""
+    old = os.environ.get("HYMT_HIP_TIMING")
+    if kernel_timing:
+        os.environ["HYMT_HIP_TIMING"] = "quiet"
+    try:
+        return HipBackend(0)
+    finally:
+        if old is None:
+            os.environ.pop("HYMT_HIP_TIMING", None)
+        else:
+            os.environ["HYMT_HIP_TIMING"] = old
+
+
+def kernel_means(be, names):
+    """{kernel: {launches, avg_us}} of the timed calls so far."""
+    out = {}
+    for name in names:
+        try:
+            n, us = be.timing(name)
+        except N.ArgumentError:
+            continue  # never launched (e.g. no merge for a single split)
+        out[name] = {"launches": n, "avg_us": round(us / n, 3)}
+    return out
+
+
 def decode_pool(config, ctx, n=8):
     """`n` distinct seeded cache contents [ctx][Hkv*D] as bf16 bits."""
     scale = 1.0 / np.sqrt(D)
@@ -103,7 +137,7 @@ def decode_pool(config, ctx, n=8):
 
 
 def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30,
-                norm=True, graph=True):
+                norm=True, graph=True, kernel_timing=False):
     """Decode attention at position `ctx` (L = ctx + 1) over distinct layers.
 
     A step is `layers_per_step` decode calls, one per layer, in stream order
@@ -113,13 +147,16 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     serve the KV reads.  Inputs (q, k, v, gammas) are device-resident.
     Returns per-call and per-step times from HIP events on the backend's
     stream around the whole timed region.  norm=False passes no gamma
-    vectors (the QK norm step is skipped)."""
+    vectors (the QK norm step is skipped).  kernel_timing: afterwards,
+    `steps` more steps call by call on a context created with
+    HYMT_HIP_TIMING=quiet, which records HIP events around each kernel on the
+    launch stream; returns each kernel's mean duration ("kernels")."""
     L = ctx + 1
     kvb = 4 if kv_dtype == F32 else 2
     bpl = decode_bytes_per_layer(L, kvb)
     nsets = max(1, -(-min_bytes // (bpl * layers_per_step)))
     nl = layers_per_step * nsets
-    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS)
+    be = new_backend(kernel_timing).configure(HQ, HKV, D, D, BASE, EPS)
     be.create_cache(nl, L, kv_dtype)
     pool = decode_pool(config, ctx)
     for layer in range(nl):
@@ -175,6 +212,13 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     ev.destroy(e1)
     for g in graphs:
         be.graph_destroy(g)
+    kernels = None
+    if kernel_timing:
+        be.timing_reset()
+        for s in range(steps):
+            record(s)
+        be.sync()
+        kernels = kernel_means(be, ("decode_attn", "decode_merge"))
 
     out = np.empty((nl, HQ * D), np.float32)
     be.download(out, dout)
@@ -196,15 +240,18 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         "bytes_per_layer": bpl,
         "layers_resident": nl,
         "tokens_per_s": 1e3 / (gpu_ms / steps),
+        "kernels": kernels,
     }
 
 
-def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
+def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timing=False):
     """One prefill chunk of `seq` tokens at positions [p0, p0+seq) over a cache
     holding `p0` seeded positions: the chunk's K/V are appended and every row
     attends causally over [0, p0+row].  Repeating the call rewrites the same
-    rows with the same values, so each timed call does identical work."""
-    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, p0 + seq, kv_dtype)
+    rows with the same values, so each timed call does identical work.
+    kernel_timing: afterwards `steps` more calls with per-kernel HIP events
+    (new_backend); returns each kernel's mean duration ("kernels")."""
+    be = new_backend(kernel_timing).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, p0 + seq, kv_dtype)
     if p0:
         kb, vb = decode_pool(config, p0, 1)[0]
         be.UploadKv(0, 0, p0, kb, vb)
@@ -235,6 +282,13 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
     ms = ev.elapsed_ms(e0, e1) / steps
     ev.destroy(e0)
     ev.destroy(e1)
+    kernels = None
+    if kernel_timing:
+        be.timing_reset()
+        for _ in range(steps):
+            run()
+        be.sync()
+        kernels = kernel_means(be, ("prefill_kv", "prefill_flash", "prefill_merge"))
     out = np.empty((seq, HQ * D), np.float32)
     be.download(out, dout)
     assert np.all(np.isfinite(out))
@@ -243,7 +297,7 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup):
     be.Dispose()
     fl = prefill_flops(p0, seq)
     return {"ms_per_call": ms, "tflops": fl / (ms * 1e-3) / 1e12, "flops": fl,
-            "tokens_per_s": seq / (ms * 1e-3)}
+            "tokens_per_s": seq / (ms * 1e-3), "kernels": kernels}
 
 
 GEMV_CASES = [  # (name, weight type, rows, cols): the decode step's matrix shapes
@@ -333,7 +387,8 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
             om.step(4242, ctx)
         sec = (time.perf_counter() - t0) / cpu_tokens
         del om
-        cpu = {"value": round(1.0 / sec, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+        cpu = {"value": round(1.0 / sec, 4), "unit": "tokens/s", "cores": 1,
+               "what": "the correctness checker's speed, not a CPU baseline",
                "sample": f"{cpu_tokens} decode steps of the same model at position {ctx} after one "
                          f"warm-up ({sec:.2f} s per token), oracle/model.py over the C "
                          f"restatement (oracle/hymt_quant.c, oracle/hymt_oracle.c)"}
@@ -383,6 +438,17 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
             logits = be.ForwardStep(prompt, 0)
         pf_ms = (time.perf_counter() - t0) * 1e3 / prefill_reps
         assert np.all(np.isfinite(logits))
+        # a first prompt of a length not seen before (its GEMM row count falls
+        # in a bucket with no chosen algorithm, which is timed once), then the
+        # same prompt again
+        cold_len = 1531
+        cold = list(np.random.default_rng(10).integers(0, cfg.vocab_size, cold_len))
+        t0 = time.perf_counter()
+        be.ForwardStep(cold, 0)
+        cold_ms = (time.perf_counter() - t0) * 1e3
+        t0 = time.perf_counter()
+        be.ForwardStep(cold, 0)
+        warm_ms = (time.perf_counter() - t0) * 1e3
     finally:
         be.Dispose()
     # prefill FLOPs: 2 per weight value per row, plus causal attention per layer
@@ -404,8 +470,19 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
                         "frac": round(pf_flops / (pf_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
                         "flops": pf_flops,
                         "timing": "wall clock per ForwardStep(prompt, 0), mean of "
-                                  f"{prefill_reps}, chunks of 2048 rows"},
-            "cpu_baseline": cpu}
+                                  f"{prefill_reps}, chunks of 2048 rows",
+                        "unseen_length": {"prompt_tokens": cold_len, "first_ms": round(cold_ms, 3),
+                                          "again_ms": round(warm_ms, 3)}},
+            # The oracle's step is the correctness checker (scalar C, double
+            # sums), not the reference's CPU path (Q8_K activations + SIMD
+            # dots), so it is no CPU baseline; the reference's own CPU figure
+            # is quoted beside it.
+            "oracle_checker_step": cpu,
+            "reference_published_cpu": {
+                "decode_tokens_per_s": 26.55, "prefill_tokens_per_s": 423.99, "quant": "Q4_K_M",
+                "hardware": "Ryzen 7 5800X, 8 threads, AVX2", "source": "README_EN.md:132,138",
+                "note": "decode of 128 tokens after a 512-token context, prefill of a 512-token prompt: "
+                        "other hardware, and a shorter context than this leg's"}}
 
 
 def time_block_store(layers=LAYERS, ctx=CTX, reps=20):
@@ -480,9 +557,9 @@ def measure_ceilings():
                 if per != 8 and not graph:
                     continue
                 ck(L.hc_stream_read(ctypes.c_size_t(nbytes), per, graph, ctypes.byref(d), ctypes.byref(i)))
-                row[f"{16 * per}k_us_{name}"] = round(d.value, 3)
-                row[f"{16 * per}k_gbs_{name}"] = round(nbytes / (d.value * 1e-6) / 1e9, 1)
-            row[f"{16 * per}k_workgroups"] = i.value
+                row[f"{4 * per}k_us_{name}"] = round(d.value, 3)
+                row[f"{4 * per}k_gbs_{name}"] = round(nbytes / (d.value * 1e-6) / 1e9, 1)
+            row[f"{4 * per}k_workgroups"] = i.value
         stream[label] = row
     out["stream_read"] = stream
     mf = {}
@@ -510,6 +587,31 @@ def cpu_threads():
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(n, 16))
+
+
+def cpu_host():
+    """The host the CPU legs ran on (Benchmark/Program.cs:189-211 prints the
+    same: processor, thread count, SIMD support).  `isa` lists the vector
+    extensions the CPU reports; the oracle itself is compiled for AVX2 + FMA +
+    F16C (oracle/Makefile) and uses no wider ones."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name") and model == "unknown":
+                    model = ln.split(":", 1)[1].strip()
+                elif ln.startswith("flags") and not flags:
+                    flags = set(ln.split(":", 1)[1].split())
+    except OSError:
+        pass
+    want = ["avx2", "fma", "f16c", "avx512f", "avx512_bf16", "avx512_fp16", "avx512_vnni", "avx_vnni",
+            "amx_tile", "amx_bf16"]
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = None
+    return {"cpu_model": model, "isa": [w for w in want if w in flags], "nproc": os.cpu_count(),
+            "affinity": aff, "oracle_isa": "avx2+fma+f16c, OpenMP over kv heads / query rows"}
 
 
 def cpu_baseline_decode(threads, layers=LAYERS, seconds=10.0):
@@ -623,17 +725,18 @@ def main():
     dec = pre = None
     extra = {}
     if args.only in (None, "decode"):
-        dec = time_decode(2, CTX, F16, args.steps, args.warmup, graph=not args.no_graph)
+        dec = time_decode(2, CTX, F16, args.steps, args.warmup, graph=not args.no_graph,
+                          kernel_timing=True)
         eager = dec if args.no_graph else time_decode(2, CTX, F16, args.steps, args.warmup,
                                                       graph=False)
     if args.only in (None, "prefill"):
-        pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup)
+        pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup, kernel_timing=True)
     if args.only in (None, "configs"):
         c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False, graph=not args.no_graph)
         extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, QK norm off "
                                         "(the configuration names none)",
                             "unit": "GB/s", "value": round(c1["gbs"], 1), **r4(c1)}
-        c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup)
+        c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup, kernel_timing=True)
         extra["config4"] = {"workload": "prefill chunk 256 at positions 8192..8447 over an "
                                         "8192-position fp16 cache, fp32 in",
                             "unit": "TFLOP/s", "value": round(c4["tflops"], 2), **r4(c4)}
@@ -660,17 +763,26 @@ def main():
     cpu = None
     if not args.no_cpu and dec is not None:
         th = cpu_threads()
-        gbs, sec, reps = cpu_baseline_decode(th)
-        tfl, psec, runs = cpu_baseline_prefill(th)
+        gbs, sec, reps = cpu_baseline_decode(th, seconds=8.0)
+        gbs1, sec1, reps1 = cpu_baseline_decode(1, layers=4, seconds=6.0)
+        tfl, psec, runs = cpu_baseline_prefill(th, seconds=8.0)
+        tfl1, psec1, runs1 = cpu_baseline_prefill(1, seq=512, seconds=6.0)
         cpu = {"value": round(gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
                "sample": f"the 32-layer 4096-context decode step (one KV set), mean of {reps} reps "
                          f"({sec * 1e3:.1f} ms per rep, {reps * sec:.1f} s), C port of "
-                         f"Ops.AttentionDecode (oracle/hymt_oracle.c), fp16 KV",
-               "prefill": {"value": round(tfl, 4), "unit": "TFLOP/s",
+                         f"Ops.AttentionDecode (oracle/hymt_oracle.c), fp16 KV, {th} threads",
+               "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                                 "sample": f"4 layers of the same step, mean of {reps1} reps "
+                                           f"({sec1 * 1e3:.1f} ms per rep), one thread"},
+               "host": cpu_host(),
+               "prefill": {"value": round(tfl, 4), "unit": "TFLOP/s", "cores": th,
                            "sample": f"the 2048-token causal prefill, mean of {runs} runs "
                                      f"({psec:.3f} s per run, {runs * psec:.1f} s), C port of "
                                      f"AttentionScores/SoftmaxCausal/AttentionCombine with "
-                                     f"Forward's 1024 chunking"}}
+                                     f"Forward's 1024 chunking, {th} threads",
+                           "single_thread": {"value": round(tfl1, 4), "unit": "TFLOP/s", "cores": 1,
+                                             "sample": f"a 512-token causal prefill, mean of {runs1} "
+                                                       f"runs ({psec1:.3f} s per run), one thread"}}}
 
     traffic = load_traffic() or {}
     rec = {
@@ -689,25 +801,45 @@ def main():
         rec["decode_eager"] = {"call_us": round(eager["call_us"], 3), "gbs": round(eager["gbs"], 1),
                                "host_submit_us_per_call": round(eager["host_submit_us_per_call"], 3),
                                "submission": eager["submission"]}
-        rec["roofline"] = {"bound": "hbm", "achieved": round(dec["gbs"], 1),
-                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-                           "traffic": traffic.get("decode_config2"),
-                           "kernel": "decode_attn_mfma_kernel<F16> + decode_merge_kernel "
-                                     "(one decode call, both launches)",
-                           "algorithmic_bytes": dec["bytes_per_layer"],
-                           "avg_us": round(dec["call_us"], 3)}
+        # the dominant kernel, decode_attn: the call's algorithmic bytes (every
+        # K/V row it reads, q, the appended row, the gammas; the 8 KiB output
+        # is written by the merge) over its own mean duration, from HIP events
+        # around each launch on the backend's stream
+        kd = (dec["kernels"] or {}).get("decode_attn")
+        kbytes = dec["bytes_per_layer"]
+        if kd:
+            ach = kbytes / (kd["avg_us"] * 1e-6) / 1e9
+            rec["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": round(ach / HBM_PEAK_GBS, 4),
+                               "traffic": traffic.get("decode_config2"),
+                               "kernel": "decode_attn_mfma_kernel<F16> (decode_attn)",
+                               "algorithmic_bytes": kbytes, "avg_us": kd["avg_us"],
+                               "launches_timed": kd["launches"],
+                               "kernels": dec["kernels"],
+                               "call": {"avg_us": round(dec["call_us"], 3),
+                                        "gbs": round(dec["gbs"], 1),
+                                        "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+                                        "what": "one whole decode call (both launches and the gap "
+                                                "between them) in the recorded step"}}
     if pre:
         rec["prefill"] = {"workload": "config 3: causal prefill 2048 tokens, one layer, bf16 in, "
                                       "bf16 MFMA fp32 acc, empty cache",
                           "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
                           "ms_per_call": round(pre["ms_per_call"], 4),
                           "tokens_per_s": round(pre["tokens_per_s"], 1),
-                          "roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
-                                       "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
-                                       "traffic": traffic.get("prefill_config3"),
-                                       "flops": pre["flops"]}}
+                          "call_roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
+                                            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                            "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+                                            "traffic": traffic.get("prefill_config3"),
+                                            "flops": pre["flops"]}}
+        kf = (pre["kernels"] or {}).get("prefill_flash")
+        if kf:
+            ach = pre["flops"] / (kf["avg_us"] * 1e-6) / 1e12
+            rec["prefill"]["roofline"] = {"bound": "mfma", "achieved": round(ach, 1), "peak": BF16_PEAK_TFLOPS,
+                                          "unit": "TFLOP/s", "frac": round(ach / BF16_PEAK_TFLOPS, 4),
+                                          "kernel": "prefill_flash_kernel<BF16> (prefill_flash)",
+                                          "flops": pre["flops"], "avg_us": kf["avg_us"],
+                                          "kernels": pre["kernels"]}
     rec.update(extra)
     rec["cpu_baseline"] = cpu
     print(json.dumps(rec))

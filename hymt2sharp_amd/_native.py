@@ -9,7 +9,9 @@ import ctypes
 import os
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libhymt_hip.so")
+# HYMT_HIP_LIB names another build of the same library (the sanitized one of
+# build_san.py, under the CPU tests)
+LIB_PATH = os.environ.get("HYMT_HIP_LIB") or os.path.join(PKG, "libhymt_hip.so")
 SYNTH_PATH = os.path.join(PKG, "libhymt_synth.so")
 
 HYMT_OK = 0
@@ -87,6 +89,8 @@ SIGNATURES = {
     "hymt_attn_prefill": [_vp, _i, _i, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_attn_prefill_ld": [_vp, _i, _i, _i, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _vp, ctypes.c_uint],
     "hymt_sync": [_vp],
+    "hymt_timing_get": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_long), ctypes.POINTER(ctypes.c_double)],
+    "hymt_timing_reset": [_vp],
     "hymt_get_stream": [_vp, ctypes.POINTER(_vp)],
     "hymt_dev_alloc": [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)],
     "hymt_dev_free": [_vp, _vp],

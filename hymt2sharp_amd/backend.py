@@ -180,6 +180,16 @@ class HipBackend:
     def sync(self):
         N.check(self._lib.hymt_sync(self._h))
 
+    # -- per-kernel timing (HYMT_HIP_TIMING=1 or quiet at creation) -------
+    def timing(self, kernel: str):
+        """(count, summed microseconds) of `kernel` over the timed calls."""
+        n, us = ctypes.c_long(), ctypes.c_double()
+        N.check(self._lib.hymt_timing_get(self._h, kernel.encode(), ctypes.byref(n), ctypes.byref(us)))
+        return n.value, us.value
+
+    def timing_reset(self):
+        N.check(self._lib.hymt_timing_reset(self._h))
+
     # ---- quantized weights (the weight half of LoadModel, IComputeBackend.cs:25-29)
     def weight_upload(self, wtype: int, rows: int, cols: int, data) -> int:
         """Upload a rows x cols matrix given as rows of GGUF blocks; returns a

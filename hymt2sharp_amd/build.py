@@ -4,6 +4,7 @@ libhymt_hip.so      C ABI (include/hymt_hip.h) + gfx950 kernels, via hipcc
 libhymt_synth.so    seeded input generator (plain C), via gcc
 libhymt_ceilings.so the benchmark's measured ceilings (launch gap, HBM stream
                     read, MFMA and LDS rates), via hipcc
+_san/               ASan/UBSan builds of the host-side code (build_san.py)
 
 Run `python -m hymt2sharp_amd.build` or call build_all().
 """
@@ -30,6 +31,7 @@ HIP_SOURCES = {
     "weights.cpp": [],
     "rows.hip": [],
     "gemm.cpp": [],
+    "ktimer.cpp": [],
 }
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 BUILD_DIR = os.path.join(PKG, "_build")
@@ -94,6 +96,10 @@ def build_all():
     build_synth()
     build_ceilings()
     build_hip()
+    # ASan/UBSan builds of the host-side code for the CPU tests (host only;
+    # they reuse the kernel objects just built)
+    from . import build_san
+    build_san.build_sanitized()
 
 
 if __name__ == "__main__":

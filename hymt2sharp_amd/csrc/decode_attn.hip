@@ -25,6 +25,7 @@
 
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
+#include "ktimer.hpp"
 
 namespace hymt {
 
@@ -742,17 +743,21 @@ hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     case 2: k = pick_mfma<BF16>(a.ppw, in_args, full); break;
     default: return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(k, grid, block, 0, s, a);
+    {
+        KernelSpan span("decode_attn", s, true);
+        launch(span, k, grid, block, 0, s, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
     const MergeArgs m{a.part_ml, a.part_acc, a.out, a.nsplit};
     const dim3 heads(a.kv_heads * kGroup);
+    KernelSpan span("decode_merge", s, true);
     if (a.nsplit <= 64)
-        hipLaunchKernelGGL((decode_merge_kernel<8, 8>), heads, dim3(256), 0, s, m);
+        launch(span, decode_merge_kernel<8, 8>, heads, dim3(256), 0, s, m);
     else if (a.nsplit <= 128)
-        hipLaunchKernelGGL((decode_merge_kernel<8, 16>), heads, dim3(256), 0, s, m);
+        launch(span, decode_merge_kernel<8, 16>, heads, dim3(256), 0, s, m);
     else
-        hipLaunchKernelGGL((decode_merge_kernel<16, 16>), heads, dim3(512), 0, s, m);
+        launch(span, decode_merge_kernel<16, 16>, heads, dim3(512), 0, s, m);
     return hipGetLastError();
 }
 

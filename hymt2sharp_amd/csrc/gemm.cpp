@@ -27,6 +27,7 @@
 #include <map>
 #include <tuple>
 
+#include "ktimer.hpp"
 #include "weights.hpp"
 
 namespace hymt {
@@ -262,6 +263,7 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
     }
     const Layouts &l = lit->second;
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
+    KernelSpan span(y_bf16 ? "gemm_bf16_out_bf16" : "gemm_bf16_out_f32", s);
     hipblasStatus_t st = hipblasLtMatmul(g->handle, ch.desc, &alpha, W, l.a, x, l.b, &beta, y, l.c, y, l.c, &l.algo,
                                          g->workspace, l.ws, s);
     return as_hip(st);

@@ -18,6 +18,7 @@
 
 #include <cstdint>
 
+#include "ktimer.hpp"
 #include "weights.hpp"
 
 namespace hymt {
@@ -502,6 +503,18 @@ __global__ __launch_bounds__(256) void embed_kernel(WeightDev w, int row, float 
     }
 }
 
+const char *gemv_span_name(int type) {
+    switch (type) {
+    case kW_F32: return "gemv_f32";
+    case kW_F16: return "gemv_f16";
+    case kW_Q8_0: return "gemv_q8_0";
+    case kW_Q4_K: return "gemv_q4_k";
+    case kW_Q6_K: return "gemv_q6_k";
+    case kW_Q2_0C: return "gemv_q2_0c";
+    default: return "gemv_stq1_0";
+    }
+}
+
 template <typename Unit, bool STQ>
 hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
                     hipStream_t s) {
@@ -516,11 +529,12 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     while (lpr < 64 && blocks(lpr) < 256) lpr *= 2;
     const size_t lds = (size_t)w.cols * 4 + (size_t)w.cols / 8 * 4;
     const dim3 grid(blocks(lpr));
+    KernelSpan span(gemv_span_name(w.type), s, true);
     switch (w.cols / 2048) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 1>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 2>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    case 3: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 3>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    default: hipLaunchKernelGGL((gemv_kernel<Unit, STQ, 4>), grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    case 1: launch(span, gemv_kernel<Unit, STQ, 1>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    case 2: launch(span, gemv_kernel<Unit, STQ, 2>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    case 3: launch(span, gemv_kernel<Unit, STQ, 3>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
+    default: launch(span, gemv_kernel<Unit, STQ, 4>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
     }
     return hipGetLastError();
 }
@@ -547,13 +561,15 @@ __global__ __launch_bounds__(256) void rows_kernel(WeightDev w, const int *__res
 
 template <typename Unit, bool STQ>
 hipError_t launch_rows_t(const WeightDev &w, const int *rows, int row0, int n, float *out, hipStream_t s) {
-    hipLaunchKernelGGL((rows_kernel<Unit, STQ>), dim3(n), dim3(256), 0, s, w, rows, row0, out);
+    KernelSpan span("weight_rows", s, true);
+    launch(span, rows_kernel<Unit, STQ>, dim3(n), dim3(256), 0, s, w, rows, row0, out);
     return hipGetLastError();
 }
 
 template <typename Unit, bool STQ>
 hipError_t launch_embed_t(const WeightDev &w, int row, float *out, hipStream_t s) {
-    hipLaunchKernelGGL((embed_kernel<Unit, STQ>), dim3(1), dim3(256), 0, s, w, row, out);
+    KernelSpan span("embed", s, true);
+    launch(span, embed_kernel<Unit, STQ>, dim3(1), dim3(256), 0, s, w, row, out);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "attn_kernels.hpp"
+#include "ktimer.hpp"
 #include "kv_pages.hpp"
 #include "weights.hpp"
 
@@ -122,6 +123,8 @@ struct hymt_ctx {
     HostBuf h_in, h_out;
     // the prefill GEMMs' hipBLASLt state (created on the first GEMM)
     GemmState *gemm = nullptr;
+    // per-kernel timing (HYMT_HIP_TIMING=1 at creation), else null
+    KernelTimer *timer = nullptr;
 
     // stream capture (hymt_graph_begin .. hymt_graph_end)
     bool capturing = false;
@@ -252,6 +255,10 @@ int check_ctx(hymt_ctx *c, bool need_kv, bool need_dev) {
     return HYMT_OK;
 }
 
+// The timer of a call on `c`: none without timing, and none while recording
+// (a recording holds no events of ours, and waiting on one would fail).
+KernelTimer *call_timer(const hymt_ctx *c) { return c && !c->capturing ? c->timer : nullptr; }
+
 // Calls that synchronise or copy host memory cannot be recorded.
 int refuse_in_capture(hymt_ctx *c, const char *what) {
     if (!c->capturing) return HYMT_OK;
@@ -309,6 +316,7 @@ int hymt_create(int device, hymt_ctx **out) {
         // the no-allocation decode's static workspace: its address on this
         // device, resolved once per device while the device is current
         HIP_TRY(decode_scratch_init(device));
+        c->timer = timer_from_env();
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -336,6 +344,8 @@ int hymt_destroy(hymt_ctx *c) {
         c->h_out.release();
         gemm_state_destroy(c->gemm);
         c->gemm = nullptr;
+        timer_destroy(c->timer);
+        c->timer = nullptr;
         (void)hipStreamDestroy(c->stream);
     }
     delete c;
@@ -598,6 +608,7 @@ static int decode_impl(hymt_ctx *c, int layer, int pos, const float *q, const fl
 
 int hymt_attn_decode(hymt_ctx *c, int layer, int pos, const float *q, const float *k, const float *v,
                      const float *qnw, const float *knw, float *out, unsigned flags) {
+    TimedCall timed(call_timer(c), "attn_decode", pos);
     return decode_impl(c, layer, pos, q, k, v, qnw, knw, out, flags, nullptr, nullptr);
 }
 
@@ -613,6 +624,7 @@ int hymt_attn_decode_noalloc(hymt_ctx *c, int layer, int pos, const float *q, co
     if (c->heads > max_heads)
         return fail(HYMT_E_UNSUPPORTED, "the static decode workspace holds " + std::to_string(max_heads) +
                                             " q heads; the context has " + std::to_string(c->heads));
+    TimedCall timed(call_timer(c), "attn_decode_noalloc", pos);
     return decode_impl(c, layer, pos, q, k, v, qnw, knw, out, HYMT_FLAG_DEVICE_PTRS, ml, acc);
 }
 
@@ -736,6 +748,7 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
 int hymt_attn_prefill(hymt_ctx *c, int layer, int pos, int seq, const void *q, const void *k,
                       const void *v, int io_dtype, const float *qnw, const float *knw, float *out,
                       unsigned flags) {
+    TimedCall timed(call_timer(c), "attn_prefill", seq);
     return prefill_impl(c, layer, pos, seq, q, 0, k, v, 0, io_dtype, qnw, knw, out, flags);
 }
 
@@ -747,6 +760,7 @@ int hymt_attn_prefill_ld(hymt_ctx *c, int layer, int pos, int seq, const void *q
         return fail(HYMT_E_ARG, "hymt_attn_prefill_ld takes device pointers (HYMT_FLAG_DEVICE_PTRS)");
     if (q_ld < c->heads * c->head_dim || kv_ld < c->kv_heads * c->head_dim || q_ld % 8 || kv_ld % 8)
         return fail(HYMT_E_ARG, "row strides must cover a row and be multiples of 8 elements");
+    TimedCall timed(call_timer(c), "attn_prefill_ld", seq);
     return prefill_impl(c, layer, pos, seq, q, q_ld, k, v, kv_ld, io_dtype, qnw, knw, out, flags);
 }
 
@@ -755,6 +769,22 @@ int hymt_sync(hymt_ctx *c) {
     if (int r = refuse_in_capture(c, "hymt_sync")) return r;
     hipError_t e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_timing_get(hymt_ctx *c, const char *kernel, long *count, double *us) {
+    if (int r = check_ctx(c, false, false)) return r;
+    if (!kernel || !count || !us) return fail(HYMT_E_ARG, "null argument");
+    if (!c->timer) return fail(HYMT_E_STATE, "timing is off (HYMT_HIP_TIMING=1 or quiet at creation)");
+    if (!timer_totals(c->timer, kernel, count, us))
+        return fail(HYMT_E_ARG, std::string("no kernel named ") + kernel + " was timed");
+    return HYMT_OK;
+}
+
+int hymt_timing_reset(hymt_ctx *c) {
+    if (int r = check_ctx(c, false, false)) return r;
+    if (!c->timer) return fail(HYMT_E_STATE, "timing is off (HYMT_HIP_TIMING=1 or quiet at creation)");
+    timer_reset(c->timer);
     return HYMT_OK;
 }
 
@@ -851,6 +881,8 @@ int hymt_graph_launch(hymt_ctx *c, hymt_graph *g) {
         return fail(HYMT_E_STATE, "the recording holds addresses of context buffers that have since been "
                                   "reallocated (RoPE table or workspace growth); record it again");
     (void)hipSetDevice(c->device);
+    TimedCall timed(call_timer(c), "graph_launch", 0);
+    KernelSpan span("graph", c->stream);
     hipError_t e = hipGraphLaunch(g->exec, c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipGraphLaunch: ") + hipGetErrorString(e));
     return HYMT_OK;
@@ -1257,6 +1289,7 @@ int hymt_model_decode(hymt_model *m, int token, int pos, float *logits) {
     if (!m) return fail(HYMT_E_ARG, "null model");
     hymt_ctx *c = m->ctx;
     if (int r = check_ctx(c, true, true)) return r;
+    TimedCall timed(call_timer(c), "model_decode", pos);
     if (!m->embd || !logits) return fail(HYMT_E_STATE, "hymt_model_set_io first (and a logits buffer)");
     for (const auto &Ly : m->L)
         if (!Ly.set) return fail(HYMT_E_STATE, "every layer needs hymt_model_set_layer");
@@ -1304,6 +1337,7 @@ int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, flo
     if (!m) return fail(HYMT_E_ARG, "null model");
     hymt_ctx *c = m->ctx;
     if (int r = check_ctx(c, true, true)) return r;
+    TimedCall timed(call_timer(c), "model_prefill", n);
     if (!m->embd || !logits) return fail(HYMT_E_STATE, "hymt_model_set_io first (and a logits buffer)");
     for (const auto &Ly : m->L)
         if (!Ly.set) return fail(HYMT_E_STATE, "every layer needs hymt_model_set_layer");

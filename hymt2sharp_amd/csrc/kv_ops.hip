@@ -4,6 +4,7 @@
 
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
+#include "ktimer.hpp"
 
 namespace hymt {
 
@@ -21,6 +22,7 @@ __global__ void tab_update_kernel(int32_t *tab, TabUpdate u) {
 }
 
 hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n, hipStream_t s) {
+    KernelSpan span("tab_update", s);
     for (int off = 0; off < n; off += 64) {
         TabUpdate u;
         u.n = n - off < 64 ? n - off : 64;
@@ -54,6 +56,7 @@ hipError_t launch_kv_copy_page(void *kpool, void *vpool, size_t layer_bytes, siz
     if (src == dst || layers <= 0) return hipSuccess;
     const size_t page_vec = page_bytes / 16;
     const int bx = (int)std::min<size_t>((page_vec + 255) / 256, 64);
+    KernelSpan span("kv_copy_page", s);
     hipLaunchKernelGGL(kv_copy_page_kernel, dim3(bx, 2 * layers), dim3(256), 0, s, (uint4 *)kpool,
                        (uint4 *)vpool, layer_bytes / 16, page_vec, src, dst);
     return hipGetLastError();
@@ -88,6 +91,7 @@ hipError_t launch_kv_upload(int kv_dtype, const uint16_t *k_bf16, const uint16_t
     int blocks = (int)((n + 255) / 256);
     if (blocks > 4096) blocks = 4096;
     if (blocks < 1) return hipSuccess;
+    KernelSpan span("kv_upload", s);
     switch (kv_dtype) {
     case 0: hipLaunchKernelGGL(kv_upload_kernel<F32>, dim3(blocks), dim3(256), 0, s, k_bf16, v_bf16, tab, (float *)kpool, (float *)vpool, pos, len, kv_heads); break;
     case 1: hipLaunchKernelGGL(kv_upload_kernel<F16>, dim3(blocks), dim3(256), 0, s, k_bf16, v_bf16, tab, (uint16_t *)kpool, (uint16_t *)vpool, pos, len, kv_heads); break;
@@ -123,6 +127,7 @@ hipError_t launch_kv_read(int kv_dtype, const int32_t *tab, const void *kpool, c
     int blocks = (int)((n + 255) / 256);
     if (blocks > 4096) blocks = 4096;
     if (blocks < 1) return hipSuccess;
+    KernelSpan span("kv_read", s);
     switch (kv_dtype) {
     case 0: hipLaunchKernelGGL(kv_read_kernel<F32>, dim3(blocks), dim3(256), 0, s, tab, (const float *)kpool, (const float *)vpool, k_out, v_out, pos, len, kv_heads); break;
     case 1: hipLaunchKernelGGL(kv_read_kernel<F16>, dim3(blocks), dim3(256), 0, s, tab, (const uint16_t *)kpool, (const uint16_t *)vpool, k_out, v_out, pos, len, kv_heads); break;

@@ -30,6 +30,7 @@
 
 #include "attn_kernels.hpp"
 #include "device_common.hpp"
+#include "ktimer.hpp"
 
 namespace hymt {
 
@@ -216,9 +217,10 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
 
 template <typename T, bool IN_BF16> void launch_kv(const PrepArgs &a, dim3 grid, hipStream_t s) {
     const int hk = a.rope_half >> 5;
-    if (hk == 2) hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 2>), grid, dim3(256), 0, s, a);
-    else if (hk == 1) hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 1>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((prefill_kv_kernel<T, IN_BF16, 0>), grid, dim3(256), 0, s, a);
+    KernelSpan span("prefill_kv", s, true);
+    if (hk == 2) launch(span, prefill_kv_kernel<T, IN_BF16, 2>, grid, dim3(256), 0, s, a);
+    else if (hk == 1) launch(span, prefill_kv_kernel<T, IN_BF16, 1>, grid, dim3(256), 0, s, a);
+    else launch(span, prefill_kv_kernel<T, IN_BF16, 0>, grid, dim3(256), 0, s, a);
 }
 
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
@@ -841,9 +843,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
 
 template <typename T, bool IN_BF16> void launch_flash(const FlashArgs &a, dim3 grid, hipStream_t s) {
     const int hk = a.rope_half >> 5;
-    if (hk == 2) hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 2>), grid, dim3(512), 0, s, a);
-    else if (hk == 1) hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 1>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((prefill_flash_kernel<T, IN_BF16, 0>), grid, dim3(512), 0, s, a);
+    KernelSpan span("prefill_flash", s, true);
+    if (hk == 2) launch(span, prefill_flash_kernel<T, IN_BF16, 2>, grid, dim3(512), 0, s, a);
+    else if (hk == 1) launch(span, prefill_flash_kernel<T, IN_BF16, 1>, grid, dim3(512), 0, s, a);
+    else launch(span, prefill_flash_kernel<T, IN_BF16, 0>, grid, dim3(512), 0, s, a);
 }
 
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s) {
@@ -908,7 +911,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
 }
 
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.npairs * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
+    KernelSpan span("prefill_merge", s, true);
+    launch(span, prefill_merge_kernel, dim3(a.npairs * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "device_common.hpp"
+#include "ktimer.hpp"
 #include "weights.hpp"
 
 namespace hymt {
@@ -103,28 +104,32 @@ hipError_t launch_rows_rmsnorm(const float *x, int m, int n, const float *w, flo
                                hipStream_t s) {
     if (n % 4 != 0 || n > 8192 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(rows_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, n, w, eps, out);
+    KernelSpan span("rows_rmsnorm", s, true);
+    launch(span, rows_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, n, w, eps, out);
     return hipGetLastError();
 }
 
 hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipStream_t s) {
     if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(rows_swiglu_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
+    KernelSpan span("rows_swiglu", s, true);
+    launch(span, rows_swiglu_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
     return hipGetLastError();
 }
 
 hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *out, hipStream_t s) {
     if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    hipLaunchKernelGGL(rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
+    KernelSpan span("rows_swiglu_bf16", s, true);
+    launch(span, rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
     return hipGetLastError();
 }
 
 hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s) {
     if (count % 4 != 0) return hipErrorInvalidValue;
     if (count == 0) return hipSuccess;
-    hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(count / 4)), dim3(256), 0, s, x, count / 4, out);
+    KernelSpan span("to_bf16", s, true);
+    launch(span, to_bf16_kernel, dim3(grid_for(count / 4)), dim3(256), 0, s, x, count / 4, out);
     return hipGetLastError();
 }
 

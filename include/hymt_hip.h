@@ -213,6 +213,28 @@ int hymt_attn_prefill_ld(hymt_ctx *ctx, int layer, int pos, int seq, const void 
 int hymt_sync(hymt_ctx *ctx);
 
 /*
+ * Per-kernel timing, the counterpart of the reference's HYMT_VK_TIMING and
+ * HYMT_VK_PFPROF modes (VulkanBackend.cs:55,71-74,410-411,488-540).  Read from
+ * the environment when a device context is created:
+ *   HYMT_HIP_TIMING=1      every public call (attention, model step, replay)
+ *                          records a HIP event pair around each kernel it
+ *                          enqueues, waits for them when it ends and prints
+ *                          one line to stderr, "[hymt timing] <call>(<arg>):
+ *                          <us> us on the GPU, <n> kernels | <kernel> <count>x
+ *                          <us> us | ..."; hymt_destroy prints the totals;
+ *   HYMT_HIP_TIMING=quiet  the same totals without printing.
+ * Timed calls wait for their own kernels; calls being recorded are not timed.
+ * hymt_timing_get returns one kernel's totals (count, summed microseconds)
+ * over the calls timed since creation or hymt_timing_reset; HYMT_E_STATE when
+ * the context does not time, HYMT_E_ARG for a kernel never timed.  Kernel
+ * names: decode_attn, decode_merge, prefill_kv, prefill_flash, prefill_merge,
+ * gemv_<type>, gemm_bf16_out_{f32,bf16}, rows_*, kv_*, embed, weight_rows,
+ * tab_update, graph (a whole replay).
+ */
+int hymt_timing_get(hymt_ctx *ctx, const char *kernel, long *count, double *us);
+int hymt_timing_reset(hymt_ctx *ctx);
+
+/*
  * Recorded call sequences (HIP graphs).  Between hymt_graph_begin and
  * hymt_graph_end the context's stream is captured: device-pointer
  * (HYMT_FLAG_DEVICE_PTRS) attention calls are recorded instead of run, and

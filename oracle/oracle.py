@@ -16,7 +16,9 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libhymt_oracle.so")
+# HYMT_ORACLE_LIB names another build of the same checker (the sanitized one of
+# hymt2sharp_amd/build_san.py, under the CPU tests)
+LIB_PATH = os.environ.get("HYMT_ORACLE_LIB") or os.path.join(HERE, "libhymt_oracle.so")
 
 F32, F16, BF16 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", F16: "f16", BF16: "bf16"}

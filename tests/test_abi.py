@@ -250,3 +250,19 @@ def test_model_prefill_refusals_without_device():
         assert L2.hymt_model_create(h, 2, 2048, 6144, 512, 1e-5, ctypes.byref(m)) == N.HYMT_E_NO_DEVICE
     finally:
         L2.hymt_destroy(h)
+
+
+def test_timing_readout_without_a_timer(monkeypatch):
+    """hymt_timing_get / hymt_timing_reset: HYMT_E_STATE when the context does
+    not time (a host-only context never does, whatever HYMT_HIP_TIMING says),
+    HYMT_E_ARG for null arguments or a null context."""
+    monkeypatch.setenv("HYMT_HIP_TIMING", "1")
+    L, h = host_ctx(64)
+    try:
+        n, us = ctypes.c_long(), ctypes.c_double()
+        assert L.hymt_timing_get(h, b"decode_attn", ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_STATE
+        assert L.hymt_timing_reset(h) == N.HYMT_E_STATE
+        assert L.hymt_timing_get(h, None, ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_ARG
+        assert L.hymt_timing_get(None, b"decode_attn", ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_ARG
+    finally:
+        L.hymt_destroy(h)
