@@ -21,7 +21,7 @@ backend's stream around the whole timed region.  `roofline` prices the
 dominant kernel, decode_attn: the call's algorithmic bytes over that
 kernel's own mean duration, from HIP events recorded around each of its
 launches on the backend's stream (a second pass over the same calls on a
-context created with HYMT_HIP_TIMING=quiet); `roofline.call` prices the whole
+context's quiet timing mode, hymt_timing_enable); `roofline.call` prices the whole
 call (both launches) the same way; `traffic` is read from
 profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when
 present.  `prefill` carries the prefill TFLOP/s with the flash kernel's MFMA
@@ -100,22 +100,6 @@ class HipEvents:
         self.L.hipEventDestroy(e)
 
 
-def new_backend(kernel_timing=False):
-    """A device backend; kernel_timing: created with HYMT_HIP_TIMING=quiet, so
-    that every call records HIP events around each kernel on the launch stream
-    (HipBackend.timing reads the totals)."""
-    old = os.environ.get("HYMT_HIP_TIMING")
-    if kernel_timing:
-        os.environ["HYMT_HIP_TIMING"] = "quiet"
-    try:
-        return HipBackend(0)
-    finally:
-        if old is None:
-            os.environ.pop("HYMT_HIP_TIMING", None)
-        else:
-            os.environ["HYMT_HIP_TIMING"] = old
-
-
 def kernel_means(be, names):
     """{kernel: {launches, avg_us}} of the timed calls so far."""
     out = {}
@@ -148,15 +132,15 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     Returns per-call and per-step times from HIP events on the backend's
     stream around the whole timed region.  norm=False passes no gamma
     vectors (the QK norm step is skipped).  kernel_timing: afterwards,
-    `steps` more steps call by call on a context created with
-    HYMT_HIP_TIMING=quiet, which records HIP events around each kernel on the
-    launch stream; returns each kernel's mean duration ("kernels")."""
+    `steps` more steps call by call with quiet per-kernel timing on
+    (hymt_timing_enable: the dispatch of each kernel stamps HIP events on the
+    launch stream); returns each kernel's mean duration ("kernels")."""
     L = ctx + 1
     kvb = 4 if kv_dtype == F32 else 2
     bpl = decode_bytes_per_layer(L, kvb)
     nsets = max(1, -(-min_bytes // (bpl * layers_per_step)))
     nl = layers_per_step * nsets
-    be = new_backend(kernel_timing).configure(HQ, HKV, D, D, BASE, EPS)
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS)
     be.create_cache(nl, L, kv_dtype)
     pool = decode_pool(config, ctx)
     for layer in range(nl):
@@ -214,10 +198,11 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         be.graph_destroy(g)
     kernels = None
     if kernel_timing:
-        be.timing_reset()
+        be.timing_enable(2)
         for s in range(steps):
             record(s)
         be.sync()
+        be.timing_enable(0)
         kernels = kernel_means(be, ("decode_attn", "decode_merge"))
 
     out = np.empty((nl, HQ * D), np.float32)
@@ -249,9 +234,9 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     holding `p0` seeded positions: the chunk's K/V are appended and every row
     attends causally over [0, p0+row].  Repeating the call rewrites the same
     rows with the same values, so each timed call does identical work.
-    kernel_timing: afterwards `steps` more calls with per-kernel HIP events
-    (new_backend); returns each kernel's mean duration ("kernels")."""
-    be = new_backend(kernel_timing).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, p0 + seq, kv_dtype)
+    kernel_timing: afterwards `steps` more calls with quiet per-kernel timing
+    on (as in time_decode); returns each kernel's mean duration ("kernels")."""
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, p0 + seq, kv_dtype)
     if p0:
         kb, vb = decode_pool(config, p0, 1)[0]
         be.UploadKv(0, 0, p0, kb, vb)
@@ -284,10 +269,11 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     ev.destroy(e1)
     kernels = None
     if kernel_timing:
-        be.timing_reset()
+        be.timing_enable(2)
         for _ in range(steps):
             run()
         be.sync()
+        be.timing_enable(0)
         kernels = kernel_means(be, ("prefill_kv", "prefill_flash", "prefill_merge"))
     out = np.empty((seq, HQ * D), np.float32)
     be.download(out, dout)

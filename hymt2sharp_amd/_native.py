@@ -91,6 +91,7 @@ SIGNATURES = {
     "hymt_sync": [_vp],
     "hymt_timing_get": [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_long), ctypes.POINTER(ctypes.c_double)],
     "hymt_timing_reset": [_vp],
+    "hymt_timing_enable": [_vp, _i],
     "hymt_get_stream": [_vp, ctypes.POINTER(_vp)],
     "hymt_dev_alloc": [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)],
     "hymt_dev_free": [_vp, _vp],

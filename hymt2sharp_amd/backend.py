@@ -187,6 +187,10 @@ class HipBackend:
         N.check(self._lib.hymt_timing_get(self._h, kernel.encode(), ctypes.byref(n), ctypes.byref(us)))
         return n.value, us.value
 
+    def timing_enable(self, mode: int):
+        """0 off (totals kept), 1 time and print per call, 2 time quietly."""
+        N.check(self._lib.hymt_timing_enable(self._h, mode))
+
     def timing_reset(self):
         N.check(self._lib.hymt_timing_reset(self._h))
 

@@ -123,8 +123,10 @@ struct hymt_ctx {
     HostBuf h_in, h_out;
     // the prefill GEMMs' hipBLASLt state (created on the first GEMM)
     GemmState *gemm = nullptr;
-    // per-kernel timing (HYMT_HIP_TIMING=1 at creation), else null
+    // per-kernel timing (HYMT_HIP_TIMING at creation, hymt_timing_enable):
+    // the timer once created, and whether calls are timed now
     KernelTimer *timer = nullptr;
+    bool timing_on = false;
 
     // stream capture (hymt_graph_begin .. hymt_graph_end)
     bool capturing = false;
@@ -257,7 +259,7 @@ int check_ctx(hymt_ctx *c, bool need_kv, bool need_dev) {
 
 // The timer of a call on `c`: none without timing, and none while recording
 // (a recording holds no events of ours, and waiting on one would fail).
-KernelTimer *call_timer(const hymt_ctx *c) { return c && !c->capturing ? c->timer : nullptr; }
+KernelTimer *call_timer(const hymt_ctx *c) { return c && c->timing_on && !c->capturing ? c->timer : nullptr; }
 
 // Calls that synchronise or copy host memory cannot be recorded.
 int refuse_in_capture(hymt_ctx *c, const char *what) {
@@ -317,6 +319,7 @@ int hymt_create(int device, hymt_ctx **out) {
         // device, resolved once per device while the device is current
         HIP_TRY(decode_scratch_init(device));
         c->timer = timer_from_env();
+        c->timing_on = c->timer != nullptr;
     } catch (const HipError &e) {
         delete c;
         return map_hip(e);
@@ -769,6 +772,20 @@ int hymt_sync(hymt_ctx *c) {
     if (int r = refuse_in_capture(c, "hymt_sync")) return r;
     hipError_t e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) return fail(HYMT_E_DEVICE, std::string("hipStreamSynchronize: ") + hipGetErrorString(e));
+    return HYMT_OK;
+}
+
+int hymt_timing_enable(hymt_ctx *c, int mode) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (mode < 0 || mode > 2) return fail(HYMT_E_ARG, "timing mode is 0 (off), 1 (print) or 2 (quiet)");
+    if (mode == 0) {
+        c->timing_on = false;
+        return HYMT_OK;
+    }
+    if (!c->timer) c->timer = timer_create(mode == 1);
+    if (!c->timer) return fail(HYMT_E_OOM, "timer allocation failed");
+    timer_set_print(c->timer, mode == 1);
+    c->timing_on = true;
     return HYMT_OK;
 }
 

@@ -77,6 +77,8 @@ class KernelTimer {
         calls_ = 0;
     }
 
+    void set_print(bool p) { print_ = p; }
+
     void summary() const {
         if (calls_ == 0 || !print_) return;
         std::string line = "[hymt timing] totals over " + std::to_string(calls_) + " calls:";
@@ -144,6 +146,12 @@ KernelTimer *timer_from_env() {
     if (std::strcmp(v, "1") == 0) return new KernelTimer(true);
     if (std::strcmp(v, "quiet") == 0) return new KernelTimer(false);
     return nullptr;
+}
+
+KernelTimer *timer_create(bool print) { return new KernelTimer(print); }
+
+void timer_set_print(KernelTimer *t, bool print) {
+    if (t) t->set_print(print);
 }
 
 void timer_destroy(KernelTimer *t) {

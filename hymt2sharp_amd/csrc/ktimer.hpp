@@ -30,6 +30,9 @@ class KernelTimer;
 
 // A timer when HYMT_HIP_TIMING is 1 or quiet, else null.
 KernelTimer *timer_from_env();
+// A timer that prints per call (print) or only collects.
+KernelTimer *timer_create(bool print);
+void timer_set_print(KernelTimer *t, bool print);
 // Totals of `kernel` over the calls reported so far; false if never timed.
 bool timer_totals(const KernelTimer *t, const char *kernel, long *count, double *us);
 void timer_reset(KernelTimer *t);

@@ -215,7 +215,8 @@ int hymt_sync(hymt_ctx *ctx);
 /*
  * Per-kernel timing, the counterpart of the reference's HYMT_VK_TIMING and
  * HYMT_VK_PFPROF modes (VulkanBackend.cs:55,71-74,410-411,488-540).  Read from
- * the environment when a device context is created:
+ * the environment when a device context is created, and switched later with
+ * hymt_timing_enable:
  *   HYMT_HIP_TIMING=1      every public call (attention, model step, replay)
  *                          records a HIP event pair around each kernel it
  *                          enqueues, waits for them when it ends and prints
@@ -231,6 +232,9 @@ int hymt_sync(hymt_ctx *ctx);
  * gemv_<type>, gemm_bf16_out_{f32,bf16}, rows_*, kv_*, embed, weight_rows,
  * tab_update, graph (a whole replay).
  */
+/* mode 0 stops timing (the totals are kept), 1 times and prints, 2 times
+ * quietly; a device context only (HYMT_E_NO_DEVICE otherwise). */
+int hymt_timing_enable(hymt_ctx *ctx, int mode);
 int hymt_timing_get(hymt_ctx *ctx, const char *kernel, long *count, double *us);
 int hymt_timing_reset(hymt_ctx *ctx);
 

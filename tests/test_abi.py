@@ -262,6 +262,7 @@ def test_timing_readout_without_a_timer(monkeypatch):
         n, us = ctypes.c_long(), ctypes.c_double()
         assert L.hymt_timing_get(h, b"decode_attn", ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_STATE
         assert L.hymt_timing_reset(h) == N.HYMT_E_STATE
+        assert L.hymt_timing_enable(h, 2) == N.HYMT_E_NO_DEVICE
         assert L.hymt_timing_get(h, None, ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_ARG
         assert L.hymt_timing_get(None, b"decode_attn", ctypes.byref(n), ctypes.byref(us)) == N.HYMT_E_ARG
     finally:

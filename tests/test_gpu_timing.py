@@ -98,3 +98,33 @@ def test_quiet_mode_totals(hip_available, monkeypatch, capfd):
     finally:
         be.Dispose()
     assert "[hymt timing]" not in capfd.readouterr().err
+
+
+def test_runtime_switch(hip_available, monkeypatch, capfd):
+    """hymt_timing_enable: a context created without timing times nothing
+    until mode 2 (quiet) or 1 (print) is set; mode 0 stops timing and keeps
+    the totals."""
+    monkeypatch.delenv("HYMT_HIP_TIMING", raising=False)
+    from hymt2sharp_amd import _native as N
+    kb, vb = cache_rows(2, 1000)
+    q, k, v, qnw, knw = new_token(2, 0, "gamma", seq=4)
+    be = HipBackend(0).configure(HQ, HKV, D, D, BASE, EPS).create_cache(1, 1004, F16)
+    try:
+        be.UploadKv(0, 0, 1000, kb, vb)
+        be.DecodeAttention(0, 1000, q[0], k[0], v[0], qnw, knw)
+        with pytest.raises(N.InvalidOperationError):
+            be.timing("decode_attn")  # no timer yet
+        be.timing_enable(2)
+        be.DecodeAttention(0, 1001, q[1], k[1], v[1], qnw, knw)
+        be.timing_enable(0)
+        be.DecodeAttention(0, 1002, q[2], k[2], v[2], qnw, knw)
+        assert be.timing("decode_attn")[0] == 1
+        be.timing_enable(1)
+        be.DecodeAttention(0, 1003, q[3], k[3], v[3], qnw, knw)
+        assert be.timing("decode_attn")[0] == 2
+        with pytest.raises(N.ArgumentError):
+            be.timing_enable(3)
+    finally:
+        be.Dispose()
+    err = capfd.readouterr().err
+    assert err.count("[hymt timing] attn_decode(") == 1 and "attn_decode(1003)" in err
