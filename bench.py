@@ -729,10 +729,13 @@ def main():
         sweep = {}
         for ctx in (1024, 4096, 16384, 32768):
             r = time_decode(5, ctx, F16, max(4, args.steps // 4), args.warmup,
-                            layers_per_step=8, graph=not args.no_graph)
+                            layers_per_step=8, graph=not args.no_graph, kernel_timing=True)
+            kd = (r["kernels"] or {}).get("decode_attn")
             sweep[str(ctx)] = {"gbs": round(r["gbs"], 1), "call_us": round(r["call_us"], 3),
                                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                               "bytes": r["bytes_per_layer"]}
+                               "bytes": r["bytes_per_layer"], "kernels": r["kernels"],
+                               "attn_frac": round(r["bytes_per_layer"] / (kd["avg_us"] * 1e-6) / 1e9
+                                                  / HBM_PEAK_GBS, 4) if kd else None}
         extra["config5"] = {"workload": "decode context sweep, fp16 KV, one layer per call",
                             "unit": "GB/s", "by_context": sweep}
         extra["block_store"] = time_block_store()

@@ -574,25 +574,35 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
 
 // Merge of the split partials (the second launch of a multi-split call):
 // out[h] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s, M = max_s m_s.
-// Workgroup = q head, NG x 32 threads; thread = (split group sg of NG, 4
-// dims) over splits sg + NG k, k < PER (NG * PER >= nsplit).  Every thread
-// issues all its loads (float2 (m, l) and float4 acc per split) at once; the
-// NG split groups are combined through LDS.
+// Workgroup = (q head, 32-dim quarter), 256 threads; thread = (split group
+// sg of 32, 4 dims d4 of the quarter) over splits sg + 32 k, k < PER
+// (32 * PER >= nsplit), so 64 workgroups share the partials' reads and each
+// thread issues at most 8 + 8 loads, all at once.  The split groups combine
+// within each wave by lane swaps, then the 4 waves through LDS.
 struct MergeArgs {
     const float *part_ml;
     const float *part_acc;
     float *out;
     int nsplit;
 };
-template <int NG, int PER>
-__global__ __launch_bounds__(NG * 32) void decode_merge_kernel(MergeArgs a) {
-    constexpr int D = kHeadDim;
-    static_assert(NG * PER <= kMaxSplits, "slots past the workspace");
-    const int h = blockIdx.x, d4 = threadIdx.x & 31, sg = threadIdx.x >> 5;
-    __shared__ float s_m[NG], s_l[NG];
-    __shared__ float4 s_o[NG][32];
+// (m, l, o) += (m2, l2, o2) in base 2: both rescaled to the larger maximum
+__device__ __forceinline__ void merge_pair(float &m, float &l, float4 &o, float m2, float l2, float4 o2) {
+    const float M = fmaxf(m, m2);
+    const float w1 = M == -INFINITY ? 0.0f : exp2f(m - M), w2 = M == -INFINITY ? 0.0f : exp2f(m2 - M);
+    m = M;
+    l = l * w1 + l2 * w2;
+    o = make_float4(o.x * w1 + o2.x * w2, o.y * w1 + o2.y * w2, o.z * w1 + o2.z * w2, o.w * w1 + o2.w * w2);
+}
+template <int PER>
+__global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
+    constexpr int D = kHeadDim, SG = 32;
+    static_assert(SG * PER <= kMaxSplits, "slots past the workspace");
+    const int h = blockIdx.x, qd = blockIdx.y, d4 = threadIdx.x & 7, sg = threadIdx.x >> 3;
+    const int wave = threadIdx.x >> 6;
+    __shared__ float s_m[4][8], s_l[4][8];
+    __shared__ float4 s_o[4][8];
     const float2 *ml = (const float2 *)(a.part_ml + (size_t)h * kMaxSplits * 2);
-    const float4 *pa = (const float4 *)(a.part_acc + (size_t)h * kMaxSplits * D) + d4;
+    const float4 *pa = (const float4 *)(a.part_acc + (size_t)h * kMaxSplits * D) + qd * 8 + d4;
     // Every slot is loaded (the workspace holds kMaxSplits per head; slots at
     // or past nsplit hold stale data) and then masked: a load under a
     // condition would be followed by a wait before the next one is issued.
@@ -600,13 +610,13 @@ __global__ __launch_bounds__(NG * 32) void decode_merge_kernel(MergeArgs a) {
     float4 x[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        const int s = sg + NG * k;
+        const int s = sg + SG * k;
         mlv[k] = ml[s];
         x[k] = pa[(size_t)s * (D / 4)];
     }
 #pragma unroll
     for (int k = 0; k < PER; k++) {
-        const bool ok = sg + NG * k < a.nsplit;
+        const bool ok = sg + SG * k < a.nsplit;
         mlv[k] = ok ? mlv[k] : make_float2(-INFINITY, 0.0f);
         x[k] = ok ? x[k] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
@@ -626,31 +636,25 @@ __global__ __launch_bounds__(NG * 32) void decode_merge_kernel(MergeArgs a) {
             O.w = fmaf(w, x[k].w, O.w);
         }
     }
-    if (d4 == 0) {
-        s_m[sg] = Mv;
-        s_l[sg] = L;
+    // the wave's 8 split groups (lanes d4 + 8 j): swaps across 8, 16, 32 lanes
+#pragma unroll
+    for (int sh = 8; sh < 64; sh <<= 1) {
+        const float m2 = __shfl_xor(Mv, sh), l2 = __shfl_xor(L, sh);
+        const float4 o2 = make_float4(__shfl_xor(O.x, sh), __shfl_xor(O.y, sh), __shfl_xor(O.z, sh),
+                                      __shfl_xor(O.w, sh));
+        merge_pair(Mv, L, O, m2, l2, o2);
     }
-    s_o[sg][d4] = O;
+    if ((threadIdx.x & 63) < 8) {
+        s_m[wave][d4] = Mv;
+        s_l[wave][d4] = L;
+        s_o[wave][d4] = O;
+    }
     __syncthreads();
-    if (sg == 0) {
-        float Mt = s_m[0];
+    if (threadIdx.x < 8) {
 #pragma unroll
-        for (int g = 1; g < NG; g++) Mt = fmaxf(Mt, s_m[g]);
-        float Lt = 0.0f;
-        float4 Ot = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int g = 0; g < NG; g++) {
-            if (s_m[g] == -INFINITY) continue;
-            const float w = exp2f(s_m[g] - Mt);
-            const float4 o = s_o[g][d4];
-            Lt = fmaf(w, s_l[g], Lt);
-            Ot.x = fmaf(w, o.x, Ot.x);
-            Ot.y = fmaf(w, o.y, Ot.y);
-            Ot.z = fmaf(w, o.z, Ot.z);
-            Ot.w = fmaf(w, o.w, Ot.w);
-        }
-        const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
-        ((float4 *)(a.out + (size_t)h * D))[d4] = make_float4(Ot.x * inv, Ot.y * inv, Ot.z * inv, Ot.w * inv);
+        for (int w = 1; w < 4; w++) merge_pair(Mv, L, O, s_m[w][d4], s_l[w][d4], s_o[w][d4]);
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        ((float4 *)(a.out + (size_t)h * D))[qd * 8 + d4] = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
     }
 }
 
@@ -750,14 +754,14 @@ hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.nsplit == 1) return e;
     const MergeArgs m{a.part_ml, a.part_acc, a.out, a.nsplit};
-    const dim3 heads(a.kv_heads * kGroup);
+    const dim3 grid_m(a.kv_heads * kGroup, kHeadDim / 32);  // (q head, 32-dim quarter)
     KernelSpan span("decode_merge", s, true);
     if (a.nsplit <= 64)
-        launch(span, decode_merge_kernel<8, 8>, heads, dim3(256), 0, s, m);
+        launch(span, decode_merge_kernel<2>, grid_m, dim3(256), 0, s, m);
     else if (a.nsplit <= 128)
-        launch(span, decode_merge_kernel<8, 16>, heads, dim3(256), 0, s, m);
+        launch(span, decode_merge_kernel<4>, grid_m, dim3(256), 0, s, m);
     else
-        launch(span, decode_merge_kernel<16, 16>, heads, dim3(512), 0, s, m);
+        launch(span, decode_merge_kernel<8>, grid_m, dim3(256), 0, s, m);
     return hipGetLastError();
 }
 
