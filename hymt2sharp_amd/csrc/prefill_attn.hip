@@ -7,9 +7,9 @@
 // does on other GPUs (pf_kvprep.comp, pf_fa32.comp).
 //
 // Kernels:
-//  prefill_kv     one workgroup per (16-position block, kv head): RoPE + norm
+//  prefill_kv     one workgroup per (32-position block, kv head): RoPE + norm
 //                 of k, k and v rounded into the paged cache (v transposed
-//                 through LDS into the 16-position V^T sub-tiles).
+//                 through LDS into whole V chunks).
 //  prefill_flash  one workgroup per (kv head, 32-row q block, kv tile range):
 //                 8 waves = the 4 q heads of the GQA group x the two parities
 //                 of the range's 64-position tiles, so every SIMD runs two
@@ -88,15 +88,18 @@ __device__ __forceinline__ void load8_in(const void *base, size_t i, bool bf16, 
 }
 
 // ------------------------------------------------------------------ k/v
-// Block (16-position block, kv head); thread (row = tid/16, dims 8*(tid%16)..).
+// Block (32-position block, kv head); thread (row = tid/16, dims 8*(tid%16)..).
 // Straight-line loads, no branch between them (a load under a branch is
 // followed by a wait before the next one): the row's page id first (only
 // the stores need it), then k, v, the row's cos/sin and gamma (the host
 // passes a ones vector when the norm is off).  The RoPE partner of dim d
 // (d +- rope_dim/2) lives in lane c ^ (rope_dim/16) of the same 16-lane row
 // and is fetched by DPP; the norm's sum of squares is a DPP reduction over
-// the row.  K is written as one 16-byte store per thread; V is transposed
-// through LDS into the page's V^T chunks.
+// the row.  K is written as one 16-byte store per thread.  V is transposed
+// through LDS: a V chunk holds 8 positions of one 32-position step, so a
+// block of 32 writes every chunk whole, 1 KiB per wave in one run (blocks
+// of 16 would each write half of every chunk, 8 bytes at a time, and two
+// workgroups on different XCDs would share each cache line).
 // IN_BF16: k/v rows are bf16 (else fp32); HK = rope_dim / 64 in {0, 1, 2}.
 template <int HK> __device__ __forceinline__ float rope_partner_dpp(float x, int c) {
     if constexpr (HK == 2) {  // c ^ 8: rotate the 16-lane row by 8
@@ -109,14 +112,14 @@ template <int HK> __device__ __forceinline__ float rope_partner_dpp(float x, int
 }
 
 template <typename T, bool IN_BF16, int HK>
-__global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
+__global__ __launch_bounds__(512) void prefill_kv_kernel(PrepArgs a) {
     constexpr int D = kHeadDim, P = kPage;
     using S = typename T::storage;
     static_assert(sizeof(S) == 2, "prefill caches are 16-bit");
-    __shared__ __attribute__((aligned(16))) S s_v[16][D];
+    __shared__ __attribute__((aligned(16))) S s_v[32][D];
     const int kvh = blockIdx.y, Hkv = a.kv_heads;
     const int tid = threadIdx.x, r = tid >> 4, c = tid & 15;
-    const int pstart = (a.pos0 & ~15) + 16 * blockIdx.x;  // 16-aligned block start
+    const int pstart = (a.pos0 & ~31) + 32 * blockIdx.x;  // 32-aligned block start
     const int m = pstart + r - a.pos0;                    // row within the chunk
     const bool valid = m >= 0 && m < a.seq;
     const int mc = m < 0 ? 0 : (m < a.seq ? m : a.seq - 1);  // clamped for loads
@@ -193,24 +196,23 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
     // would be waited for at the barrier
     __syncthreads();
     if (valid) *(uint4 *)((S *)a.kpool + page_base + k_off16(pstart % P + r, d0)) = make_uint4(kw[0], kw[1], kw[2], kw[3]);
-    // V: thread -> (d = tid/2, positions h8 + [0, 8) of the block, h8 = 8*(tid%2)),
-    // i.e. 4 positions in each of two V chunks (8-byte stores)
+    // V: thread -> chunk (pc = 4 * (step) + g, d) with d = tid % 128, g = tid / 128:
+    // block rows 4g + [0, 4) and 16 + 4g + [0, 4), one 16-byte store.  In the
+    // chunk's first block a position before the chunk (pos0 not a multiple
+    // of 32) keeps its cached value: those chunks are stored element-wise.
     {
-        const int d = tid >> 1, h8 = (tid & 1) * 8, t0 = pstart % P + h8;
-        S *vpage = (S *)a.vpool + page_base;
-        const int m0 = pstart + h8 - a.pos0;
-        if (m0 >= 0) {
+        const int d = tid & (D - 1), g = tid >> 7;
+        S *vpage = (S *)a.vpool + page_base + v_off16(pstart % P + 4 * g, d);
+        const int rows[8] = {4 * g, 4 * g + 1, 4 * g + 2, 4 * g + 3, 16 + 4 * g, 17 + 4 * g, 18 + 4 * g, 19 + 4 * g};
+        if (pstart + 4 * g >= a.pos0) {
+            uint32_t w[4];
 #pragma unroll
-            for (int q4 = 0; q4 < 2; q4++) {
-                const int rr4 = h8 + 4 * q4;
-                const uint32_t w0 = (uint32_t)s_v[rr4][d] | ((uint32_t)s_v[rr4 + 1][d] << 16);
-                const uint32_t w1 = (uint32_t)s_v[rr4 + 2][d] | ((uint32_t)s_v[rr4 + 3][d] << 16);
-                *(uint2 *)(vpage + v_off16(t0 + 4 * q4, d)) = make_uint2(w0, w1);
-            }
+            for (int e = 0; e < 4; e++) w[e] = (uint32_t)s_v[rows[2 * e]][d] | ((uint32_t)s_v[rows[2 * e + 1]][d] << 16);
+            *(uint4 *)vpage = make_uint4(w[0], w[1], w[2], w[3]);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++)
-                if (m0 + e >= 0) vpage[v_off16(t0 + e, d)] = s_v[h8 + e][d];
+                if (pstart + rows[e] >= a.pos0) vpage[e] = s_v[rows[e]][d];
         }
     }
 }
@@ -218,16 +220,16 @@ __global__ __launch_bounds__(256) void prefill_kv_kernel(PrepArgs a) {
 template <typename T, bool IN_BF16> void launch_kv(const PrepArgs &a, dim3 grid, hipStream_t s) {
     const int hk = a.rope_half >> 5;
     KernelSpan span("prefill_kv", s, true);
-    if (hk == 2) launch(span, prefill_kv_kernel<T, IN_BF16, 2>, grid, dim3(256), 0, s, a);
-    else if (hk == 1) launch(span, prefill_kv_kernel<T, IN_BF16, 1>, grid, dim3(256), 0, s, a);
-    else launch(span, prefill_kv_kernel<T, IN_BF16, 0>, grid, dim3(256), 0, s, a);
+    if (hk == 2) launch(span, prefill_kv_kernel<T, IN_BF16, 2>, grid, dim3(512), 0, s, a);
+    else if (hk == 1) launch(span, prefill_kv_kernel<T, IN_BF16, 1>, grid, dim3(512), 0, s, a);
+    else launch(span, prefill_kv_kernel<T, IN_BF16, 0>, grid, dim3(512), 0, s, a);
 }
 
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
-    // blocks of 16 positions from the chunk's first to the end of the page
+    // blocks of 32 positions from the chunk's first to the end of the page
     // holding its last position (the V rows past the chunk are zeroed)
-    const int first = a.pos0 & ~15, last = ((a.pos0 + a.seq + kPage - 1) & ~(kPage - 1)) - 1;
-    dim3 grid((last - first) / 16 + 1, a.kv_heads);
+    const int first = a.pos0 & ~31, last = ((a.pos0 + a.seq + kPage - 1) & ~(kPage - 1)) - 1;
+    dim3 grid((last - first) / 32 + 1, a.kv_heads);
     if (a.rope_dim != 0 && a.rope_dim != 64 && a.rope_dim != 128) return hipErrorInvalidValue;
     switch (kv_dtype) {
     case 1: a.io_bf16 ? launch_kv<F16, true>(a, grid, s) : launch_kv<F16, false>(a, grid, s); break;
