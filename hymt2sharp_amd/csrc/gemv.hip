@@ -40,14 +40,27 @@ __device__ __forceinline__ float group_sum(float v, int lanes) {
 
 __device__ __forceinline__ float h2f(uint32_t h) { return (float)__builtin_bit_cast(_Float16, (uint16_t)h); }
 
-// bytes 0..3 of w as floats
+// bytes 0..3 of w as floats (v_cvt_f32_ubyte0..3)
 __device__ __forceinline__ void bytes4(uint32_t w, float *o) {
-    // (v_cvt_f32_ubyte0..3)
     o[0] = (float)(w & 0xFFu);
     o[1] = (float)((w >> 8) & 0xFFu);
     o[2] = (float)((w >> 16) & 0xFFu);
     o[3] = (float)(w >> 24);
 }
+
+// w & mask with the mask hidden from the optimiser: bytes4 of the result is
+// then one v_cvt_f32_ubyteN per byte, where a visible mask would be folded
+// into a bit-field extract per byte before each conversion
+__device__ __forceinline__ uint32_t masked(uint32_t w, uint32_t mask) {
+    uint32_t r = w & mask;
+    asm("" : "+v"(r));
+    return r;
+}
+
+// x is staged in LDS with 4 floats of padding after every 64, so that the
+// 16-byte reads of the lanes of a wave (every row of the wave reads the same
+// 8 or 16 addresses, 64 floats apart) fall in different banks
+__device__ __forceinline__ int xpad(int f) { return f + ((f >> 6) << 2); }
 
 __device__ __forceinline__ float dot4(const float *a, float4 b, float acc) {
     acc = fmaf(a[0], b.x, acc);
@@ -68,7 +81,7 @@ struct UnitF32 {
         for (int i = 0; i < 8; i++) v[i] = p[i];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
-        const float4 *xv = (const float4 *)(x + 32 * u);
+        const float4 *xv = (const float4 *)(x + xpad(32 * u));
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -95,7 +108,7 @@ struct UnitF16 {
         for (int i = 0; i < 4; i++) v[i] = p[i];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
-        const float4 *xv = (const float4 *)(x + 32 * u);
+        const float4 *xv = (const float4 *)(x + xpad(32 * u));
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -132,7 +145,7 @@ struct UnitQ8_0 {
         d = w.d[(size_t)r * (w.cols / 32) + u];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *) const {
-        const float4 *xv = (const float4 *)(x + 32 * u);
+        const float4 *xv = (const float4 *)(x + xpad(32 * u));
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -189,16 +202,19 @@ struct UnitQ4_K {
         int sc[2], m[2];
         scales(g, sc, m);
         const uint32_t wd[4] = {qs.x, qs.y, qs.z, qs.w};
-        const float4 *xl = (const float4 *)(x + base), *xh = (const float4 *)(x + base + 32);
+        const float4 *xl = (const float4 *)(x + xpad(base)), *xh = (const float4 *)(x + xpad(base + 32));
         float al = 0.f, ah = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
+            // the high nibbles in place: bytes 16 q, summed then scaled by
+            // 1/16 (exact, the sum's roundings scale with it)
             float lo[4], hi[4];
-            bytes4(wd[i] & 0x0F0F0F0Fu, lo);
-            bytes4((wd[i] >> 4) & 0x0F0F0F0Fu, hi);
+            bytes4(masked(wd[i], 0x0F0F0F0Fu), lo);
+            bytes4(masked(wd[i], 0xF0F0F0F0u), hi);
             al = dot4(lo, xl[i], al);
             ah = dot4(hi, xh[i], ah);
         }
+        ah *= 0.0625f;
         const float sl = xs[base / 8] + xs[base / 8 + 1], sh = xs[base / 8 + 4] + xs[base / 8 + 5];
         return d * (sc[0] * al + sc[1] * ah) - dmin * (m[0] * sl + m[1] * sh);
     }
@@ -259,7 +275,7 @@ struct UnitQ6_K {
             for (int j = 0; j < 4; j++) {
                 float f[4];
                 bytes4(qq[j], f);
-                acc[j] = dot4(f, *(const float4 *)(x + base + 32 * j + 4 * hw), acc[j]);
+                acc[j] = dot4(f, *(const float4 *)(x + xpad(base + 32 * j + 4 * hw)), acc[j]);
             }
         }
         float a_ = 0.f;
@@ -301,7 +317,7 @@ struct UnitQ2_0C {
         d = w.d[(size_t)r * (w.cols / 512) + u / 16];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
-        const float4 *xv = (const float4 *)(x + 32 * u);
+        const float4 *xv = (const float4 *)(x + xpad(32 * u));
         float a = 0.f;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
@@ -358,7 +374,7 @@ struct UnitSTQ1_0 {
         float a = 0.f;
 #pragma unroll
         for (int ln = 0; ln < 4; ln++) {
-            const float4 xa = *(const float4 *)(x + base + 16 * ln), xb = *(const float4 *)(x + base + 16 * ln + 4);
+            const float4 xa = *(const float4 *)(x + xpad(base + 16 * ln)), xb = *(const float4 *)(x + xpad(base + 16 * ln + 4));
             const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
             for (int gi = 0; gi < 8; gi++) a = fmaf((float)((pk[gi] >> (2 * ln)) & 3), xv[gi], a);
@@ -388,8 +404,8 @@ template <typename Unit, bool STQ, int NJ>
 __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__restrict__ xg, float *__restrict__ y,
                                                    int lpr, int flags, const float *__restrict__ nw, float eps) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float *x = smem;               // [cols]
-    float *xs = smem + w.cols;     // [cols / 8]
+    float *x = smem;                        // [cols + cols / 16] (xpad)
+    float *xs = smem + w.cols + w.cols / 16;  // [cols / 8]
     __shared__ uint8_t book[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int upr = w.cols / 32;
@@ -469,8 +485,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
         if (j < nj) {
             const int i = tid + 256 * j;
             const float4 a = xa[j], b = xb[j];
-            ((float4 *)x)[2 * i] = a;
-            ((float4 *)x)[2 * i + 1] = b;
+            float4 *xd = (float4 *)(x + xpad(8 * i));
+            xd[0] = a;
+            xd[1] = b;
             xs[i] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
         }
     __syncthreads();
@@ -527,7 +544,7 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     while (upr / lpr > Unit::kMax) lpr *= 2;
     auto blocks = [&](int l) { return (w.rows + 4 * (64 / l) - 1) / (4 * (64 / l)); };
     while (lpr < 64 && blocks(lpr) < 256) lpr *= 2;
-    const size_t lds = (size_t)w.cols * 4 + (size_t)w.cols / 8 * 4;
+    const size_t lds = ((size_t)w.cols + w.cols / 16) * 4 + (size_t)w.cols / 8 * 4;
     const dim3 grid(blocks(lpr));
     KernelSpan span(gemv_span_name(w.type), s, true);
     switch (w.cols / 2048) {
