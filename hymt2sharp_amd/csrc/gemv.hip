@@ -174,9 +174,9 @@ struct UnitQ4_K {
     static constexpr int kMax = 8;  // units in flight per lane
     uint4 hdr, qs;
     __device__ void load(const WeightDev &w, int r, int u) {
-        const uint8_t *b = (const uint8_t *)w.q + ((size_t)r * (w.cols / 256) + u / 8) * 144;
+        const uint8_t *b = (const uint8_t *)w.q + ((size_t)r * (w.cols / 256) + (u >> 3)) * 144;
         hdr = *(const uint4 *)b;
-        qs = *(const uint4 *)(b + 16 + 16 * (u % 8));
+        qs = *(const uint4 *)(b + 16 + 16 * (u & 7));
     }
     // scales and mins of sub-blocks 2 g and 2 g + 1 (GetScaleMin, Q4K.cs:8-19);
     // scale bytes s[0..11] are hdr.y, hdr.z, hdr.w, byte k of a dword taken by
@@ -196,8 +196,8 @@ struct UnitQ4_K {
         }
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
-        const int g = (u % 8) / 2, h = u % 2;
-        const int base = 256 * (u / 8) + 64 * g + 16 * h;
+        const int g = (u & 7) >> 1, h = (u & 1);
+        const int base = 256 * (u >> 3) + 64 * g + 16 * h;
         const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
         int sc[2], m[2];
         scales(g, sc, m);
@@ -219,8 +219,8 @@ struct UnitQ4_K {
         return d * (sc[0] * al + sc[1] * ah) - dmin * (m[0] * sl + m[1] * sh);
     }
     __device__ void store(int u, float, float *o) const {
-        const int g = (u % 8) / 2, h = u % 2;
-        const int base = 256 * (u / 8) + 64 * g + 16 * h;
+        const int g = (u & 7) >> 1, h = (u & 1);
+        const int base = 256 * (u >> 3) + 64 * g + 16 * h;
         const float d = h2f(hdr.x & 0xFFFF), dmin = h2f(hdr.x >> 16);
         int sc[2], m[2];
         scales(g, sc, m);
@@ -248,9 +248,9 @@ struct UnitQ6_K {
     uint2 a, b, h, sc;
     float d;
     __device__ void load(const WeightDev &w, int r, int u) {
-        const size_t sb = (size_t)r * (w.cols / 256) + u / 8;
+        const size_t sb = (size_t)r * (w.cols / 256) + (u >> 3);
         const uint8_t *blk = (const uint8_t *)w.q + sb * 208;
-        const int n = (u % 8) / 4, p = u % 4;
+        const int n = (u & 7) >> 2, p = (u & 3);
         a = *(const uint2 *)(blk + 64 * n + 8 * p);
         b = *(const uint2 *)(blk + 64 * n + 32 + 8 * p);
         h = *(const uint2 *)(blk + 128 + 32 * n + 8 * p);
@@ -258,8 +258,8 @@ struct UnitQ6_K {
         d = w.d[sb];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs) const {
-        const int n = (u % 8) / 4, p = u % 4;
-        const int base = 256 * (u / 8) + 128 * n + 8 * p;
+        const int n = (u & 7) >> 2, p = (u & 3);
+        const int base = 256 * (u >> 3) + 128 * n + 8 * p;
         // int8 scale i (0..7) of this half: byte i of sc, by shift
         auto scale = [&](int i) { return (float)(int8_t)((((i < 4) ? sc.x : sc.y) >> (8 * (i & 3))) & 0xFFu); };
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -270,9 +270,10 @@ struct UnitQ6_K {
             const uint32_t q2 = (B & 0x0F0F0F0Fu) | (((H >> 2) & 0x03030303u) << 4);
             const uint32_t q3 = ((A >> 4) & 0x0F0F0F0Fu) | (((H >> 4) & 0x03030303u) << 4);
             const uint32_t q4 = ((B >> 4) & 0x0F0F0F0Fu) | (((H >> 6) & 0x03030303u) << 4);
-            const uint32_t qq[4] = {q1, q2, q3, q4};
+            uint32_t qq[4] = {q1, q2, q3, q4};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
+                asm("" : "+v"(qq[j]));  // one v_cvt_f32_ubyteN per code (see masked)
                 float f[4];
                 bytes4(qq[j], f);
                 acc[j] = dot4(f, *(const float4 *)(x + xpad(base + 32 * j + 4 * hw)), acc[j]);
@@ -284,8 +285,8 @@ struct UnitQ6_K {
         return d * a_;
     }
     __device__ void store(int u, float, float *o) const {
-        const int n = (u % 8) / 4, p = u % 4;
-        const int base = 256 * (u / 8) + 128 * n + 8 * p;
+        const int n = (u & 7) >> 2, p = (u & 3);
+        const int base = 256 * (u >> 3) + 128 * n + 8 * p;
         auto scale = [&](int i) { return (float)(int8_t)((((i < 4) ? sc.x : sc.y) >> (8 * (i & 3))) & 0xFFu); };
 #pragma unroll
         for (int hw = 0; hw < 2; hw++) {
@@ -363,11 +364,11 @@ struct UnitSTQ1_0 {
     __device__ void load(const WeightDev &w, int r, int u) {
         slots = *(const uint32_t *)((const uint8_t *)w.q + (size_t)r * (w.cols / 8) + 4 * u);
         signs = ((const uint8_t *)w.q2)[(size_t)r * (w.cols / 32) + u];
-        d = w.d[(size_t)r * (w.cols / 256) + u / 8];
+        d = w.d[(size_t)r * (w.cols / 256) + (u >> 3)];
     }
     __device__ float dot(const WeightDev &, int, int u, const float *x, const float *xs, const uint8_t *book) const {
-        const int c = (u % 8) / 2, hg = u % 2;
-        const int base = 256 * (u / 8) + 64 * c + 8 * hg;
+        const int c = (u & 7) >> 1, hg = (u & 1);
+        const int base = 256 * (u >> 3) + 64 * c + 8 * hg;
         uint32_t pk[8];
 #pragma unroll
         for (int gi = 0; gi < 8; gi++) pk[gi] = book[(((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF)];
@@ -383,8 +384,8 @@ struct UnitSTQ1_0 {
         return d * (a - sx);
     }
     __device__ void store(int u, const uint8_t *book, float *o) const {
-        const int c = (u % 8) / 2, hg = u % 2;
-        const int base = 256 * (u / 8) + 64 * c + 8 * hg;
+        const int c = (u & 7) >> 1, hg = (u & 1);
+        const int base = 256 * (u >> 3) + 64 * c + 8 * hg;
 #pragma unroll
         for (int gi = 0; gi < 8; gi++) {
             const uint32_t pk = book[(((signs >> gi) & 1) << 4) | ((slots >> (4 * gi)) & 0xF)];
