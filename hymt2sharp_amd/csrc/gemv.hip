@@ -413,6 +413,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     const int K = upr / lpr;  // units per lane, <= Unit::kMax
     const int row = (blockIdx.x * 4 + wave) * (64 / lpr) + lane / lpr;
     const int sub = lane % lpr;
+    // unit sub + lpr k, written with lpr = 8 lpr8 (lpr is 8, 16, 32 or 64) so
+    // that the compiler sees u & 7 = sub & 7: the unit's place inside its
+    // 256-value block (and the scale bytes it needs) is a lane constant
+    const int lpr8 = lpr >> 3;
 
     // 1. the activations first (small, from L2: their data returns while the
     // weight loads below are still in flight), then this lane's weight loads,
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     const int rl = min(row, w.rows - 1);
 #pragma unroll
     for (int k = 0; k < kMaxK; k++)
-        if (k < K) un[k].load(w, rl, sub + lpr * k);
+        if (k < K) un[k].load(w, rl, sub + 8 * (lpr8 * k));
     if (STQ && tid < 32) book[tid] = kStqBook[tid];
     // 2. x as the input mode makes it, into LDS with its 8-value sums
     auto silu_mul = [](float4 g, float4 u) {
@@ -497,8 +501,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
 #pragma unroll
     for (int k = 0; k < kMaxK; k++) {
         if (k < K) {
-            if constexpr (STQ) part += un[k].dot(w, 0, sub + lpr * k, x, xs, book);
-            else part += un[k].dot(w, 0, sub + lpr * k, x, xs);
+            if constexpr (STQ) part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs, book);
+            else part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs);
         }
     }
     const float s = group_sum(part, lpr);
