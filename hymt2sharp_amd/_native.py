@@ -123,7 +123,7 @@ SIGNATURES = {
 
 # weight types (GgmlTensorType codes) and gemv flags, as in include/hymt_hip.h
 W_F32, W_F16, W_Q8_0, W_Q4_K, W_Q6_K, W_Q2_0C, W_STQ1_0 = 0, 1, 8, 12, 14, 40, 43
-GEMV_ACCUMULATE, GEMV_IN_RMSNORM, GEMV_IN_SWIGLU = 1, 2, 4
+GEMV_ACCUMULATE, GEMV_IN_RMSNORM, GEMV_IN_SWIGLU, GEMV_OUT_SWIGLU = 1, 2, 4, 8
 GEMM_ACCUMULATE, GEMM_OUT_BF16 = 1, 2
 PREFILL_GATE_UP_F32 = 1
 

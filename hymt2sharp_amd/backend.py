@@ -214,11 +214,12 @@ class HipBackend:
         return {"type": t.value, "rows": r.value, "cols": c.value, "device_bytes": b.value}
 
     def gemv(self, w, x_dev, y_dev, accumulate: bool = False, rmsnorm=None, eps: float = 1e-6,
-             swiglu: bool = False):
+             swiglu: bool = False, swiglu_out: bool = False):
         """y (+)= W x' on device vectors (enqueued on the context's stream);
-        x' = RMSNorm(x) * rmsnorm (a device pointer) or silu(gate) * up."""
+        x' = RMSNorm(x) * rmsnorm (a device pointer) or silu(gate) * up.
+        swiglu_out: W is [gate; up] and y = silu(gate rows . x') * (up rows . x')."""
         flags = (N.GEMV_ACCUMULATE if accumulate else 0) | (N.GEMV_IN_RMSNORM if rmsnorm else 0) | \
-                (N.GEMV_IN_SWIGLU if swiglu else 0)
+                (N.GEMV_IN_SWIGLU if swiglu else 0) | (N.GEMV_OUT_SWIGLU if swiglu_out else 0)
         N.check(self._lib.hymt_gemv(self._h, w, x_dev, y_dev, flags, rmsnorm, eps))
 
     # ---- the model: IComputeBackend.LoadModel / ForwardStep (IComputeBackend.cs:25-47)

@@ -411,7 +411,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int upr = w.cols / 32;
     const int K = upr / lpr;  // units per lane, <= Unit::kMax
-    const int row = (blockIdx.x * 4 + wave) * (64 / lpr) + lane / lpr;
+    // lane group gi computes row gi; with kGemvOutSwiGLU (W = [gate; up], F
+    // rows each) the groups alternate gate row gi/2 and up row F + gi/2, so
+    // that a row pair sits in neighbouring groups
+    const int gi = (blockIdx.x * 4 + wave) * (64 / lpr) + lane / lpr;
+    const bool out_swiglu = flags & kGemvOutSwiGLU;
+    const int row = out_swiglu ? (gi & 1) * (w.rows >> 1) + (gi >> 1) : gi;
     const int sub = lane % lpr;
     // unit sub + lpr k, written with lpr = 8 lpr8 (lpr is 8, 16, 32 or 64) so
     // that the compiler sees u & 7 = sub & 7: the unit's place inside its
@@ -443,7 +448,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     }
     constexpr int kMaxK = Unit::kMax;
     Unit un[kMaxK];
-    const int rl = min(row, w.rows - 1);
+    const int rl = gi < w.rows ? row : w.rows - 1;
 #pragma unroll
     for (int k = 0; k < kMaxK; k++)
         if (k < K) un[k].load(w, rl, sub + 8 * (lpr8 * k));
@@ -506,7 +511,24 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
         }
     }
     const float s = group_sum(part, lpr);
-    if (sub == 0 && row < w.rows) y[row] = (flags & kGemvAccumulate) ? y[row] + s : s;
+    if (out_swiglu) {
+        // y[gi/2] = silu(gate) * up (Ops.SiLUMul, Ops.cs:1016-1052; the
+        // reference's fused decode gate/up, dec_ffngu.comp:9-11, 292-301): the
+        // up sum comes from the neighbouring group, in this wave for lpr < 64,
+        // else from the neighbouring wave through LDS
+        float u;
+        if (lpr < 64) {
+            u = __shfl_xor(s, lpr, 64);
+        } else {
+            __shared__ float pair[4];
+            if (lane == 0) pair[wave] = s;
+            __syncthreads();
+            u = pair[wave ^ 1];
+        }
+        if (sub == 0 && !(gi & 1) && gi < w.rows) y[gi >> 1] = s / (1.f + expf(-s)) * u;
+        return;
+    }
+    if (sub == 0 && gi < w.rows) y[row] = (flags & kGemvAccumulate) ? y[row] + s : s;
 }
 
 // One row of the matrix, dequantized (the embedding lookup,

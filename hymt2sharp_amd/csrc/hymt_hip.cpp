@@ -1004,8 +1004,12 @@ int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int f
               float eps) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or vector");
-    if (flags & ~(HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_RMSNORM | HYMT_GEMV_IN_SWIGLU))
+    if (flags & ~(HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_RMSNORM | HYMT_GEMV_IN_SWIGLU | HYMT_GEMV_OUT_SWIGLU))
         return fail(HYMT_E_ARG, "unknown gemv flags");
+    if ((flags & HYMT_GEMV_OUT_SWIGLU) && (flags & HYMT_GEMV_ACCUMULATE))
+        return fail(HYMT_E_ARG, "HYMT_GEMV_OUT_SWIGLU and HYMT_GEMV_ACCUMULATE exclude each other");
+    if ((flags & HYMT_GEMV_OUT_SWIGLU) && (w->dev.rows & 1))
+        return fail(HYMT_E_ARG, "HYMT_GEMV_OUT_SWIGLU needs [gate; up] rows (an even count)");
     if ((flags & HYMT_GEMV_IN_RMSNORM) && (flags & HYMT_GEMV_IN_SWIGLU))
         return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM and HYMT_GEMV_IN_SWIGLU exclude each other");
     if ((flags & HYMT_GEMV_IN_RMSNORM) && !norm_w) return fail(HYMT_E_ARG, "HYMT_GEMV_IN_RMSNORM needs norm_w");
@@ -1337,11 +1341,17 @@ int hymt_model_decode(hymt_model *m, int token, int pos, float *logits) {
                                          HYMT_FLAG_DEVICE_PTRS))
                 return r;
             HIP_TRY(hymt::launch_gemv(Ly.w[3]->dev, ao, h, HYMT_GEMV_ACCUMULATE, nullptr, m->eps, c->stream));
-            HIP_TRY(hymt::launch_gemv(Ly.w[4]->dev, h, gu, norm_in, Ly.ffn_norm, m->eps, c->stream));
-            if (Ly.w[5])
+            if (!Ly.w[5]) {
+                // one [gate; up] matrix: silu(gate) * up straight out of its GEMV
+                HIP_TRY(hymt::launch_gemv(Ly.w[4]->dev, h, gu, norm_in | HYMT_GEMV_OUT_SWIGLU, Ly.ffn_norm, m->eps,
+                                          c->stream));
+                HIP_TRY(hymt::launch_gemv(Ly.down->dev, gu, h, HYMT_GEMV_ACCUMULATE, nullptr, m->eps, c->stream));
+            } else {
+                HIP_TRY(hymt::launch_gemv(Ly.w[4]->dev, h, gu, norm_in, Ly.ffn_norm, m->eps, c->stream));
                 HIP_TRY(hymt::launch_gemv(Ly.w[5]->dev, h, gu + m->ffn, norm_in, Ly.ffn_norm, m->eps, c->stream));
-            HIP_TRY(hymt::launch_gemv(Ly.down->dev, gu, h, HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_SWIGLU, nullptr,
-                                      m->eps, c->stream));
+                HIP_TRY(hymt::launch_gemv(Ly.down->dev, gu, h, HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_SWIGLU, nullptr,
+                                          m->eps, c->stream));
+            }
         }
         HIP_TRY(hymt::launch_gemv(m->out->dev, h, logits, norm_in, m->out_norm, m->eps, c->stream));
     } catch (const HipError &e) {

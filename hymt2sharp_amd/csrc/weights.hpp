@@ -45,7 +45,7 @@ struct PackedWeight {
 bool pack_weight(int type, int rows, int cols, const uint8_t *src, PackedWeight &out);
 
 // gemv flags (as HYMT_GEMV_* in include/hymt_hip.h)
-constexpr int kGemvAccumulate = 1, kGemvInRmsNorm = 2, kGemvInSwiGLU = 4;
+constexpr int kGemvAccumulate = 1, kGemvInRmsNorm = 2, kGemvInSwiGLU = 4, kGemvOutSwiGLU = 8;
 hipError_t launch_gemv(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
                        hipStream_t s);
 hipError_t launch_embed(const WeightDev &w, int row, float *out, hipStream_t s);

@@ -10,12 +10,15 @@ One decode step of a token at position `pos`:
         qkv = [Wq; Wk; Wv] RMSNorm(h, attn_norm)            hymt_gemv IN_RMSNORM
         ao  = attention(q, k, v) (RoPE, QK norm, append)    hymt_attn_decode
         h  += Wo ao                                         hymt_gemv ACCUMULATE
-        gu  = [Wgate; Wup] RMSNorm(h, ffn_norm)             hymt_gemv IN_RMSNORM
-        h  += Wdown (silu(gate) * up)                       hymt_gemv IN_SWIGLU|ACCUMULATE
+        act = silu(Wgate x') * (Wup x'),
+              x' = RMSNorm(h, ffn_norm)                     hymt_gemv IN_RMSNORM|OUT_SWIGLU
+        h  += Wdown act                                     hymt_gemv ACCUMULATE
     logits = Wout RMSNorm(h, output_norm)                   hymt_gemv IN_RMSNORM
 q, k and v (and gate and up) of a layer are uploaded as one matrix when
-their types agree (rows concatenated), so each takes one GEMV.  Everything
-stays on the device; only the logits come back.
+their types agree (rows concatenated), so each takes one GEMV.  Separate
+gate and up matrices take a GEMV each into [gate | up], and the down GEMV
+applies silu(gate) * up to its input (IN_SWIGLU).  Everything stays on the
+device; only the logits come back.
 
 A call with several tokens runs them as a prefill, in chunks of up to 2048
 rows (Forward chunks a prompt by 1024, HunyuanDenseModel.cs:342-355; the
@@ -173,11 +176,12 @@ class DeviceModel:
             be.gemv(L["o"], self.ao, self.h, accumulate=True)
             gu = L["gate_up"]
             if len(gu) == 1:
-                be.gemv(gu[0], self.h, self.gu, rmsnorm=L["ffn_norm"], eps=c.eps)
+                be.gemv(gu[0], self.h, self.gu, rmsnorm=L["ffn_norm"], eps=c.eps, swiglu_out=True)
+                be.gemv(L["down"], self.gu, self.h, accumulate=True)
             else:
                 for w, off in zip(gu, (0, c.ffn_size)):
                     be.gemv(w, self.h, self.gu + 4 * off, rmsnorm=L["ffn_norm"], eps=c.eps)
-            be.gemv(L["down"], self.gu, self.h, accumulate=True, swiglu=True)
+                be.gemv(L["down"], self.gu, self.h, accumulate=True, swiglu=True)
         be.gemv(self.out, self.h, self.logits, rmsnorm=self.out_norm, eps=c.eps)
 
     def prefill(self, tokens, pos: int, gate_up_f32: bool = False):

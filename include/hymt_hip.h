@@ -306,11 +306,17 @@ int hymt_weight_info(const hymt_weight *w, int *type, int *rows, int *cols, size
  *   HYMT_GEMV_IN_SWIGLU   x holds gate[cols] then up[cols];
  *                         x' = gate / (1 + exp(-gate)) * up (Ops.SiLUMul,
  *                         Ops.cs:999-1052: the FFN's down projection input)
+ * and the output as HYMT_GEMV_OUT_SWIGLU makes it:
+ *   HYMT_GEMV_OUT_SWIGLU  W is [gate; up] (rows = 2 F); y[F] = silu(gate) * up
+ *                         with gate = W[0:F] x', up = W[F:2F] x' (the fused
+ *                         gate/up of the reference's Vulkan decode,
+ *                         dec_ffngu.comp:9-11, 292-301; excludes ACCUMULATE)
  * x, y and norm_w are device pointers (x and norm_w 16-byte aligned); the call
  * only enqueues work and may be recorded.  fp32 activations and accumulation. */
 #define HYMT_GEMV_ACCUMULATE 1
 #define HYMT_GEMV_IN_RMSNORM 2
 #define HYMT_GEMV_IN_SWIGLU 4
+#define HYMT_GEMV_OUT_SWIGLU 8
 int hymt_gemv(hymt_ctx *ctx, const hymt_weight *w, const float *x, float *y, int flags,
               const float *norm_w, float eps);
 

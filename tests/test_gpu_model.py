@@ -88,6 +88,64 @@ def test_gemv_swiglu_input_accumulates(hip_available, wtype):
     assert np.all(np.abs(got - ref) <= 1e-5 * mag + 1e-6), np.max(np.abs(got - ref) / mag)
 
 
+@pytest.mark.parametrize("wtype,F,cols,rms", [
+    (N.W_Q4_K, 6145, 2048, True),   # 16 lanes a row: gate/up pairs swap by lane shuffle; a ragged last workgroup
+    (N.W_Q4_K, 301, 2048, False),   # 64 lanes a row: pairs swap through LDS
+    (N.W_Q6_K, 1000, 2048, True),
+    (N.W_Q8_0, 301, 6144, True),
+    (N.W_F32, 64, 2048, False),
+])
+def test_gemv_swiglu_output(hip_available, wtype, F, cols, rms):
+    """HYMT_GEMV_OUT_SWIGLU: W = [gate; up] (2F rows), y[F] = silu(gate x') * (up x')."""
+    rows, eps = 2 * F, 1e-5
+    raw = S.random_weight(70 + wtype + F, wtype, rows, cols)
+    rng = np.random.default_rng(F + cols)
+    x = (rng.standard_normal(cols) * 2).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, cols).astype(np.float32)
+    be = HipBackend(0)
+    try:
+        w = be.weight_upload(wtype, rows, cols, raw)
+        y = np.full(F + 7, 123.0, np.float32)
+
+        def run(dx, dnw, dy):
+            be.gemv(w, dx, dy, rmsnorm=dnw if rms else None, eps=eps, swiglu_out=True)
+            be.sync()
+            out = be.download(np.empty(F + 7, np.float32), dy)
+            with pytest.raises(N.ArgumentError):
+                be.gemv(w, dx, dy, accumulate=True, swiglu_out=True)
+            return out
+        got = _with(be, [x, nw, y], run)
+        be.weight_free(w)
+    finally:
+        be.Dispose()
+    assert np.all(got[F:] == 123.0), "wrote past the F outputs"
+    got = got[:F]
+    xn = O.rmsnorm(x[None, :], nw, eps)[0] if rms else x
+    full = O.dequant(wtype, raw, rows, cols).astype(np.float64)
+    ref = full @ xn.astype(np.float64)
+    mag = np.abs(full) @ np.abs(xn.astype(np.float64))
+    g, u = ref[:F], ref[F:]
+    with np.errstate(over="ignore"):  # exp(-g) = inf for g << 0: silu(g) = -0
+        act = g / (1 + np.exp(-g)) * u
+    # the fp32 sums' errors (1e-5 of sum |w x| each) carried through silu (slope <= 1.1) and the product
+    tol = 1.1 * np.abs(u) * 1e-5 * mag[:F] + np.abs(g) * 1e-5 * mag[F:] + 1e-6 * np.abs(act) + 1e-6
+    assert np.all(np.abs(got - act) <= tol), np.max(np.abs(got - act) / tol)
+
+
+def test_gemv_swiglu_output_needs_pairs(hip_available):
+    be = HipBackend(0)
+    try:
+        w = be.weight_upload(N.W_F32, 3, 2048, np.zeros(3 * 2048, np.float32).tobytes())
+        dx, dy = be.alloc(4 * 2048), be.alloc(16)
+        with pytest.raises(N.ArgumentError):
+            be.gemv(w, dx, dy, swiglu_out=True)
+        be.free(dx)
+        be.free(dy)
+        be.weight_free(w)
+    finally:
+        be.Dispose()
+
+
 @pytest.mark.parametrize("wtype", TYPES)
 def test_embed_rows(hip_available, wtype):
     rows, cols = 97, 2048
