@@ -109,7 +109,7 @@ struct FlashArgs {
     const float *rope_cos, *rope_sin;  // table base [cap][rope_half]
     const int32_t *tab;
     const void *kpool, *vpool;
-    float *out;         // [seq][Hq*D]
+    float *out;         // [seq][Hq*D], fp32, or bf16 bits (RNE) when out_bf16
     float *part_o;      // [Hkv*items][G][32][D]  (split items only)
     float *part_ml;     // [Hkv*items][G][32][2]
     int pos0, seq;
@@ -123,6 +123,7 @@ struct FlashArgs {
     int cap;            // max kv tiles per work item
     int items_per_kvh;  // work items per kv head
     int q_ld;           // elements from one q row to the next, >= Hq*D
+    int out_bf16;       // write out as bf16 (the input of a bf16 GEMM)
 };
 
 // Number of kv tiles (pages) the 16-row q block b attends to.

@@ -16,13 +16,14 @@
 // Algorithm choice.  hipBLASLt's first heuristic choice is not always its
 // fastest at the prefill shapes, so the first call of a shape in an m bucket
 // (m rounded up to a power of two, at least 256) times up to kCandidates
-// candidates on the call's operands and keeps the fastest.  A later m in the
+// of its candidates on the call's operands and keeps the fastest.  A later m in the
 // same bucket reuses that algorithm when the heuristic offers it for the new
 // m (else its first choice): no timing runs and no scratch allocation for
 // each new prompt length.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <tuple>
@@ -35,7 +36,7 @@ namespace hymt {
 namespace {
 
 constexpr size_t kWorkspace = 64u << 20;
-constexpr int kCandidates = 8;
+constexpr int kCandidates = 16;
 
 struct Layouts {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
@@ -139,11 +140,16 @@ hipblasStatus_t heuristic(GemmState &g, hipblasLtMatmulDesc_t desc, const Layout
     return st;
 }
 
-// Time each usable candidate once on the call's operands (writing the
-// state's scratch output, beta = 0 or 1 alike) and return the fastest.
+// Time the usable candidates on the call's operands (writing the state's
+// scratch output, beta = 0 or 1 alike): each runs once to warm up, then
+// kRounds rounds time every candidate once in turn, so that a drift of the
+// clock over the tuning weighs on all candidates alike; the fastest median
+// wins.  (Three back-to-back runs per candidate let such drift pick a
+// candidate 25 % slower than the best on the 12288 x 2048 gate/up GEMM.)
 hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layouts &l,
                            const hipblasLtMatmulHeuristicResult_t *res, int found, const uint16_t *W,
                            const uint16_t *x, size_t ybytes, bool acc, hipStream_t s, int &best) {
+    constexpr int kRounds = 5;
     best = 0;
     hipError_t e = hipSuccess;
     if (ybytes > g.scratch_bytes) {
@@ -156,34 +162,44 @@ hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layou
         g.scratch_bytes = ybytes;
     }
     e = hipMemsetAsync(g.scratch, 0, ybytes, s);
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (e == hipSuccess) e = hipEventCreate(&e0);
-    if (e == hipSuccess) e = hipEventCreate(&e1);
     const float alpha = 1.0f, beta = acc ? 1.0f : 0.0f;
-    float best_ms = 0.f;
-    bool have = false;
+    auto run = [&](int i) {
+        return hipblasLtMatmul(g.handle, desc, &alpha, W, l.a, x, l.b, &beta, g.scratch, l.c, g.scratch, l.c,
+                               &res[i].algo, g.workspace, res[i].workspaceSize, s);
+    };
+    int usable[kCandidates], nu = 0;
     for (int i = 0; i < found && e == hipSuccess; i++) {
         if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspace) continue;
-        auto run = [&]() {
-            return hipblasLtMatmul(g.handle, desc, &alpha, W, l.a, x, l.b, &beta, g.scratch, l.c, g.scratch, l.c,
-                                   &res[i].algo, g.workspace, res[i].workspaceSize, s);
-        };
-        if (run() != HIPBLAS_STATUS_SUCCESS) continue;  // warm-up; a candidate that fails is skipped
-        e = hipEventRecord(e0, s);
-        for (int r = 0; r < 3 && e == hipSuccess; r++)
-            if (run() != HIPBLAS_STATUS_SUCCESS) e = hipErrorUnknown;
-        if (e == hipSuccess) e = hipEventRecord(e1, s);
-        if (e == hipSuccess) e = hipEventSynchronize(e1);
-        float ms = 0.f;
-        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-        if (e == hipSuccess && (!have || ms < best_ms)) {
-            have = true;
-            best_ms = ms;
-            best = i;
+        if (run(i) == HIPBLAS_STATUS_SUCCESS) usable[nu++] = i;  // warm-up; a candidate that fails is skipped
+    }
+    if (nu < 2) {
+        if (nu == 1) best = usable[0];
+        return e;
+    }
+    hipEvent_t ev[2 * kCandidates] = {};
+    for (int j = 0; j < 2 * nu && e == hipSuccess; j++) e = hipEventCreate(&ev[j]);
+    float ms[kCandidates][kRounds] = {};
+    for (int r = 0; r < kRounds && e == hipSuccess; r++) {
+        for (int j = 0; j < nu && e == hipSuccess; j++) {
+            e = hipEventRecord(ev[2 * j], s);
+            if (e == hipSuccess && run(usable[j]) != HIPBLAS_STATUS_SUCCESS) e = hipErrorUnknown;
+            if (e == hipSuccess) e = hipEventRecord(ev[2 * j + 1], s);
+        }
+        if (e == hipSuccess) e = hipEventSynchronize(ev[2 * nu - 1]);
+        for (int j = 0; j < nu && e == hipSuccess; j++) e = hipEventElapsedTime(&ms[j][r], ev[2 * j], ev[2 * j + 1]);
+    }
+    float best_ms = 0.f;
+    for (int j = 0; j < nu && e == hipSuccess; j++) {
+        float v[kRounds];
+        std::memcpy(v, ms[j], sizeof(v));
+        std::sort(v, v + kRounds);
+        if (j == 0 || v[kRounds / 2] < best_ms) {
+            best_ms = v[kRounds / 2];
+            best = usable[j];
         }
     }
-    if (e0) (void)hipEventDestroy(e0);
-    if (e1) (void)hipEventDestroy(e1);
+    for (int j = 0; j < 2 * nu; j++)
+        if (ev[j]) (void)hipEventDestroy(ev[j]);
     return e;
 }
 

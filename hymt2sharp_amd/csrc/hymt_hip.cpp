@@ -632,9 +632,11 @@ int hymt_attn_decode_noalloc(hymt_ctx *c, int layer, int pos, const float *q, co
 }
 
 // q_ld / kv_ld: elements from one q (k, v) row to the next; 0 = packed rows
+// out_bf16 (the model's prefill): out receives bf16 bits, the o-projection
+// GEMM's input, rounded as hymt_to_bf16 rounds the fp32 output
 static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q, int q_ld, const void *k,
                         const void *v, int kv_ld, int io_dtype, const float *qnw, const float *knw, float *out,
-                        unsigned flags) {
+                        unsigned flags, bool out_bf16 = false) {
     if (int r = check_ctx(c, true, false)) return r;
     if (layer < 0 || layer >= c->layers || pos < 0 || seq <= 0 || !q || !k || !v || !out ||
         (io_dtype != HYMT_F32 && io_dtype != HYMT_BF16))
@@ -655,6 +657,7 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
     if (!c->has_device()) return fail(HYMT_E_NO_DEVICE, "context has no device");
     if (!dev)
         if (int r = refuse_in_capture(c, "a host-pointer prefill")) return r;
+    if (out_bf16 && !dev) return fail(HYMT_E_ARG, "bf16 output needs device pointers");
     if (c->capturing && c->pages.needs_copy(pos, seq)) return fail_capture(c, "a write into a harvested block");
     try {
         HIP_TRY(hipSetDevice(c->device));
@@ -706,15 +709,18 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         f.eps = c->eps;
         f.qscale = 1.4426950408889634f / sqrtf((float)D);
         f.q_ld = q_ld ? q_ld : c->heads * (int)D;
+        f.out_bf16 = out_bf16;
         f.nb16 = (seq + 15) / 16;
         f.npairs = (f.nb16 + 1) / 2;
-        // Work items: split the kv range of block pairs only when there are
-        // too few (kv head, pair) combinations to fill the GPU.
+        // Work items: split the kv range of block pairs only when the (kv
+        // head, pair) combinations fill less than half the GPU.  From half
+        // up, the merge launch and its partials cost more than the idle CUs
+        // (1531 rows, 192 pairs: 38.5 + 20.0 us split against 25 us whole).
         int max_tiles = 0;
         for (int pr = 0; pr < f.npairs; pr++) max_tiles = std::max(max_tiles, pair_tiles(pos, pr, f.nb16, seq));
         int cap = max_tiles;
         const int pairs = f.npairs * c->kv_heads;
-        if (pairs < 256) {
+        if (pairs < 128) {
             const int per = (256 + pairs - 1) / pairs;
             cap = std::max(4, (max_tiles + per - 1) / per);
         }
@@ -1004,6 +1010,7 @@ int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int f
               float eps) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or vector");
+    TimedCall timed(call_timer(c), "gemv", w->dev.rows);
     if (flags & ~(HYMT_GEMV_ACCUMULATE | HYMT_GEMV_IN_RMSNORM | HYMT_GEMV_IN_SWIGLU | HYMT_GEMV_OUT_SWIGLU))
         return fail(HYMT_E_ARG, "unknown gemv flags");
     if ((flags & HYMT_GEMV_OUT_SWIGLU) && (flags & HYMT_GEMV_ACCUMULATE))
@@ -1027,6 +1034,7 @@ int hymt_gemv(hymt_ctx *c, const hymt_weight *w, const float *x, float *y, int f
 int hymt_embed(hymt_ctx *c, const hymt_weight *w, int row, float *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !out) return fail(HYMT_E_ARG, "null weight or output");
+    TimedCall timed(call_timer(c), "embed", row);
     if (row < 0 || row >= w->dev.rows)
         return fail(HYMT_E_ARG, "row " + std::to_string(row) + " outside [0, " + std::to_string(w->dev.rows) + ")");
     try {
@@ -1072,6 +1080,7 @@ int hymt_weight_dense(hymt_ctx *c, hymt_weight *w) {
 int hymt_gemm(hymt_ctx *c, const hymt_weight *w, int row0, int nrows, const void *x, int m, void *y, int flags) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !x || !y) return fail(HYMT_E_ARG, "null weight or matrix");
+    TimedCall timed(call_timer(c), "gemm", m);
     if (!w->dense) return fail(HYMT_E_STATE, "weight has no dense copy (hymt_weight_dense)");
     if (flags & ~(HYMT_GEMM_ACCUMULATE | HYMT_GEMM_OUT_BF16)) return fail(HYMT_E_ARG, "unknown gemm flags");
     if ((flags & HYMT_GEMM_ACCUMULATE) && (flags & HYMT_GEMM_OUT_BF16))
@@ -1096,6 +1105,7 @@ int hymt_gemm(hymt_ctx *c, const hymt_weight *w, int row0, int nrows, const void
 int hymt_embed_rows(hymt_ctx *c, const hymt_weight *w, const int32_t *rows, int n, float *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !rows || !out) return fail(HYMT_E_ARG, "null weight, rows or output");
+    TimedCall timed(call_timer(c), "embed_rows", n);
     if (n < 0) return fail(HYMT_E_ARG, "negative row count");
     for (int i = 0; i < n; i++)
         if (rows[i] < 0 || rows[i] >= w->dev.rows)
@@ -1118,6 +1128,7 @@ int hymt_embed_rows(hymt_ctx *c, const hymt_weight *w, const int32_t *rows, int 
 int hymt_rows_rmsnorm(hymt_ctx *c, const float *x, int m, int n, const float *norm_w, float eps, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!x || !norm_w || !out) return fail(HYMT_E_ARG, "null input, weight or output");
+    TimedCall timed(call_timer(c), "rows_rmsnorm", m);
     if (m < 0 || n < 4 || n > 8192 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4 up to 8192");
     if (misaligned16(x) || misaligned16(norm_w) || ((uintptr_t)out & 7u))
         return fail(HYMT_E_ARG, "x and norm_w must be 16-byte aligned, out 8-byte aligned");
@@ -1133,6 +1144,7 @@ int hymt_rows_rmsnorm(hymt_ctx *c, const float *x, int m, int n, const float *no
 int hymt_rows_swiglu(hymt_ctx *c, const float *gate_up, int m, int n, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!gate_up || !out) return fail(HYMT_E_ARG, "null input or output");
+    TimedCall timed(call_timer(c), "rows_swiglu", m);
     if (m < 0 || n < 4 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4");
     if (misaligned16(gate_up) || ((uintptr_t)out & 7u))
         return fail(HYMT_E_ARG, "gate_up must be 16-byte aligned, out 8-byte aligned");
@@ -1148,6 +1160,7 @@ int hymt_rows_swiglu(hymt_ctx *c, const float *gate_up, int m, int n, void *out)
 int hymt_rows_swiglu_bf16(hymt_ctx *c, const void *gate_up, int m, int n, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!gate_up || !out) return fail(HYMT_E_ARG, "null input or output");
+    TimedCall timed(call_timer(c), "rows_swiglu_bf16", m);
     if (m < 0 || n < 4 || n % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "row length must be a multiple of 4");
     if (((uintptr_t)gate_up & 7u) || ((uintptr_t)out & 7u))
         return fail(HYMT_E_ARG, "gate_up and out must be 8-byte aligned");
@@ -1163,6 +1176,7 @@ int hymt_rows_swiglu_bf16(hymt_ctx *c, const void *gate_up, int m, int n, void *
 int hymt_to_bf16(hymt_ctx *c, const float *x, size_t count, void *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!x || !out) return fail(HYMT_E_ARG, "null input or output");
+    TimedCall timed(call_timer(c), "to_bf16", (int)count);
     if (count % 4 != 0) return fail(HYMT_E_UNSUPPORTED, "count must be a multiple of 4");
     if (misaligned16(x) || ((uintptr_t)out & 7u)) return fail(HYMT_E_ARG, "x must be 16-byte aligned, out 8-byte aligned");
     try {
@@ -1192,10 +1206,10 @@ struct hymt_model {
     DevBuf h, qkv, ao, gu;
     // prefill activations (hymt_model_prefill), allocated on its first call
     // for kPrefillRows rows: x fp32 [C][H], xn bf16 [C][H], qkv bf16
-    // [C][q|k|v], ao fp32 and ao16 bf16 [C][qd], gu [C][2F] (bf16, or fp32
+    // [C][q|k|v], ao16 bf16 [C][qd] (the attention writes it as bf16), gu [C][2F] (bf16, or fp32
     // with HYMT_PREFILL_GATE_UP_F32), act bf16 [C][F]; token ids through a
     // pinned buffer whose last copy is marked by tok_ev
-    DevBuf px, pxn, pqkv, pao, pao16, pgu, pact, ptok;
+    DevBuf px, pxn, pqkv, pao16, pgu, pact, ptok;
     HostBuf htok;
     hipEvent_t tok_ev = nullptr;
 };
@@ -1394,7 +1408,6 @@ int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, flo
         m->px.reserve(C * H * 4);
         m->pxn.reserve(C * H * 2);
         m->pqkv.reserve(C * ld * 2);
-        m->pao.reserve(C * qd * 4);
         m->pao16.reserve(C * qd * 2);
         m->pgu.reserve(C * 2 * F * 4);
         m->pact.reserve(C * F * 2);
@@ -1403,7 +1416,7 @@ int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, flo
             m->htok.reserve(C * 4);
             HIP_TRY(hipEventCreateWithFlags(&m->tok_ev, hipEventDisableTiming));
         }
-        float *x = (float *)m->px.p, *ao = (float *)m->pao.p;
+        float *x = (float *)m->px.p;
         uint16_t *xn = (uint16_t *)m->pxn.p, *qkv = (uint16_t *)m->pqkv.p, *ao16 = (uint16_t *)m->pao16.p;
         uint16_t *act = (uint16_t *)m->pact.p;
         void *gu = m->pgu.p;
@@ -1427,9 +1440,8 @@ int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, flo
                     model_gemm(c, Ly.w[2], xn, rows, qkv + qd + kd, ld, true, false);
                 }
                 if (int r = prefill_impl(c, l, p0, rows, qkv, ld, qkv + qd, qkv + qd + kd, ld, HYMT_BF16, Ly.q_norm,
-                                         Ly.k_norm, ao, HYMT_FLAG_DEVICE_PTRS))
+                                         Ly.k_norm, (float *)ao16, HYMT_FLAG_DEVICE_PTRS, true))
                     return r;
-                HIP_TRY(launch_to_bf16(ao, (size_t)rows * qd, ao16, c->stream));
                 model_gemm(c, Ly.w[3], ao16, rows, x, H, false, true);
                 HIP_TRY(launch_rows_rmsnorm(x, rows, H, Ly.ffn_norm, m->eps, xn, c->stream));
                 if (!Ly.w[5]) {
@@ -1462,7 +1474,7 @@ int hymt_model_destroy(hymt_model *m) {
         (void)hipSetDevice(c->device);
         (void)hipStreamSynchronize(c->stream);
     }
-    for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu, &m->px, &m->pxn, &m->pqkv, &m->pao, &m->pao16, &m->pgu,
+    for (DevBuf *b : {&m->h, &m->qkv, &m->ao, &m->gu, &m->px, &m->pxn, &m->pqkv, &m->pao16, &m->pgu,
                       &m->pact, &m->ptok})
         b->release();
     m->htok.release();

@@ -516,7 +516,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     asm volatile(""
                  : "+s"(a.pos0), "+s"(a.seq), "+s"(a.heads), "+s"(a.kv_heads), "+s"(a.rope_half), "+s"(a.io_bf16),
                    "+s"(a.norm_q), "+s"(a.eps), "+s"(a.qscale), "+s"(a.nb16), "+s"(a.npairs), "+s"(a.cap),
-                   "+s"(a.items_per_kvh), "+s"(a.q_ld)
+                   "+s"(a.items_per_kvh), "+s"(a.q_ld), "+s"(a.out_bf16)
                  : "s"(a.q), "s"(a.qnw), "s"(a.rope_cos), "s"(a.rope_sin), "s"(a.tab), "s"(a.kpool), "s"(a.vpool),
                    "s"(a.out), "s"(a.part_o), "s"(a.part_ml));
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
@@ -816,11 +816,23 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
             const int row = rowq[qq] + c;
             if (!okq[qq] || row >= a.seq) continue;
             const float inv = lrun[qq] > 0.f ? 1.0f / lrun[qq] : 0.f;
-            float *orow = a.out + (size_t)row * qdim + (size_t)h * D + grp * 4;
+            const size_t off = (size_t)row * qdim + (size_t)h * D + grp * 4;
+            if (a.out_bf16) {
+                uint16_t *orow = (uint16_t *)a.out + off;
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                f32x4 v = o[db][qq] * inv;
-                *(float4 *)(orow + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
+                for (int db = 0; db < 8; db++) {
+                    f32x4 v = o[db][qq] * inv;
+                    *(uint2 *)(orow + db * 16) =
+                        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+                }
+            } else {
+                float *orow = a.out + off;
+#pragma unroll
+                for (int db = 0; db < 8; db++) {
+                    f32x4 v = o[db][qq] * inv;
+                    *(float4 *)(orow + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
+                }
             }
         }
     } else {
@@ -908,8 +920,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
         acc.w = fmaf(w, v.w, acc.w);
     }
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
-    *(float4 *)(a.out + (size_t)row * a.heads * D + (size_t)(kvh * G + g) * D + d) =
-        make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    const size_t off = (size_t)row * a.heads * D + (size_t)(kvh * G + g) * D + d;
+    if (a.out_bf16)
+        *(uint2 *)((uint16_t *)a.out + off) =
+            make_uint2((uint32_t)f32_to_bf16(acc.x * inv) | ((uint32_t)f32_to_bf16(acc.y * inv) << 16),
+                       (uint32_t)f32_to_bf16(acc.z * inv) | ((uint32_t)f32_to_bf16(acc.w * inv) << 16));
+    else
+        *(float4 *)(a.out + off) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s) {

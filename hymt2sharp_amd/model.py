@@ -37,6 +37,8 @@ separate C ABI calls:
         GU = bf16 RMSNorm(X, ffn_norm) . [Wgate; Wup]^T     hymt_rows_rmsnorm, hymt_gemm OUT_BF16
         X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu_bf16, hymt_gemm ACCUMULATE
     logits = Wout RMSNorm(X[last], output_norm)             hymt_gemv IN_RMSNORM
+(hymt_model_prefill has the attention write bf16(AO) itself, with the
+rounding of hymt_to_bf16, so the two sequences give the same bits.)
 """
 from __future__ import annotations
 

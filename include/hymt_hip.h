@@ -217,7 +217,8 @@ int hymt_sync(hymt_ctx *ctx);
  * HYMT_VK_PFPROF modes (VulkanBackend.cs:55,71-74,410-411,488-540).  Read from
  * the environment when a device context is created, and switched later with
  * hymt_timing_enable:
- *   HYMT_HIP_TIMING=1      every public call (attention, model step, replay)
+ *   HYMT_HIP_TIMING=1      every public call that enqueues kernels (attention,
+ *                          GEMV/GEMM and row kernels, model step, replay)
  *                          records a HIP event pair around each kernel it
  *                          enqueues, waits for them when it ends and prints
  *                          one line to stderr, "[hymt timing] <call>(<arg>):

@@ -61,7 +61,7 @@ def pair_items(pos0, seq, kv_heads, cap=None):
     if cap is None:
         cap = max_tiles
         pairs = npairs * kv_heads
-        if pairs < 256:
+        if pairs < 128:
             per = (256 + pairs - 1) // pairs
             cap = max(4, (max_tiles + per - 1) // per)
     cap = min(cap, ITEM_TILES)
