@@ -31,6 +31,7 @@ HIP_SOURCES = {
     "weights.cpp": [],
     "rows.hip": [],
     "gemm.cpp": [],
+    "gemm_mfma.hip": [],
     "ktimer.cpp": [],
 }
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -55,6 +55,25 @@ __device__ __forceinline__ float dpp_sum16(float v) {
     v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x140, 0xF, 0xF, false));
     return v;
 }
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane i writes LDS bytes lds_base + 16 i.
+// Issued as inline assembly so that the compiler does not treat it as an LDS
+// store that every later LDS read might alias (it would then wait for the
+// load before each read and no copy could overlap the work on earlier
+// tiles).  lds_base must be the same in every lane.  The caller orders it:
+// s_waitcnt vmcnt, then a barrier, before any wave reads the destination.
+// m0 is written here and declared clobbered; the kernels that use this keep
+// nothing else in m0.
+__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(src)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
+}
+
 // The softmax floor of Ops.SoftmaxRow (exp(max(x - max, -80)),
 // Ops.cs:231,245,256) in base-2 units.
 constexpr float kFloor2 = -80.0f * 1.4426950408889634f;

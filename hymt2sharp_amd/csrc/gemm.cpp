@@ -1,6 +1,8 @@
 // gemm.cpp -- the prefill GEMMs: y[m][n] (+)= x[m][k] . W[n][k]^T with bf16
-// operands and fp32 accumulation, on hipBLASLt (plain library GEMMs; the
-// fused work around them lives in rows.hip and the attention kernels).
+// operands and fp32 accumulation, on this library's MFMA kernel
+// (gemm_mfma.hip) or on hipBLASLt, whichever the first call of a shape
+// times faster (the fused work around them lives in rows.hip and the
+// attention kernels).
 //
 // hipBLASLt is column-major.  The row-major buffers map onto it without
 // copies: W [n][k] is a k x n column-major matrix (ld k) used transposed,
@@ -15,15 +17,18 @@
 //
 // Algorithm choice.  hipBLASLt's first heuristic choice is not always its
 // fastest at the prefill shapes, so the first call of a shape in an m bucket
-// (m rounded up to a power of two, at least 256) times up to kCandidates
-// of its candidates on the call's operands and keeps the fastest.  A later m in the
-// same bucket reuses that algorithm when the heuristic offers it for the new
-// m (else its first choice): no timing runs and no scratch allocation for
-// each new prompt length.
+// (m rounded up to a power of two, at least 256) times up to kCandidates of
+// its candidates and the MFMA kernel on the call's operands and keeps the
+// fastest.  A later m in the same bucket reuses that choice (for hipBLASLt,
+// when the heuristic offers the algorithm for the new m, else its first
+// choice): no timing runs and no scratch allocation for each new prompt
+// length.  HYMT_HIP_GEMM=mfma (the MFMA kernel wherever its shape rules
+// allow) or =hipblaslt, read when the state is created, skips the timing.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <tuple>
@@ -42,12 +47,16 @@ struct Layouts {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
     hipblasLtMatmulAlgo_t algo{};
     size_t ws = 0;
+    bool mfma = false;  // the MFMA kernel, when the call's operands fit it
 };
 
 struct Choice {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatmulAlgo_t algo{};  // the timed algorithm of the bucket
+    bool mfma = false;             // the MFMA kernel timed fastest
 };
+
+enum GemmMode { kAuto = 0, kMfmaOnly = 1, kLibOnly = 2 };
 
 void destroy_layouts(Layouts &l) {
     if (l.a) hipblasLtMatrixLayoutDestroy(l.a);
@@ -81,6 +90,7 @@ bool same_algo(const hipblasLtMatmulAlgo_t &x, const hipblasLtMatmulAlgo_t &y) {
 }  // namespace
 
 struct GemmState {
+    int mode = kAuto;
     hipblasLtHandle_t handle = nullptr;
     void *workspace = nullptr;
     void *scratch = nullptr;  // timing output of the candidate runs
@@ -91,7 +101,15 @@ struct GemmState {
     std::map<std::tuple<int, int, int, int, bool, bool>, Layouts> layouts;
 };
 
-GemmState *gemm_state_create() { return new (std::nothrow) GemmState(); }
+GemmState *gemm_state_create() {
+    GemmState *g = new (std::nothrow) GemmState();
+    if (g) {
+        const char *e = std::getenv("HYMT_HIP_GEMM");
+        if (e && !std::strcmp(e, "mfma")) g->mode = kMfmaOnly;
+        if (e && !std::strcmp(e, "hipblaslt")) g->mode = kLibOnly;
+    }
+    return g;
+}
 
 void gemm_state_destroy(GemmState *g) {
     if (!g) return;
@@ -140,17 +158,20 @@ hipblasStatus_t heuristic(GemmState &g, hipblasLtMatmulDesc_t desc, const Layout
     return st;
 }
 
-// Time the usable candidates on the call's operands (writing the state's
-// scratch output, beta = 0 or 1 alike): each runs once to warm up, then
-// kRounds rounds time every candidate once in turn, so that a drift of the
-// clock over the tuning weighs on all candidates alike; the fastest median
-// wins.  (Three back-to-back runs per candidate let such drift pick a
-// candidate 25 % slower than the best on the 12288 x 2048 gate/up GEMM.)
+// Time the usable candidates -- hipBLASLt's and, with_mfma, the MFMA kernel
+// (best = -1) -- on the call's operands, writing the state's scratch output
+// (beta = 0 or 1 alike): each runs once to warm up, then kRounds rounds time
+// every candidate once in turn, so that a drift of the clock over the tuning
+// weighs on all candidates alike; the fastest median wins.  (Three
+// back-to-back runs per candidate let such drift pick a candidate 25 % slower
+// than the best on the 12288 x 2048 gate/up GEMM.)
 hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layouts &l,
                            const hipblasLtMatmulHeuristicResult_t *res, int found, const uint16_t *W,
-                           const uint16_t *x, size_t ybytes, bool acc, hipStream_t s, int &best) {
+                           const uint16_t *x, int n, int k, int m, int ldy, bool y_bf16, bool acc, bool with_mfma,
+                           hipStream_t s, int &best) {
     constexpr int kRounds = 5;
     best = 0;
+    const size_t ybytes = ((size_t)(m - 1) * ldy + n) * (y_bf16 ? 2 : 4);
     hipError_t e = hipSuccess;
     if (ybytes > g.scratch_bytes) {
         e = hipStreamSynchronize(s);
@@ -163,26 +184,29 @@ hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layou
     }
     e = hipMemsetAsync(g.scratch, 0, ybytes, s);
     const float alpha = 1.0f, beta = acc ? 1.0f : 0.0f;
-    auto run = [&](int i) {
+    // candidate i >= 0: hipBLASLt's res[i]; -1: the MFMA kernel
+    auto run = [&](int i) -> bool {
+        if (i < 0) return gemm_bf16_mfma(W, n, k, x, m, g.scratch, ldy, y_bf16, acc, s) == hipSuccess;
         return hipblasLtMatmul(g.handle, desc, &alpha, W, l.a, x, l.b, &beta, g.scratch, l.c, g.scratch, l.c,
-                               &res[i].algo, g.workspace, res[i].workspaceSize, s);
+                               &res[i].algo, g.workspace, res[i].workspaceSize, s) == HIPBLAS_STATUS_SUCCESS;
     };
-    int usable[kCandidates], nu = 0;
+    int usable[kCandidates + 1], nu = 0;
+    if (with_mfma && e == hipSuccess && run(-1)) usable[nu++] = -1;
     for (int i = 0; i < found && e == hipSuccess; i++) {
         if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kWorkspace) continue;
-        if (run(i) == HIPBLAS_STATUS_SUCCESS) usable[nu++] = i;  // warm-up; a candidate that fails is skipped
+        if (run(i)) usable[nu++] = i;  // warm-up; a candidate that fails is skipped
     }
     if (nu < 2) {
         if (nu == 1) best = usable[0];
         return e;
     }
-    hipEvent_t ev[2 * kCandidates] = {};
+    hipEvent_t ev[2 * (kCandidates + 1)] = {};
     for (int j = 0; j < 2 * nu && e == hipSuccess; j++) e = hipEventCreate(&ev[j]);
-    float ms[kCandidates][kRounds] = {};
+    float ms[kCandidates + 1][kRounds] = {};
     for (int r = 0; r < kRounds && e == hipSuccess; r++) {
         for (int j = 0; j < nu && e == hipSuccess; j++) {
             e = hipEventRecord(ev[2 * j], s);
-            if (e == hipSuccess && run(usable[j]) != HIPBLAS_STATUS_SUCCESS) e = hipErrorUnknown;
+            if (e == hipSuccess && !run(usable[j])) e = hipErrorUnknown;
             if (e == hipSuccess) e = hipEventRecord(ev[2 * j + 1], s);
         }
         if (e == hipSuccess) e = hipEventSynchronize(ev[2 * nu - 1]);
@@ -209,6 +233,8 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
                      void *y, int ldy, bool y_bf16, bool accumulate) {
     if (!g || n < 1 || k < 1 || m < 0 || ldy < n || (accumulate && y_bf16)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
+    const bool fits = gemm_mfma_fits(W, n, k, x, m, y, ldy);
+    if (g->mode == kMfmaOnly && fits) return gemm_bf16_mfma(W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     hipError_t e = hipSuccess;
     if (!g->handle) {
         hipblasStatus_t st = hipblasLtCreate(&g->handle);
@@ -255,9 +281,10 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
         }
         int pick = 0;
         if (first_in_bucket) {
-            if (found > 1) {
-                const size_t ybytes = ((size_t)(m - 1) * ldy + n) * (y_bf16 ? 2 : 4);
-                e = time_candidates(*g, ch.desc, l, res, found, W, x, ybytes, accumulate, s, pick);
+            const bool with_mfma = fits && g->mode == kAuto;
+            if (found > 1 || with_mfma) {
+                e = time_candidates(*g, ch.desc, l, res, found, W, x, n, k, m, ldy, y_bf16, accumulate, with_mfma, s,
+                                    pick);
                 if (e != hipSuccess) {
                     destroy_layouts(l);
                     hipblasLtMatmulDescDestroy(ch.desc);
@@ -265,6 +292,8 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
                     return e;
                 }
             }
+            ch.mfma = pick < 0;
+            if (pick < 0) pick = 0;  // hipBLASLt's first choice stays the fallback
             ch.algo = res[pick].algo;
         } else {
             for (int i = 0; i < found; i++)
@@ -275,9 +304,11 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
         }
         l.algo = res[pick].algo;
         l.ws = res[pick].workspaceSize;
+        l.mfma = ch.mfma;
         lit = g->layouts.emplace(lkey, l).first;
     }
     const Layouts &l = lit->second;
+    if (l.mfma && fits) return gemm_bf16_mfma(W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     KernelSpan span(y_bf16 ? "gemm_bf16_out_bf16" : "gemm_bf16_out_f32", s);
     hipblasStatus_t st = hipblasLtMatmul(g->handle, ch.desc, &alpha, W, l.a, x, l.b, &beta, y, l.c, y, l.c, &l.algo,

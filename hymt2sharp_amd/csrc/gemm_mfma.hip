@@ -1,0 +1,245 @@
+// gemm_mfma.hip -- the prefill GEMMs written for gfx950: y[m][n] (+)= x[m][k]
+// . W[n][k]^T with bf16 operands and fp32 accumulation on
+// v_mfma_f32_16x16x32_bf16.  The counterpart of the reference's prefill GEMM
+// shaders (pf_gemm_t32.comp, dispatched at VulkanBackend.cs:782-856): W is a
+// layer's bf16 dense copy (features x k), x the prompt rows (tokens x k).
+//
+// Workgroup tile: 128 features x 128 tokens, 4 waves of 64 x 64 (2 x 2), so a
+// wave runs 16 MFMAs per 32-k step from 8 operand fragments.  k advances in
+// stages of 64; a stage is 32 fragments of 1 KiB (16 of W, 16 of x), copied
+// from global memory straight into LDS (global_load_lds_dwordx4) four stages
+// deep, so that three stages of loads are in flight behind the MFMAs.
+//
+// A fragment (16 rows x 32 k) sits in LDS in operand order: lane (grp, c) =
+// 16 grp + c holds row c, k 8 grp .. 8 grp + 7 at byte 16 lane.  Staging and
+// operand reads are then both linear 1 KiB wave accesses (no bank conflicts),
+// and a lane's staging load is 16 contiguous bytes of one row.
+//
+// Output: MFMA row = feature, column = token, so lane (grp, c) holds features
+// 4 grp .. 4 grp + 3 of token c: one 16-byte store per tile (8 for bf16).
+//
+// Measured on the MI355X at m = 2048 (gemm.cpp times it against hipBLASLt's
+// candidates on a shape's first call and keeps the faster): 0.44-0.52
+// PFLOP/s, below hipBLASLt's 0.6-1.2, so the library serves the model's
+// shapes.  What bounds it, from variants timed on the o projection (2048^3,
+// 39 us): without the copies 22 us -- 64 x 64 wave tiles read 0.5 operand
+// fragments per MFMA, 128 bytes per clock per CU at the MFMA rate, about the
+// LDS read rate; the copies add 17 us -- the direct global->LDS path moves
+// about 28 bytes per clock per CU.  Larger wave tiles (tried up to
+// 128 x 128 per wave with 256-token workgroups) cut the LDS reads but not
+// the copy rate.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "device_common.hpp"
+#include "ktimer.hpp"
+#include "weights.hpp"
+
+namespace hymt {
+namespace {
+
+constexpr int kTF = 128;                  // features per workgroup
+constexpr int kTT = 128;                  // tokens per workgroup
+constexpr int kBK = 64;                   // k per stage
+constexpr int kStages = 4;                // LDS ring depth (stages of kBK)
+constexpr int kFrag = 1024;               // bytes of one 16 x 32 operand fragment
+constexpr int kStageBytes = 32 * kFrag;   // W fragments 0..15, x fragments 16..31
+constexpr int kGroupF = 4;                // feature tiles walked together (L2 reuse)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const uint16_t *W;  // [n][k]
+    const uint16_t *x;  // [m][k]
+    void *y;            // [m][ldy], fp32 or bf16
+    int n, k, m, ldy;
+    int tiles_f, tiles_t, group_f;
+    int xcd_per;        // tiles per XCD run, 0: identity order
+};
+
+// s_waitcnt with only vmcnt (<= 63) constrained (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt and lgkmcnt at their "no wait" maxima)
+#define HYMT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+// Wait until at most `later` stages of this wave's copies (8 each) are
+// outstanding: the copies retire in order, so every earlier stage has landed.
+__device__ __forceinline__ void wait_stages(int later) {
+    switch (later) {
+    case 0: HYMT_WAIT_VM(0); break;
+    case 1: HYMT_WAIT_VM(8); break;
+    case 2: HYMT_WAIT_VM(16); break;
+    default: HYMT_WAIT_VM(24); break;
+    }
+}
+
+// Workgroup b runs on XCD b % 8 (dispatch is round-robin over the 8 XCDs).
+// Tile order: groups of group_f feature tiles, walked token tile by token
+// tile, so that the 32 workgroups an XCD holds at a time cover about 4 x 8
+// tiles and share their W and x rows in that XCD's L2; each XCD takes one
+// contiguous run of that order.
+__device__ __forceinline__ void tile_of(const GemmArgs &a, int b, int &tf, int &tt) {
+    const int L = a.xcd_per ? (b & 7) * a.xcd_per + (b >> 3) : b;
+    const int per_group = a.group_f * a.tiles_t;
+    const int g = L / per_group, r = L - g * per_group;
+    tt = r / a.group_f;
+    tf = g * a.group_f + (r - tt * a.group_f);
+}
+
+typedef bf16x8 Frags[2][4];  // [k step of 32][row block of 16]
+
+// One stage of a wave: the 32 MFMAs of the operands in (cw, cx), with the 16
+// operand reads of the next stage (LDS at sb, this lane's bytes) into (nw,
+// nx) interleaved, one read per two MFMAs, so that the LDS and the matrix
+// pipe work at the same time.
+__device__ __forceinline__ void stage_step(const uint8_t *sb, int wf, int wt, const Frags &cw, const Frags &cx,
+                                           Frags &nw, Frags &nx, f32x4 (&acc)[4][4]) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            nw[ks][i] = *(const bf16x8 *)(sb + ((4 * wf + i) * 2 + ks) * kFrag);
+            nx[ks][i] = *(const bf16x8 *)(sb + (16 + (4 * wt + i) * 2 + ks) * kFrag);
+        }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cw[ks][i], cx[ks][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+    }
+}
+
+template <bool YBF16, bool ACC, int STAGES>
+__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * kStageBytes];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int grp = lane >> 4, c = lane & 15;
+    int tf, tt;
+    tile_of(a, blockIdx.x, tf, tt);
+    const int f0 = tf * kTF, t0 = tt * kTT;
+
+    // staging: wave w copies fragments 8 w .. 8 w + 7 of each stage, i.e.
+    // row blocks rb = 4 (w & 1) + j/2 (j < 8) at k step j & 1 of W (w < 2) or
+    // of x (w >= 2); lane (grp, c) loads row 16 rb + c, k 8 (4 ks + grp) + [0, 8)
+    const bool stage_x = wave >= 2;
+    const uint16_t *src[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int row = (wave & 1) * 64 + j * 16 + c;
+        src[j] = stage_x ? a.x + (size_t)min(t0 + row, a.m - 1) * a.k : a.W + (size_t)(f0 + row) * a.k;
+        src[j] += grp * 8;
+    }
+    const uint32_t lds0 = lds_addr(lds) + wave * 8 * kFrag;
+    auto issue = [&](int s) {
+        const uint32_t dst = lds0 + (s % STAGES) * kStageBytes;
+        const int kk = s * kBK;
+#pragma unroll
+        for (int j = 0; j < 8; j++) lds_dma16(src[j >> 1] + kk + (j & 1) * 32, dst + j * kFrag);
+    };
+    const uint8_t *lane_lds = lds + lane * 16;
+
+    const int wf = wave & 1, wt = wave >> 1;
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int kt = a.k / kBK;  // even, >= 2
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; s++)
+        if (s < kt) issue(s);
+    // stage 0 into registers
+    wait_stages(min(STAGES - 2, kt - 1));
+    asm volatile("s_barrier" ::: "memory");
+    Frags aw, ax, bw, bx;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            aw[ks][i] = *(const bf16x8 *)(lane_lds + ((4 * wf + i) * 2 + ks) * kFrag);
+            ax[ks][i] = *(const bf16x8 *)(lane_lds + (16 + (4 * wt + i) * 2 + ks) * kFrag);
+        }
+    // Stage s: its operands are in registers; make stage s + 1 visible (this
+    // wave's copies landed, then a barrier for every wave's, which also
+    // frees the slot of stage s - 1), refill that slot with stage
+    // s + STAGES - 1, then the MFMAs of s with the reads of s + 1.  After the
+    // last stage the reads fetch a stale slot, unused.
+    auto step = [&](int s, const Frags &cw, const Frags &cx, Frags &nw, Frags &nx) {
+        if (s + 1 < kt) {
+            wait_stages(min(s + STAGES - 2, kt - 1) - (s + 1));
+            asm volatile("s_barrier" ::: "memory");
+            if (s + STAGES - 1 < kt) issue(s + STAGES - 1);
+        }
+        stage_step(lane_lds + ((s + 1) % STAGES) * kStageBytes, wf, wt, cw, cx, nw, nx, acc);
+    };
+    for (int s = 0; s < kt; s += 2) {
+        step(s, aw, ax, bw, bx);
+        step(s + 1, bw, bx, aw, ax);
+    }
+
+    // epilogue: lane (grp, c) of tile (i, j) holds features f .. f + 3 of token t
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int t = t0 + 64 * wt + 16 * j + c;
+        if (t >= a.m) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int f = f0 + 64 * wf + 16 * i + 4 * grp;
+            const f32x4 v = acc[i][j];
+            if constexpr (YBF16) {
+                uint16_t *yp = (uint16_t *)a.y + (size_t)t * a.ldy + f;
+                *(uint2 *)yp = make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                          (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+            } else {
+                float4 *yp = (float4 *)((float *)a.y + (size_t)t * a.ldy + f);
+                float4 o = make_float4(v[0], v[1], v[2], v[3]);
+                if constexpr (ACC) {
+                    const float4 p = *yp;
+                    o = make_float4(p.x + o.x, p.y + o.y, p.z + o.z, p.w + o.w);
+                }
+                *yp = o;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, const void *y, int ldy) {
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    return n > 0 && n % kTF == 0 && k >= 2 * kBK && k % (2 * kBK) == 0 && m > 0 && ldy >= n && ldy % 4 == 0 && a16(W) &&
+           a16(x) && a16(y);
+}
+
+hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,
+                          bool accumulate, hipStream_t s) {
+    if (!gemm_mfma_fits(W, n, k, x, m, y, ldy) || (accumulate && y_bf16)) return hipErrorInvalidValue;
+    GemmArgs a;
+    a.W = W;
+    a.x = x;
+    a.y = y;
+    a.n = n;
+    a.k = k;
+    a.m = m;
+    a.ldy = ldy;
+    a.tiles_f = n / kTF;
+    a.tiles_t = (m + kTT - 1) / kTT;
+    a.group_f = a.tiles_f % kGroupF == 0 ? kGroupF : 1;
+    const int tiles = a.tiles_f * a.tiles_t;
+    a.xcd_per = tiles % 8 == 0 ? tiles / 8 : 0;
+    KernelSpan span(y_bf16 ? "gemm_mfma_out_bf16" : "gemm_mfma_out_f32", s, true);
+    if (y_bf16) launch(span, gemm_bf16_kernel<true, false, kStages>, dim3(tiles), dim3(256), 0, s, a);
+    else if (accumulate) launch(span, gemm_bf16_kernel<false, true, kStages>, dim3(tiles), dim3(256), 0, s, a);
+    else launch(span, gemm_bf16_kernel<false, false, kStages>, dim3(tiles), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace hymt

@@ -316,24 +316,6 @@ template <> struct Mfma<F16> {
 //      its positions are the S^T outputs of lane (grp, c) for blocks 2 ks2
 //      and 2 ks2 + 1: the P^T B operand of that lane, as packed.
 
-// 16 bytes per lane from global memory straight into LDS
-// (global_load_lds_dwordx4): lane i writes LDS bytes lds_base + 16 i.
-// Issued as inline assembly so that the compiler does not treat it as an LDS
-// store that every later LDS read might alias (it would then wait for the
-// load before each read and no copy could overlap the work on earlier
-// tiles).  lds_base must be the same in every lane.  The caller orders it:
-// s_waitcnt vmcnt, then a barrier, before any wave reads the destination.
-// m0 is written here and declared clobbered; the kernels that use this keep
-// nothing else in m0.
-__device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(src)
-                 : "memory", "m0");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
-}
 
 // Row sum of a packed pair of softmax weights (v_dot2c_f32_{bf16,f16} with
 // (1, 1)): l accumulates exactly the rounded weights the P*V MFMA uses.

@@ -58,13 +58,20 @@ hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipS
 hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *out, hipStream_t s);
 hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s);
 // y[m][n] (+)= x[m][k] . W[n][k]^T, bf16 operands, fp32 accumulation
-// (gemm.cpp, hipBLASLt); y is fp32 or, with y_bf16, bf16, rows ldy elements
-// apart.  The GemmState (library handle, workspace, chosen algorithms)
-// belongs to one context.
+// (gemm.cpp: this library's MFMA kernel, gemm_mfma.hip, or hipBLASLt,
+// whichever the first call of a shape times faster); y is fp32 or, with
+// y_bf16, bf16, rows ldy elements apart.  The GemmState (library handle,
+// workspace, chosen kernels) belongs to one context.  HYMT_HIP_GEMM=mfma or
+// =hipblaslt, read when the state is created, fixes the choice.
 struct GemmState;
 GemmState *gemm_state_create();
 void gemm_state_destroy(GemmState *g);
 hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int k, const uint16_t *x, int m,
                      void *y, int ldy, bool y_bf16, bool accumulate);
+// the MFMA kernel alone (n a multiple of 128, k of 64, ldy of 4, 16-byte
+// aligned operands: gemm_mfma_fits)
+bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, const void *y, int ldy);
+hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,
+                          bool accumulate, hipStream_t s);
 
 }  // namespace hymt

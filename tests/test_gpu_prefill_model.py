@@ -273,13 +273,21 @@ def test_native_prefill_equals_composed_calls(be, n):
         m.prefill([1] * 200, n)  # past the capacity
 
 
-def test_deep_prefill_gate_up_rounding(be):
+@pytest.mark.parametrize("fused", [True, False])
+def test_deep_prefill_gate_up_rounding(be, fused):
     """The bf16 gate/up GEMM output (two extra bf16 roundings per FFN element
-    against the reference's fp32 _pfGu, VulkanBackend.cs:595,604) over a
-    6-layer model: logits of both forms within the prefill bound of the
-    oracle's fp32/double decode steps; their distances are printed."""
+    against the reference's fp32 _pfGu, VulkanBackend.cs:595,604) and the
+    fp32 one over a 6-layer model, with gate and up as one [gate; up] weight
+    (one GEMM) or, of different types, as two: logits of both forms within
+    the prefill bound of the oracle's fp32/double decode steps; their
+    distances are printed."""
     cfg = ModelConfig(num_layers=6, vocab_size=512)
     t = S.random_model(12, cfg, {"attn": N.W_Q4_K, "ffn": N.W_Q4_K, "embd": N.W_Q6_K, "out": N.W_Q6_K})
+    if not fused:
+        for l in range(cfg.num_layers):
+            name = f"blk.{l}.ffn_up.weight"
+            r, c = t[name].rows, t[name].cols
+            t[name] = Tensor(N.W_Q8_0, r, c, S.random_weight(300 + l, N.W_Q8_0, r, c))
     toks = [int(x) for x in np.random.default_rng(12).integers(0, cfg.vocab_size, 24)]
     om = OracleModel(cfg, t, 64, N.BF16)
     ref = om.forward(toks, 0)
@@ -291,6 +299,6 @@ def test_deep_prefill_gate_up_rounding(be):
         be.sync()
         got = _read_logits(be, m)
         errs[f32] = np.max(np.abs(got - ref)) / np.max(np.abs(ref))
-    print(f"6-layer prefill logits rel: bf16 gate/up {errs[False]:.2e}, fp32 gate/up {errs[True]:.2e}",
+    print(f"6-layer prefill logits rel (fused {fused}): flag off {errs[False]:.2e}, flag on {errs[True]:.2e}",
           flush=True)
     assert errs[False] <= PREFILL_BOUND and errs[True] <= PREFILL_BOUND
