@@ -520,7 +520,9 @@ def measure_ceilings():
     """Ceilings measured on this GPU (libhymt_ceilings.so, HIP events): the
     cost of a dependent launch, the time to stream the decode call's bytes
     (and a 32k-context layer's, and 1 GiB) from HBM with the decode kernel's
-    access pattern, the dense bf16 MFMA rate and the LDS read rate."""
+    access pattern, the dispatch-stamped duration of an empty kernel and of
+    that stream read (the floor under the per-kernel durations reported
+    here), the dense bf16 MFMA rate and the LDS read rate."""
     from hymt2sharp_amd import build as B
     L = ctypes.CDLL(B.CEIL_LIB)
     d = ctypes.c_double()
@@ -548,6 +550,15 @@ def measure_ceilings():
             row[f"{4 * per}k_workgroups"] = i.value
         stream[label] = row
     out["stream_read"] = stream
+    # the floor under a kernel duration as the timing mode and rocprofv3 stamp
+    # it: a kernel timed by itself pays the wake of an idle queue
+    disp = {}
+    L.hc_dispatch_duration.argtypes = [ctypes.c_int, ctypes.c_size_t, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    for kind, label, nbytes in ((0, "empty", 0), (1, "stream_config2_layer", decode_bytes_per_layer(CTX + 1))):
+        for iso, name in ((1, "isolated"), (0, "back_to_back")):
+            ck(L.hc_dispatch_duration(kind, nbytes, iso, ctypes.byref(d)))
+            disp[f"{label}_us_{name}"] = round(d.value, 3)
+    out["dispatch_stamped"] = disp
     mf = {}
     for w in (1, 2, 4):
         ck(L.hc_mfma_bf16(w, ctypes.byref(d)))
@@ -563,7 +574,9 @@ def measure_ceilings():
     out["device"] = {"cus": cu.value, "clock_mhz": clk.value // 1000, "mem_clock_mhz": mclk.value // 1000,
                      "bus_bits": bus.value}
     out["note"] = ("per-launch times of back-to-back launches on one stream: a graph of them replayed, "
-                   "or enqueued one by one; stream reads rotate over > 1 GiB of buffers")
+                   "or enqueued one by one; stream reads rotate over > 1 GiB of buffers; dispatch_stamped: "
+                   "start-to-end event stamps of one kernel (the timing mode's and rocprofv3's kernel "
+                   "duration), launched alone on a drained stream or back to back")
     return out
 
 
@@ -810,6 +823,16 @@ def main():
                                         "frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
                                         "what": "one whole decode call (both launches and the gap "
                                                 "between them) in the recorded step"}}
+            disp = (extra.get("ceilings") or {}).get("dispatch_stamped")
+            if disp:
+                # the same stamps around an empty kernel and around a kernel
+                # that only streams this call's bytes: the floor of avg_us
+                st = disp["stream_config2_layer_us_isolated"]
+                rec["roofline"]["measurement_floor"] = {
+                    "empty_kernel_us": disp["empty_us_isolated"], "stream_same_bytes_us": st,
+                    "stream_over_kernel": round(st / kd["avg_us"], 3),
+                    "what": "dispatch-stamped durations (the stamps avg_us uses) of an empty kernel and of a "
+                            "kernel streaming the call's 8.4 MB with the decode pattern, each timed alone"}
     if pre:
         rec["prefill"] = {"workload": "config 3: causal prefill 2048 tokens, one layer, bf16 in, "
                                       "bf16 MFMA fp32 acc, empty cache",

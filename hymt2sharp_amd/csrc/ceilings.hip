@@ -6,6 +6,7 @@
 // of the attention path's C ABI.  Every function allocates what it times,
 // times it with HIP events on its own stream and frees it; all return 0 on
 // success or the hipError_t of the first failing call.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -197,6 +198,58 @@ int hc_stream_read(size_t bytes, int per_thread, int graph, double *us, int *wgs
     if (sink) (void)hipFree(sink);
     if (rc) return rc;
     *wgs = nwg;
+    return 0;
+}
+
+// Dispatch-stamped duration (hipExtLaunchKernelGGL's start/stop events, what
+// the library's timing mode and rocprofv3's kernel trace report) of an empty
+// one-wave kernel (kind 0) or of a kernel streaming `bytes` from HBM with the
+// decode kernel's pattern (kind 1, 16 KiB per workgroup, a fresh buffer per
+// launch), averaged over 64 launches, each alone on the stream (isolated:
+// the stream drained before it, as in a call timed by itself) or back to
+// back.  Microseconds.
+int hc_dispatch_duration(int kind, size_t bytes, int isolated, double *us) {
+    constexpr int kN = 64, kPer = 4;
+    const size_t WG_BYTES = (size_t)256 * kPer * 16;
+    const int nwg = kind ? (int)((bytes + WG_BYTES - 1) / WG_BYTES) : 1;
+    Timer t;
+    if (int e = t.init()) return e;
+    std::vector<void *> bufs(kind ? kN : 0, nullptr);
+    std::vector<hipEvent_t> ev(2 * kN, nullptr);
+    uint32_t *sink = nullptr;
+    int rc = (int)hipMalloc((void **)&sink, (size_t)nwg * 4);
+    for (size_t i = 0; i < bufs.size() && !rc; i++) {
+        rc = (int)hipMalloc(&bufs[i], (size_t)nwg * WG_BYTES);
+        if (!rc) rc = (int)hipMemsetAsync(bufs[i], (int)i & 0xff, (size_t)nwg * WG_BYTES, t.s);
+    }
+    for (int i = 0; i < 2 * kN && !rc; i++) rc = (int)hipEventCreate(&ev[i]);
+    if (!rc) rc = (int)hipStreamSynchronize(t.s);
+    for (int rep = 0; rep < 2 && !rc; rep++) {  // the first round warms up
+        for (int i = 0; i < kN && !rc; i++) {
+            if (isolated) rc = (int)hipStreamSynchronize(t.s);
+            if (rc) break;
+            if (kind)
+                hipExtLaunchKernelGGL(stream_kernel<kPer>, dim3(nwg), dim3(256), 0, t.s, ev[2 * i], ev[2 * i + 1], 0,
+                                      (const uint4 *)bufs[i], sink, 0x9e3779b9u);
+            else
+                hipExtLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, t.s, ev[2 * i], ev[2 * i + 1], 0, (int *)sink);
+            rc = (int)hipGetLastError();
+        }
+        if (!rc) rc = (int)hipStreamSynchronize(t.s);
+    }
+    double sum = 0.0;
+    for (int i = 0; i < kN && !rc; i++) {
+        float ms = 0.f;
+        rc = (int)hipEventElapsedTime(&ms, ev[2 * i], ev[2 * i + 1]);
+        sum += ms;
+    }
+    for (hipEvent_t e : ev)
+        if (e) (void)hipEventDestroy(e);
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    if (sink) (void)hipFree(sink);
+    if (rc) return rc;
+    *us = sum * 1e3 / kN;
     return 0;
 }
 
