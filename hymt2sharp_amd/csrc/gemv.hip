@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "ktimer.hpp"
 #include "weights.hpp"
@@ -401,7 +402,15 @@ __constant__ uint8_t kStqBook[32] = {
     0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68,
 };
 
-template <typename Unit, bool STQ, int NJ>
+// K = cols / 32 / lpr units per lane and the input mode are template
+// arguments: the loads then sit in straight-line code, so the wait before the
+// activations' arithmetic counts only the activation loads (a run-time loop
+// bound and mode made the compiler wait for every weight load there too, and
+// the RMSNorm, the LDS staging and its barriers ran after the weights had
+// landed: 0.7 us on the 12288 x 2048 gate/up GEMV).
+// MODE is the input mode: 0 x as given, 1 RMSNorm (kGemvInRmsNorm), 2
+// SwiGLU (kGemvInSwiGLU); each loads only the vectors it needs.
+template <typename Unit, bool STQ, int NJ, int K, int MODE>
 __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__restrict__ xg, float *__restrict__ y,
                                                    int lpr, int flags, const float *__restrict__ nw, float eps) {
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -409,8 +418,6 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     float *xs = smem + w.cols + w.cols / 16;  // [cols / 8]
     __shared__ uint8_t book[32];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int upr = w.cols / 32;
-    const int K = upr / lpr;  // units per lane, <= Unit::kMax
     // lane group gi computes row gi; with kGemvOutSwiGLU (W = [gate; up], F
     // rows each) the groups alternate gate row gi/2 and up row F + gi/2, so
     // that a row pair sits in neighbouring groups
@@ -428,30 +435,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     // all issued before anything waits.  Thread tid holds the 8 values
     // [8i, 8i+8) for i = tid + 256j, j < NJ = cols / 2048.
     constexpr int nj = NJ;
+    constexpr bool swiglu = MODE == 2, rms = MODE == 1;
     float4 xa[NJ], xb[NJ], ua[NJ], ub[NJ], ga[NJ], gb[NJ];
-    const bool swiglu = flags & kGemvInSwiGLU, rms = flags & kGemvInRmsNorm;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-        if (j < nj) {
-            const int i = tid + 256 * j;
-            xa[j] = ((const float4 *)xg)[2 * i];
-            xb[j] = ((const float4 *)xg)[2 * i + 1];
-            if (swiglu) {
-                ua[j] = ((const float4 *)(xg + w.cols))[2 * i];
-                ub[j] = ((const float4 *)(xg + w.cols))[2 * i + 1];
-            }
-            if (rms) {
-                ga[j] = ((const float4 *)nw)[2 * i];
-                gb[j] = ((const float4 *)nw)[2 * i + 1];
-            }
+        const int i = tid + 256 * j;
+        xa[j] = ((const float4 *)xg)[2 * i];
+        xb[j] = ((const float4 *)xg)[2 * i + 1];
+        if constexpr (swiglu) {
+            ua[j] = ((const float4 *)(xg + w.cols))[2 * i];
+            ub[j] = ((const float4 *)(xg + w.cols))[2 * i + 1];
+        }
+        if constexpr (rms) {
+            ga[j] = ((const float4 *)nw)[2 * i];
+            gb[j] = ((const float4 *)nw)[2 * i + 1];
         }
     }
-    constexpr int kMaxK = Unit::kMax;
-    Unit un[kMaxK];
+    Unit un[K];
     const int rl = gi < w.rows ? row : w.rows - 1;
 #pragma unroll
-    for (int k = 0; k < kMaxK; k++)
-        if (k < K) un[k].load(w, rl, sub + 8 * (lpr8 * k));
+    for (int k = 0; k < K; k++) un[k].load(w, rl, sub + 8 * (lpr8 * k));
+    // nothing moves across: left free, the scheduler put the RMSNorm's sum
+    // of squares (and with it a wait for x) before the weight loads
+    __builtin_amdgcn_sched_barrier(0);
     if (STQ && tid < 32) book[tid] = kStqBook[tid];
     // 2. x as the input mode makes it, into LDS with its 8-value sums
     auto silu_mul = [](float4 g, float4 u) {
@@ -459,7 +465,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
         return make_float4(g.x / (1.f + expf(-g.x)) * u.x, g.y / (1.f + expf(-g.y)) * u.y,
                            g.z / (1.f + expf(-g.z)) * u.z, g.w / (1.f + expf(-g.w)) * u.w);
     };
-    if (swiglu) {
+    if constexpr (swiglu) {
 #pragma unroll
         for (int j = 0; j < NJ; j++)
             if (j < nj) {
@@ -467,7 +473,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
                 xb[j] = silu_mul(xb[j], ub[j]);
             }
     }
-    if (rms) {
+    if constexpr (rms) {
         // x / sqrt(mean(x^2) + eps) * nw (Ops.RmsNorm, Ops.cs:12-90)
         __shared__ float red[4];
         float ss = 0.f;
@@ -504,11 +510,9 @@ __global__ __launch_bounds__(256) void gemv_kernel(WeightDev w, const float *__r
     // 3. dot products, then the row's sum over its lane group
     float part = 0.f;
 #pragma unroll
-    for (int k = 0; k < kMaxK; k++) {
-        if (k < K) {
-            if constexpr (STQ) part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs, book);
-            else part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs);
-        }
+    for (int k = 0; k < K; k++) {
+        if constexpr (STQ) part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs, book);
+        else part += un[k].dot(w, 0, sub + 8 * (lpr8 * k), x, xs);
     }
     const float s = group_sum(part, lpr);
     if (out_swiglu) {
@@ -576,12 +580,39 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     const size_t lds = ((size_t)w.cols + w.cols / 16) * 4 + (size_t)w.cols / 8 * 4;
     const dim3 grid(blocks(lpr));
     KernelSpan span(gemv_span_name(w.type), s, true);
-    switch (w.cols / 2048) {
-    case 1: launch(span, gemv_kernel<Unit, STQ, 1>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    case 2: launch(span, gemv_kernel<Unit, STQ, 2>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    case 3: launch(span, gemv_kernel<Unit, STQ, 3>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    default: launch(span, gemv_kernel<Unit, STQ, 4>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw, eps); break;
-    }
+    const int K = upr / lpr;  // 64 NJ / lpr with lpr 8..64: a power of two, or 3 or 6 for NJ = 3
+    const int mode = (flags & kGemvInRmsNorm) ? 1 : (flags & kGemvInSwiGLU) ? 2 : 0;
+    bool ok = false;
+    auto go = [&](auto nj_tag, auto k_tag) {
+        constexpr int NJ = decltype(nj_tag)::value, KK = decltype(k_tag)::value;
+        if constexpr (KK <= Unit::kMax) {
+            if (w.cols / 2048 == NJ && K == KK) {
+                if (mode == 1)
+                    launch(span, gemv_kernel<Unit, STQ, NJ, KK, 1>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw,
+                           eps);
+                else if (mode == 2)
+                    launch(span, gemv_kernel<Unit, STQ, NJ, KK, 2>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw,
+                           eps);
+                else
+                    launch(span, gemv_kernel<Unit, STQ, NJ, KK, 0>, grid, dim3(256), lds, s, w, x, y, lpr, flags, nw,
+                           eps);
+                ok = true;
+            }
+        }
+    };
+    using std::integral_constant;
+    go(integral_constant<int, 1>{}, integral_constant<int, 1>{});
+    go(integral_constant<int, 1>{}, integral_constant<int, 2>{});
+    go(integral_constant<int, 1>{}, integral_constant<int, 4>{});
+    go(integral_constant<int, 1>{}, integral_constant<int, 8>{});
+    go(integral_constant<int, 2>{}, integral_constant<int, 2>{});
+    go(integral_constant<int, 2>{}, integral_constant<int, 4>{});
+    go(integral_constant<int, 2>{}, integral_constant<int, 8>{});
+    go(integral_constant<int, 3>{}, integral_constant<int, 3>{});
+    go(integral_constant<int, 3>{}, integral_constant<int, 6>{});
+    go(integral_constant<int, 4>{}, integral_constant<int, 4>{});
+    go(integral_constant<int, 4>{}, integral_constant<int, 8>{});
+    if (!ok) return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
