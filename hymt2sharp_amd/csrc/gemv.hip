@@ -173,6 +173,7 @@ struct UnitQ8_0 {
 // high nibbles at 64 g + 32 + 16 h + i (scale 2 g + 1).
 struct UnitQ4_K {
     static constexpr int kMax = 8;  // units in flight per lane
+    static constexpr int kGrid = 1024;  // workgroups the lane split aims for (see launch_t)
     uint4 hdr, qs;
     __device__ void load(const WeightDev &w, int r, int u) {
         const uint8_t *b = (const uint8_t *)w.q + ((size_t)r * (w.cols / 256) + (u >> 3)) * 144;
@@ -563,6 +564,13 @@ const char *gemv_span_name(int type) {
     }
 }
 
+template <typename U, typename = void> struct HasGrid : std::false_type {};
+template <typename U> struct HasGrid<U, std::void_t<decltype(U::kGrid)>> : std::true_type {};
+template <typename Unit> constexpr int unit_grid() {
+    if constexpr (HasGrid<Unit>::value) return Unit::kGrid;
+    else return 512;
+}
+
 template <typename Unit, bool STQ>
 hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, const float *nw, float eps,
                     hipStream_t s) {
@@ -570,13 +578,15 @@ hipError_t launch_t(const WeightDev &w, const float *x, float *y, int flags, con
     // a row's units must fit a wave; a thread stages at most 4 x 8 values of x
     if (w.cols % 2048 != 0 || w.cols > 8192 || upr > Unit::kMax * 64) return hipErrorInvalidValue;
     // lanes per row: the fewest (most units in flight per lane, K <= kMax), but
-    // more until the grid gives every CU two workgroups: the dequantising
-    // arithmetic is then spread over twice the waves (the 12288-row gate|up
-    // GEMV: 8.6 -> 7.0 us going from 384 to 768 workgroups; 1536 was slower)
+    // more until the grid has kGrid workgroups (512 unless the unit says
+    // otherwise): the dequantising arithmetic is then spread over more waves.
+    // Measured on the 32-layer decode step: Q4_K at 1024 (gate|up with 1536
+    // workgroups of 2 units a lane) 0.935 -> 0.906 ms against 512; the other
+    // formats' gate|up GEMVs are a little slower at 1024.
     int lpr = 8;
     while (upr / lpr > Unit::kMax) lpr *= 2;
     auto blocks = [&](int l) { return (w.rows + 4 * (64 / l) - 1) / (4 * (64 / l)); };
-    while (lpr < 64 && blocks(lpr) < 512) lpr *= 2;
+    while (lpr < 64 && blocks(lpr) < unit_grid<Unit>()) lpr *= 2;
     const size_t lds = ((size_t)w.cols + w.cols / 16) * 4 + (size_t)w.cols / 8 * 4;
     const dim3 grid(blocks(lpr));
     KernelSpan span(gemv_span_name(w.type), s, true);
