@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "ktimer.hpp"
@@ -54,6 +55,49 @@ __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(const float *__restri
     }
 }
 
+// As rows_rmsnorm_kernel for rows of n <= 64 NJ float4s (n <= 4096): one
+// wave per RPW rows, 4 waves per workgroup.  Every load (the rows' float4s
+// and gamma's, gamma once for the RPW rows) is issued unconditionally before
+// the first use -- past the row end a lane reloads the last float4 and counts
+// nothing -- so the loads share one memory round trip; the row sum is a wave
+// reduction, no barrier.
+template <int NJ, int RPW>
+__global__ __launch_bounds__(256) void rows_rmsnorm_wave_kernel(const float *__restrict__ x, int m, int n,
+                                                                const float *__restrict__ w, float eps,
+                                                                uint16_t *__restrict__ out) {
+    const int lane = threadIdx.x & 63, n4 = n / 4;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+    float4 v[RPW][NJ], g[NJ];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        const float4 *xr = (const float4 *)(x + (size_t)min(row0 + r, m - 1) * n);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) v[r][j] = xr[min(lane + 64 * j, n4 - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; j++) g[j] = ((const float4 *)w)[min(lane + 64 * j, n4 - 1)];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            if (lane + 64 * j < n4)
+                ss += (v[r][j].x * v[r][j].x + v[r][j].y * v[r][j].y) + (v[r][j].z * v[r][j].z + v[r][j].w * v[r][j].w);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        const float rr = 1.0f / sqrtf(ss / (float)n + eps);
+        if (row0 + r >= m) continue;
+        uint2 *orow = (uint2 *)(out + (size_t)(row0 + r) * n);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int i = lane + 64 * j;
+            if (i < n4)
+                orow[i] = pack4(v[r][j].x * rr * g[j].x, v[r][j].y * rr * g[j].y, v[r][j].z * rr * g[j].z,
+                                v[r][j].w * rr * g[j].w);
+        }
+    }
+}
+
 // out[r][i] = g / (1 + exp(-g)) * u with g = gu[r][i], u = gu[r][n + i]
 // (Ops.SiLUMulRange, Ops.cs:1016-1052)
 __global__ __launch_bounds__(256) void rows_swiglu_kernel(const float *__restrict__ gu, int m, int n,
@@ -85,6 +129,39 @@ __global__ __launch_bounds__(256) void rows_swiglu_bf16_kernel(const uint16_t *_
     }
 }
 
+// silu(g) = g / (1 + e^-g) from the hardware's base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each): a few fp32 ulps from
+// the correctly rounded quotient, far inside the bf16 rounding of the result.
+// Large |g| behaves as the exact form: e^-g overflows to inf for g < -88 and
+// gives -0, and underflows to 0 for large g and gives g.
+__device__ __forceinline__ float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
+
+// As rows_swiglu_bf16_kernel with 16-byte accesses (8 values) when n is a
+// multiple of 8 and the buffers are 16-byte aligned, 32-bit index arithmetic
+// (m n / 8 < 2^31 is checked by the launcher) and silu_fast: the exact
+// quotient's exp and division were most of its time.
+__global__ __launch_bounds__(256) void rows_swiglu_bf16_x8_kernel(const uint16_t *__restrict__ gu, int m, int n,
+                                                                  uint16_t *__restrict__ out) {
+    const int n8 = n / 8, total = m * n8;
+    for (int e = blockIdx.x * 256 + threadIdx.x; e < total; e += gridDim.x * 256) {
+        const int r = e / n8, i = e - r * n8;
+        const uint4 gb = ((const uint4 *)(gu + (size_t)r * 2 * n))[i];
+        const uint4 ub = ((const uint4 *)(gu + (size_t)r * 2 * n + n))[i];
+        const uint32_t gw[4] = {gb.x, gb.y, gb.z, gb.w};
+        const uint32_t uw[4] = {ub.x, ub.y, ub.z, ub.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float g0 = bf16_to_f32(gw[k] & 0xFFFF), g1 = bf16_to_f32(gw[k] >> 16);
+            const float u0 = bf16_to_f32(uw[k] & 0xFFFF), u1 = bf16_to_f32(uw[k] >> 16);
+            o[k] = (uint32_t)f32_to_bf16(silu_fast(g0) * u0) | ((uint32_t)f32_to_bf16(silu_fast(g1) * u1) << 16);
+        }
+        ((uint4 *)(out + (size_t)r * n))[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 __global__ __launch_bounds__(256) void to_bf16_kernel(const float *__restrict__ x, size_t n4,
                                                       uint16_t *__restrict__ out) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256) {
@@ -105,7 +182,20 @@ hipError_t launch_rows_rmsnorm(const float *x, int m, int n, const float *w, flo
     if (n % 4 != 0 || n > 8192 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     KernelSpan span("rows_rmsnorm", s, true);
-    launch(span, rows_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, n, w, eps, out);
+    const int nj = (n / 4 + 63) / 64;  // float4s per lane with a wave per row
+    auto wave_rows = [&](auto nj_tag, auto rpw_tag) {
+        constexpr int NJ = decltype(nj_tag)::value, RPW = decltype(rpw_tag)::value;
+        const unsigned blocks = (unsigned)((m + 4 * RPW - 1) / (4 * RPW));
+        launch(span, rows_rmsnorm_wave_kernel<NJ, RPW>, dim3(blocks), dim3(256), 0, s, x, m, n, w, eps, out);
+    };
+    using I = std::integral_constant<int, 1>;
+    using II = std::integral_constant<int, 2>;
+    if (nj <= 1) wave_rows(std::integral_constant<int, 1>{}, II{});
+    else if (nj <= 2) wave_rows(std::integral_constant<int, 2>{}, II{});
+    else if (nj <= 4) wave_rows(std::integral_constant<int, 4>{}, II{});
+    else if (nj <= 8) wave_rows(std::integral_constant<int, 8>{}, II{});
+    else if (nj <= 16) wave_rows(std::integral_constant<int, 16>{}, I{});
+    else launch(span, rows_rmsnorm_kernel, dim3(m), dim3(256), 0, s, x, n, w, eps, out);
     return hipGetLastError();
 }
 
@@ -121,7 +211,10 @@ hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *o
     if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     KernelSpan span("rows_swiglu_bf16", s, true);
-    launch(span, rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
+    if (n % 8 == 0 && ((uintptr_t)gu & 15u) == 0 && ((uintptr_t)out & 15u) == 0 && (size_t)m * (n / 8) < (1u << 31))
+        launch(span, rows_swiglu_bf16_x8_kernel, dim3(grid_for((size_t)m * n / 8)), dim3(256), 0, s, gu, m, n, out);
+    else
+        launch(span, rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
     return hipGetLastError();
 }
 

@@ -92,6 +92,65 @@ def test_rows_rmsnorm_swiglu_and_rounding(be):
         be.free(p)
 
 
+@pytest.mark.parametrize("m,n", [
+    (1, 4),        # one float4: a wave per row, lanes past the row reload it
+    (9, 1000),     # 250 float4s: the last wave column partly empty; ragged row count
+    (37, 2048),    # the model's rows
+    (8, 4096),     # a wave per row, 16 float4s per lane
+    (5, 4100),     # past 4096: a workgroup per row
+    (3, 8192),
+])
+def test_rows_rmsnorm_shapes(be, m, n):
+    """Every row-length class of hymt_rows_rmsnorm against the oracle's
+    RMSNorm, rounded to bf16: within one bf16 ulp (the sum order differs)."""
+    rng = np.random.default_rng(m * 10007 + n)
+    x = (rng.standard_normal((m, n)) * 2).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    dx, dw, do = dev(be, x), dev(be, w), be.alloc(m * n * 2 + 64)
+    be.upload(do, np.full(m * n + 32, 0x7FC1, np.uint16))  # a canary past the rows
+    be.rows_rmsnorm(dx, m, n, dw, 1e-5, do)
+    be.sync()
+    got = be.download(np.empty(m * n + 32, np.uint16), do)
+    ref = bf16_bits(O.rmsnorm(x, w, 1e-5)).reshape(m, n)
+    assert ulp_diff(got[:m * n].reshape(m, n), ref).max() <= 1
+    assert np.all(got[m * n:] == 0x7FC1)
+    for p in (dx, dw, do):
+        be.free(p)
+
+
+@pytest.mark.parametrize("m,F,offset,scale", [
+    (37, 6144, 0, 4.0),   # 16-byte path, the model's width
+    (3, 520, 0, 4.0),     # 16-byte path, rows that end mid-workgroup
+    (6, 1024, 0, 12.0),   # 16-byte path, gates to about +-50, plus the extremes below
+    (5, 1004, 0, 4.0),    # F not a multiple of 8: the 8-byte kernel
+    (4, 6144, 8, 4.0),    # input 8 bytes off 16-byte alignment: the 8-byte kernel
+])
+def test_rows_swiglu_bf16_paths(be, m, F, offset, scale):
+    """Both SwiGLU kernels over a bf16 gate/up against the float64 form
+    rounded to bf16: within one bf16 ulp."""
+    rng = np.random.default_rng(F + m)
+    gu = (rng.standard_normal((m, 2 * F)) * scale).astype(np.float32)
+    # gates where e^-g overflows fp32 (result -0 * u) or vanishes (result g u)
+    gu[0, :6] = [-200.0, -100.0, -90.0, 90.0, 100.0, 200.0]
+    gu[0, F:F + 6] = 1.0
+    gub = bf16_bits(gu).reshape(m, 2 * F)
+    base = be.alloc(gub.nbytes + 64)
+    be.upload(base + offset, gub)
+    dact = be.alloc(m * F * 2 + 64)
+    be.upload(dact, np.full(m * F + 32, 0x7FC1, np.uint16))
+    be.rows_swiglu_bf16(base + offset, m, F, dact)
+    be.sync()
+    got = be.download(np.empty(m * F + 32, np.uint16), dact)
+    gv = bf16_val(gub)
+    g, u = gv[:, :F], gv[:, F:]
+    with np.errstate(over="ignore"):  # fp32 semantics: e^-g = inf gives -0
+        ref = bf16_bits(g / (np.float32(1) + np.exp(-g)) * u).reshape(m, F)
+    assert ulp_diff(got[:m * F].reshape(m, F), ref).max() <= 1
+    assert np.all(got[m * F:] == 0x7FC1)
+    be.free(base)
+    be.free(dact)
+
+
 @pytest.mark.parametrize("wtype", [N.W_Q4_K, N.W_Q6_K, N.W_Q8_0, N.W_Q2_0C, N.W_STQ1_0, N.W_F16])
 def test_dense_copy_and_embed_rows(be, wtype):
     rows, cols = 300, 2048
