@@ -110,8 +110,8 @@ struct FlashArgs {
     const int32_t *tab;
     const void *kpool, *vpool;
     float *out;         // [seq][Hq*D], fp32, or bf16 bits (RNE) when out_bf16
-    float *part_o;      // [Hkv*items][G][32][D]  (split items only)
-    float *part_ml;     // [Hkv*items][G][32][2]
+    void *part_o;       // [Hkv*items][G][32][D] O / l in the cache type (split items only)
+    float *part_ml;     // [Hkv*items][G][32][2] (m, l)
     int pos0, seq;
     int heads, kv_heads;
     int rope_half, rope_dim;  // rope_dim in {0, 64, 128}
@@ -150,7 +150,7 @@ hipError_t decode_scratch_init(int device);
 hipError_t decode_scratch(int device, float **part_ml, float **part_acc, int *max_heads);
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s);
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s);
-hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s);
+hipError_t launch_prefill_merge(int kv_dtype, const FlashArgs &a, hipStream_t s);
 hipError_t launch_tab_update(int32_t *tab, const int *idx, const int *val, int n, hipStream_t s);
 hipError_t launch_kv_copy_page(void *kpool, void *vpool, size_t layer_bytes, size_t page_bytes, int src,
                                int dst, int layers, hipStream_t s);

@@ -736,15 +736,17 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         f.items_per_kvh = items;
         if (split) {
             const size_t slots = (size_t)c->kv_heads * items;
-            if (c->capturing && slots * kGroup * 32 * D * 4 > c->part_o.bytes)
+            // partial O / l in the 16-bit cache type, (m, l) in fp32
+            if (c->capturing &&
+                (slots * kGroup * 32 * D * 2 > c->part_o.bytes || slots * kGroup * 32 * 2 * 4 > c->part_ml.bytes))
                 return fail_capture(c, "prefill workspace growth");
-            c->part_o.reserve(slots * kGroup * 32 * D * 4);
+            c->part_o.reserve(slots * kGroup * 32 * D * 2);
             c->part_ml.reserve(slots * kGroup * 32 * 2 * 4);
         }
-        f.part_o = (float *)c->part_o.p;
+        f.part_o = c->part_o.p;
         f.part_ml = (float *)c->part_ml.p;
         HIP_TRY(launch_prefill_flash(c->kv_dtype, f, items * c->kv_heads, c->stream));
-        if (split) HIP_TRY(launch_prefill_merge(f, c->stream));
+        if (split) HIP_TRY(launch_prefill_merge(c->kv_dtype, f, c->stream));
         if (!dev) stage_out(c, c->out_o.p, out, qn * 4);
     } catch (const HipError &e) {
         return map_hip(e);

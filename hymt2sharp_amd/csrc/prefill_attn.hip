@@ -818,15 +818,18 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
             }
         }
     } else {
+        // split item: O / l rounded to the operand type (the weights sum to 1,
+        // so |O / l| <= max |V| fits it), and (m, l) in fp32 for the merge
         const size_t slot = (size_t)kvh * a.items_per_kvh + item_idx;
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
             const int r = qq * 16 + c;
-            float *po = a.part_o + ((slot * G + hw) * 32 + r) * D + grp * 4;
+            const float inv = lrun[qq] > 0.f ? 1.0f / lrun[qq] : 0.f;
+            uint16_t *po = (uint16_t *)a.part_o + ((slot * G + hw) * 32 + r) * D + grp * 4;
 #pragma unroll
             for (int db = 0; db < 8; db++) {
-                f32x4 v = o[db][qq];
-                *(float4 *)(po + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
+                const f32x4 v = o[db][qq] * inv;
+                *(uint2 *)(po + db * 16) = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
             }
             if (grp == 0) {
                 float *pm = a.part_ml + ((slot * G + hw) * 32 + r) * 2;
@@ -862,8 +865,10 @@ hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_item
 // ------------------------------------------------------------------ merge
 // Combine the split items of a block pair: one workgroup per (pair, kv head,
 // head in group, 8-row quarter of the pair's 32 rows); thread -> (row, 4
-// dims).  All (m, l) of the row are read first, then the partial O rows
-// stream with up to 8 loads in flight per thread.
+// dims).  All (m, l) of the row are read first, then the partial rows
+// O_s / l_s (type T) stream with up to 8 loads in flight per thread:
+// out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s, w_s = 2^(m_s - max m).
+template <typename T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, G = kGroup;
     int b = blockIdx.x;
@@ -885,7 +890,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     const int d = (threadIdx.x % 32) * 4;
     const size_t slot0 = (size_t)kvh * a.items_per_kvh + first;
     const float *pm = a.part_ml + ((slot0 * G + g) * 32 + r) * 2;
-    const float *po = a.part_o + ((slot0 * G + g) * 32 + r) * D + d;
+    const uint16_t *po = (const uint16_t *)a.part_o + ((slot0 * G + g) * 32 + r) * D + d;
     const size_t ml_stride = (size_t)G * 32 * 2, o_stride = (size_t)G * 32 * D;
     float M = -INFINITY;
     for (int s = 0; s < ns; s++) M = fmaxf(M, pm[s * ml_stride]);
@@ -893,13 +898,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     float Ls = 0.f;
 #pragma unroll 8
     for (int s = 0; s < ns; s++) {
-        const float w = exp2f(pm[s * ml_stride] - M);
-        Ls = fmaf(w, pm[s * ml_stride + 1], Ls);
-        const float4 v = *(const float4 *)(po + s * o_stride);
-        acc.x = fmaf(w, v.x, acc.x);
-        acc.y = fmaf(w, v.y, acc.y);
-        acc.z = fmaf(w, v.z, acc.z);
-        acc.w = fmaf(w, v.w, acc.w);
+        const float wl = exp2f(pm[s * ml_stride] - M) * pm[s * ml_stride + 1];
+        Ls += wl;
+        const uint2 u = *(const uint2 *)(po + s * o_stride);
+        acc.x = fmaf(wl, from_elem<T>((uint16_t)(u.x & 0xFFFF)), acc.x);
+        acc.y = fmaf(wl, from_elem<T>((uint16_t)(u.x >> 16)), acc.y);
+        acc.z = fmaf(wl, from_elem<T>((uint16_t)(u.y & 0xFFFF)), acc.z);
+        acc.w = fmaf(wl, from_elem<T>((uint16_t)(u.y >> 16)), acc.w);
     }
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const size_t off = (size_t)row * a.heads * D + (size_t)(kvh * G + g) * D + d;
@@ -911,9 +916,14 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
         *(float4 *)(a.out + off) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
-hipError_t launch_prefill_merge(const FlashArgs &a, hipStream_t s) {
+hipError_t launch_prefill_merge(int kv_dtype, const FlashArgs &a, hipStream_t s) {
     KernelSpan span("prefill_merge", s, true);
-    launch(span, prefill_merge_kernel, dim3(a.npairs * a.kv_heads * kGroup * 4), dim3(256), 0, s, a);
+    const dim3 grid(a.npairs * a.kv_heads * kGroup * 4);
+    switch (kv_dtype) {
+    case 1: launch(span, prefill_merge_kernel<F16>, grid, dim3(256), 0, s, a); break;
+    case 2: launch(span, prefill_merge_kernel<BF16>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

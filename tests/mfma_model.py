@@ -19,7 +19,8 @@ fp32 reference in its roundings and its order of accumulation only:
 * the tiles of a work item alternate between two wave halves (even and odd
   tile offsets), each with its own (m, l, O), combined with weights
   2^(m_i - max m); work items that split a pair's kv range are combined
-  the same way.
+  the same way, each split item's O / l rounded to the operand type first
+  (the partials are stored in it) and weighted by its l.
 
 This model reproduces those steps in fp64 so the GPU result can be checked
 far tighter than against the fp32 oracle.  Test infrastructure only.
@@ -135,6 +136,9 @@ def prefill_model(q_hat, cache_k, cache_v, heads, kv_heads, head_dim, pos0, seq,
                 halves = [_half_softmax(s_all[rows], vis[rows], range(t0 + hp, t1, 2), L,
                                         V[:, kvh, :], dtype) for hp in (0, 1)]
                 items.append(_combine(halves))
+            if len(items) > 1:  # partials stored as O / l in the operand type
+                items = [(mi, li, li[:, None] * round_to(np.where(li[:, None] > 0, oi / np.where(li > 0, li, 1)[:, None], 0),
+                                                         dtype)) for mi, li, oi in items]
             m, l, o = items[0] if len(items) == 1 else _combine(items)
             out[rows, h, :] = np.where(l[:, None] > 0, o / np.where(l > 0, l, 1)[:, None], 0)
     return out.reshape(seq, heads * D)
