@@ -139,9 +139,10 @@ __device__ __forceinline__ float silu_fast(float g) {
 }
 
 // As rows_swiglu_bf16_kernel with 16-byte accesses (8 values) when n is a
-// multiple of 8 and the buffers are 16-byte aligned, 32-bit index arithmetic
-// (m n / 8 < 2^31 is checked by the launcher) and silu_fast: the exact
-// quotient's exp and division were most of its time.
+// multiple of 8 and the buffers are 16-byte aligned, with 32-bit index
+// arithmetic (the launcher checks m n / 8 <= 2^30, so e plus the grid stride
+// stays below 2^31) and silu_fast: the exact quotient's exp and division were
+// most of its time.
 __global__ __launch_bounds__(256) void rows_swiglu_bf16_x8_kernel(const uint16_t *__restrict__ gu, int m, int n,
                                                                   uint16_t *__restrict__ out) {
     const int n8 = n / 8, total = m * n8;
@@ -185,7 +186,7 @@ hipError_t launch_rows_rmsnorm(const float *x, int m, int n, const float *w, flo
     const int nj = (n / 4 + 63) / 64;  // float4s per lane with a wave per row
     auto wave_rows = [&](auto nj_tag, auto rpw_tag) {
         constexpr int NJ = decltype(nj_tag)::value, RPW = decltype(rpw_tag)::value;
-        const unsigned blocks = (unsigned)((m + 4 * RPW - 1) / (4 * RPW));
+        const unsigned blocks = (unsigned)(((size_t)m + 4 * RPW - 1) / (4 * RPW));
         launch(span, rows_rmsnorm_wave_kernel<NJ, RPW>, dim3(blocks), dim3(256), 0, s, x, m, n, w, eps, out);
     };
     using I = std::integral_constant<int, 1>;
@@ -211,7 +212,7 @@ hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *o
     if (n % 4 != 0 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     KernelSpan span("rows_swiglu_bf16", s, true);
-    if (n % 8 == 0 && ((uintptr_t)gu & 15u) == 0 && ((uintptr_t)out & 15u) == 0 && (size_t)m * (n / 8) < (1u << 31))
+    if (n % 8 == 0 && ((uintptr_t)gu & 15u) == 0 && ((uintptr_t)out & 15u) == 0 && (size_t)m * (n / 8) <= (1u << 30))
         launch(span, rows_swiglu_bf16_x8_kernel, dim3(grid_for((size_t)m * n / 8)), dim3(256), 0, s, gu, m, n, out);
     else
         launch(span, rows_swiglu_bf16_kernel, dim3(grid_for((size_t)m * n / 4)), dim3(256), 0, s, gu, m, n, out);
