@@ -4,6 +4,7 @@ libhymt_hip.so      C ABI (include/hymt_hip.h) + gfx950 kernels, via hipcc
 libhymt_synth.so    seeded input generator (plain C), via gcc
 libhymt_ceilings.so the benchmark's measured ceilings (launch gap, HBM stream
                     read, MFMA and LDS rates), via hipcc
+tests/c/abi_host    a plain C host of the C ABI (tests/test_c_host.py), via gcc
 _san/               ASan/UBSan builds of the host-side code (build_san.py)
 
 Run `python -m hymt2sharp_amd.build` or call build_all().
@@ -93,10 +94,26 @@ def build_synth():
     return SYNTH_LIB
 
 
+C_HOST_SRC = os.path.join(ROOT, "tests", "c", "abi_host.c")
+C_HOST = os.path.join(ROOT, "tests", "c", "abi_host")
+
+
+def build_c_host():
+    """The plain C host of the C ABI that tests/test_c_host.py runs: gcc,
+    include/hymt_hip.h, linked to libhymt_hip.so by a path relative to the
+    binary (so the copy on a GPU box finds the library beside it)."""
+    tmp = C_HOST + ".tmp"
+    _run(["gcc", "-O2", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), C_HOST_SRC,
+          "-L", PKG, "-lhymt_hip", "-Wl,-rpath,$ORIGIN/../../hymt2sharp_amd", "-o", tmp])
+    os.replace(tmp, C_HOST)
+    return C_HOST
+
+
 def build_all():
     build_synth()
     build_ceilings()
     build_hip()
+    build_c_host()
     # ASan/UBSan builds of the host-side code for the CPU tests (host only;
     # they reuse the kernel objects just built)
     from . import build_san
