@@ -360,7 +360,7 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
     wbytes = sum(len(x.data) for n, x in t.items() if n != "token_embd.weight") + \
         len(emb.data) // emb.rows
     kvbytes = cfg.num_layers * decode_bytes_per_layer(ctx + 1, 4 if kv_dtype == F32 else 2)
-    cpu = None
+    cpu = model_cpu = None
     if cpu_tokens:
         # the oracle's decode step (C restatement, one thread, double sums) on
         # the same weights at the same position; the cache rows are zeros,
@@ -378,6 +378,31 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
                "sample": f"{cpu_tokens} decode steps of the same model at position {ctx} after one "
                          f"warm-up ({sec:.2f} s per token), oracle/model.py over the C "
                          f"restatement (oracle/hymt_quant.c, oracle/hymt_oracle.c)"}
+        # the reference's CPU decode path restated (oracle/cpu_decode.c:
+        # projections over Q8_K activations with AVX2 integer dots, the
+        # reference's bf16 cache, rows over threads): the model leg's CPU
+        # baseline, on min(cores, 16) threads and on one
+        from oracle import oracle as OR
+        from oracle.model import CpuDecodePort
+        port = CpuDecodePort(cfg, t, ctx + 1, OR.BF16)
+        nthr = cpu_threads()
+        port.step(4242, ctx, nthr)
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            port.step(4242, ctx, nthr)
+        sec_n = (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        for _ in range(2):
+            port.step(4242, ctx, 1)
+        sec_1 = (time.perf_counter() - t0) / 2
+        del port
+        model_cpu = {"value": round(1.0 / sec_n, 3), "unit": "tokens/s", "cores": nthr, "kind": "port",
+                     "sample": f"{reps} decode steps at position {ctx} after one warm-up ({sec_n * 1e3:.1f} ms per "
+                               f"token), oracle/cpu_decode.c: the reference's CPU decode step (Q8_K activations, "
+                               f"Q4_K/Q6_K integer dots, bf16 cache), same weights",
+                     "single_thread": {"value": round(1.0 / sec_1, 3), "unit": "tokens/s", "cores": 1,
+                                       "sample": f"2 steps on one thread ({sec_1:.2f} s per token)"}}
     be = HipBackend(0)
     try:
         be.LoadModel(t, cfg, max_tokens=ctx + 1, kv_dtype=kv_dtype)
@@ -459,10 +484,11 @@ def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefi
                                   f"{prefill_reps}, chunks of 2048 rows",
                         "unseen_length": {"prompt_tokens": cold_len, "first_ms": round(cold_ms, 3),
                                           "again_ms": round(warm_ms, 3)}},
-            # The oracle's step is the correctness checker (scalar C, double
-            # sums), not the reference's CPU path (Q8_K activations + SIMD
-            # dots), so it is no CPU baseline; the reference's own CPU figure
-            # is quoted beside it.
+            # cpu_baseline is the reference's CPU path restated (Q8_K
+            # activations + SIMD dots); the oracle's step is the correctness
+            # checker (scalar C, double sums), reported for its speed only;
+            # the reference's own published CPU figure is quoted beside them.
+            "cpu_baseline": model_cpu,
             "oracle_checker_step": cpu,
             "reference_published_cpu": {
                 "decode_tokens_per_s": 26.55, "prefill_tokens_per_s": 423.99, "quant": "Q4_K_M",

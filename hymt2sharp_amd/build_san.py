@@ -7,7 +7,7 @@ hymt2sharp_amd/_san/libhymt_hip.so
     the kernel sources are linked from the normal build's objects (their device
     code is never instrumented).
 hymt2sharp_amd/_san/libhymt_oracle.so
-    The CPU oracle (oracle/hymt_oracle.c, hymt_quant.c), instrumented.
+    The CPU oracle (oracle/hymt_oracle.c, hymt_quant.c, cpu_decode.c), instrumented.
 hymt2sharp_amd/_san/runtime.txt
     The sanitizer runtime to preload into the Python that loads them.
 
@@ -81,7 +81,7 @@ def build_san_oracle():
     B._run([CLANG, "-O1", "-g", "-fPIC", "-std=c11", "-mavx2", "-mfma", "-mf16c", "-ffp-contract=off", "-fopenmp",
             "-Wall", "-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer",
             "-shared-libasan", "-shared", os.path.join(ORACLE_DIR, "hymt_oracle.c"),
-            os.path.join(ORACLE_DIR, "hymt_quant.c"), "-lm", "-L" + omp, "-Wl,-rpath," + omp, "-o", tmp])
+            os.path.join(ORACLE_DIR, "hymt_quant.c"), os.path.join(ORACLE_DIR, "cpu_decode.c"), "-lm", "-L" + omp, "-Wl,-rpath," + omp, "-o", tmp])
     os.replace(tmp, SAN_ORACLE_LIB)
 
 

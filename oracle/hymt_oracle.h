@@ -140,6 +140,38 @@ long orc_row_bytes(int type, int n);
 int orc_dequant_row(int type, const void *row, int n, float *y);
 int orc_gemv(int type, const void *w, int rows, int cols, const float *x, float *y, int accumulate);
 
+/*
+ * The reference's CPU decode step (cpu_decode.c): projections over Q8_K-
+ * quantized activations (Q8K.cs, VecDotQ4K.cs, Q6K.cs, KQuantGemv.cs) around
+ * orc_decode_attention, in the order of HunyuanDenseModel.Decode.cs:30-101.
+ * The CPU baseline bench.py times; pinned against orc_gemv and the fp64 model
+ * step within the Q8_K quantisation bound (tests/test_cpu_decode_port.py).
+ * Weights are GGUF blocks of Q4_K (12) or Q6_K (14); the cache is kv_dtype.
+ */
+typedef struct {
+    const void *wq, *wk, *wv, *wo, *wg, *wu, *wd;
+    int wq_type, wk_type, wv_type, wo_type, wg_type, wu_type, wd_type;
+    const float *attn_norm, *ffn_norm, *q_norm, *k_norm;
+    void *cache_k, *cache_v;  /* [cap][kv_heads*head_dim] */
+} orc_cpu_layer;
+
+typedef struct {
+    int layers, hidden, ffn, vocab, heads, kv_heads, head_dim, rope_dim, kv_dtype;
+    float eps, rope_base;
+    const void *embd;        /* token embedding, embd_type blocks */
+    int embd_type;
+    const void *out;         /* output projection (the embedding when tied) */
+    int out_type;
+    const float *out_norm;
+    const orc_cpu_layer *layer;
+} orc_cpu_model;
+
+/* y (+)= W . q8k(x) with W Q4_K or Q6_K, rows over `threads` threads */
+int orc_cpu_q8k_gemv(int type, const void *w, int rows, int cols, const float *x, float *y, int accumulate,
+                     int threads);
+/* one decode step at `pos` for `token`: logits[vocab]; appends to the caches */
+int orc_cpu_decode_step(const orc_cpu_model *m, int token, int pos, float *logits, int threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,8 @@ def _declare(L):
     L.orc_row_bytes.argtypes = [_i, _i]
     L.orc_dequant_row.argtypes = [_i, _vp, _i, _vp]
     L.orc_gemv.argtypes = [_i, _vp, _i, _i, _vp, _vp, _i]
+    L.orc_cpu_q8k_gemv.argtypes = [_i, _vp, _i, _i, _vp, _vp, _i, _i]
+    L.orc_cpu_decode_step.argtypes = [_vp, _i, _i, _vp, _i]
 
 
 def _p(a):
@@ -286,6 +288,18 @@ def dequant(wtype: int, data, rows: int, cols: int) -> np.ndarray:
     for r in range(rows):
         if lib().orc_dequant_row(wtype, _p(raw[r * rb:(r + 1) * rb]), cols, _p(out[r])) != 0:
             raise ValueError(wtype)
+    return out
+
+
+def q8k_gemv(wtype: int, data, rows: int, cols: int, x, y=None, threads: int = 1) -> np.ndarray:
+    """The reference's CPU projection (cpu_decode.c): x quantized to Q8_K,
+    integer dots against Q4_K / Q6_K blocks; y given: accumulate."""
+    raw = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8))
+    x = np.ascontiguousarray(x, np.float32)
+    acc = y is not None
+    out = np.array(y, np.float32, copy=True) if acc else np.empty(rows, np.float32)
+    if lib().orc_cpu_q8k_gemv(wtype, _p(raw), rows, cols, _p(x), _p(out), int(acc), threads) != 0:
+        raise ValueError(wtype)
     return out
 
 
