@@ -706,33 +706,39 @@ template <typename T, int PPW, bool RUNS, bool ARGS> DecodeKernel pick_full(bool
     return full ? decode_attn_mfma_kernel<T, PPW, RUNS, ARGS, true> : decode_attn_mfma_kernel<T, PPW, RUNS, ARGS, false>;
 }
 // Instances that launch_decode can reach: page lists in the arguments hold at
-// most kArgPages pages, taken one or two per split.
+// most kArgPages pages, taken one or two per split; splits of more than two
+// pages run them two at a time (one at a time for an odd count, so no run
+// reads a page only to mask it out).
 template <typename T> DecodeKernel pick_mfma(int ppw, bool args, bool full) {
     if (args) return ppw == 1 ? pick_full<T, 1, false, true>(full) : pick_full<T, 2, false, true>(full);
     switch (ppw) {
     case 1: return pick_full<T, 1, false, false>(full);
     case 2: return pick_full<T, 2, false, false>(full);
-    case 3: return pick_full<T, 3, false, false>(full);
-    case 4: return pick_full<T, 4, false, false>(full);
-    default: return pick_full<T, 4, true, false>(full);
+    default: return ppw % 2 == 0 ? pick_full<T, 2, true, false>(full) : pick_full<T, 1, true, false>(full);
     }
 }
 
 // Pages per split for `pages` cached pages (at most kMaxSplits splits).
-// Measured at 1k-32k positions: a page per split while there are at most 128
-// (4k positions: 64 workgroups per kv head), then two (fewer partials for
-// the merge to read: 13.7 against 16.1 us per call at 16k).
+// Measured at 1k-64k positions (fp16 cache, 4 kv heads): a page per split
+// while there are at most 128 (4k positions: 64 workgroups per kv head), then
+// two (fewer partials for the merge to read: 13.7 against 16.1 us per call at
+// 16k), then 128 splits of runs.  The kernel holds 216 registers (VGPR +
+// AGPR) per lane, so a SIMD runs two of its waves and the chip 512
+// workgroups at once: 128 splits per kv head fill it in one round, where
+// 2-page splits past 16k need a second (32k: 18.8 against 20.0 us per call;
+// 64k, against 4-page splits issued at once at one wave per SIMD: 29.8
+// against 38.2 us).
 int decode_pages_per_split(int pages) {
-    return pages <= 128 ? 1 : pages <= 2 * kMaxSplits ? 2 : (pages + kMaxSplits - 1) / kMaxSplits;
+    return pages <= 128 ? 1 : pages <= 256 ? 2 : (pages + 127) / 128;
 }
 
 hipError_t launch_decode(int kv_dtype, const DecodeArgs &args, hipStream_t s) {
     DecodeArgs a = args;
     // Work split: pages of the cached positions [0, L-1), the new token riding
-    // with the last split.  One page per split until the split count reaches
-    // kMaxSplits (the merge width, so up to 32768 positions take at most two
-    // pages per split); a split's pages are loaded PPW (<= 4) at a time, all
-    // issued at once.
+    // with the last split.  One or two pages per split up to 16k positions,
+    // all loads issued at once, then 128 splits whose pages are loaded in
+    // runs of PPW (2, or 1 for an odd count); the split count stays within
+    // kMaxSplits, the merge width.
     const int pages = (a.L - 1 + kPage - 1) / kPage;
     a.ppw = decode_pages_per_split(pages);
     a.nsplit = std::max(1, (pages + a.ppw - 1) / a.ppw);
