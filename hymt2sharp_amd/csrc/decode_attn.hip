@@ -11,8 +11,8 @@
 // MslDecodeKernels.cs:172-300, but over KV heads so that each K/V byte is read
 // from HBM once for all 4 q heads of its GQA group):
 //   workgroup = (split, kv head), 4 waves, `ppw` 64-position pages per split
-//   (one page per split until the split count reaches kMaxSplits, so a
-//   4k-context layer spreads over 256 workgroups, every CU).
+//   (one page per split up to 128 pages, so a 4k-context layer spreads over
+//   256 workgroups, every CU; past 256 pages, 128 splits per kv head).
 //   Wave w owns 16 positions of every page of its split: those of V chunks 2w
 //   and 2w+1 (f16/bf16 pages) or the sub-tile [16w, 16w+16) (f32 pages), so
 //   that its K and V operand loads are whole 128-byte segments.
@@ -222,27 +222,37 @@ template <typename S> struct PageOps {
     using VL = typename std::conditional<W4, uint4, uint2>::type;
     uint4 k[KL];
     VL v[8];
-    __device__ __forceinline__ void load(const S *kpool, const S *vpool, size_t pb, int wave, int grp, int c) {
+    __device__ __forceinline__ void load_k(const S *kpool, size_t pb, int wave, int grp, int c) {
         constexpr int D = kHeadDim, SUB = 16;
         if constexpr (W4) {
             const S *kp = kpool + pb + (size_t)(SUB * wave + c) * D + 8 * grp;
-            const S *vp = vpool + pb + (size_t)(wave * D + c) * SUB + 4 * grp;
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
                 k[2 * ks] = *(const uint4 *)(kp + 32 * ks);
                 k[2 * ks + 1] = *(const uint4 *)(kp + 32 * ks + 4);
             }
-#pragma unroll
-            for (int db = 0; db < 8; db++) v[db] = *(const VL *)(vp + 256 * db);
         } else {
             const S *kp = kpool + pb + 2048 * (2 * (wave >> 1) + ((c >> 2) & 1)) + 128 * grp +
                           8 * (8 * (wave & 1) + 4 * (c >> 3) + (c & 3));
-            const S *vp = vpool + pb + (size_t)(2 * wave + (grp >> 1)) * 1024 + 8 * c + 4 * (grp & 1);
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) k[ks] = *(const uint4 *)(kp + 512 * ks);
+        }
+    }
+    __device__ __forceinline__ void load_v(const S *vpool, size_t pb, int wave, int grp, int c) {
+        constexpr int D = kHeadDim, SUB = 16;
+        if constexpr (W4) {
+            const S *vp = vpool + pb + (size_t)(wave * D + c) * SUB + 4 * grp;
+#pragma unroll
+            for (int db = 0; db < 8; db++) v[db] = *(const VL *)(vp + 256 * db);
+        } else {
+            const S *vp = vpool + pb + (size_t)(2 * wave + (grp >> 1)) * 1024 + 8 * c + 4 * (grp & 1);
 #pragma unroll
             for (int db = 0; db < 8; db++) v[db] = *(const VL *)(vp + 128 * db);
         }
+    }
+    __device__ __forceinline__ void load(const S *kpool, const S *vpool, size_t pb, int wave, int grp, int c) {
+        load_k(kpool, pb, wave, grp, c);
+        load_v(vpool, pb, wave, grp, c);
     }
 };
 
@@ -257,7 +267,8 @@ template <typename S> struct PageOps {
 //     O += Pcat . V_sub, lane (grp, c) gets rows 4*grp + i of dims 16*db + c,
 //     rows 0-3 = hi(P) of the 4 heads, rows 4-7 = lo(P).
 //   A split of more than PPW pages runs its pages PPW at a time, merging the
-//   runs online.
+//   runs online; the next run's K loads are issued once this run's scores
+//   are in (its K registers are free), its V loads after this run's P.V.
 //   The new token (position pos) is one more position, handled in the last
 //   split on the VALU from registers while the K/V stream is in flight: wave
 //   w computes the new K row after RoPE + norm and V, both rounded to the
@@ -439,6 +450,15 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
                 else sc[p][i] = -INFINITY;
             }
         }
+        // the next run's K while this run's softmax and P.V proceed
+        size_t nb[PPW];
+        const bool more = RUNS && run0 + PPW < page_end;
+        if (more) {
+#pragma unroll
+            for (int p = 0; p < PPW; p++) nb[p] = page_base(tab_page(run0 + PPW + p));
+#pragma unroll
+            for (int p = 0; p < PPW; p++) pg[p].load_k(kpool, nb[p], wave, grp, c);
+        }
         mt = xrow32_max(xrow16_max(mt));
         const float mnew = fmaxf(m_run, mt);
         const float alpha = exp2f(m_run - mnew);
@@ -497,10 +517,10 @@ __global__ __launch_bounds__(256) void decode_attn_mfma_kernel(DecodeArgs a) {
                     acc[db] = M::pv(pa, make_uint2(pg[p].v[db].x & keep[0], pg[p].v[db].y & keep[1]), acc[db]);
             }
         }
-        // the next run's pages (splits of more than PPW pages)
-        if (RUNS && run0 + PPW < page_end) {
+        // the next run's V (splits of more than PPW pages)
+        if (more) {
 #pragma unroll
-            for (int p = 0; p < PPW; p++) pg[p].load(kpool, vpool, page_base(tab_page(run0 + PPW + p)), wave, grp, c);
+            for (int p = 0; p < PPW; p++) pg[p].load_v(vpool, nb[p], wave, grp, c);
         }
     }
 
