@@ -728,13 +728,20 @@ template <typename T, int PPW, bool RUNS, bool ARGS> DecodeKernel pick_full(bool
 // Instances that launch_decode can reach: page lists in the arguments hold at
 // most kArgPages pages, taken one or two per split; splits of more than two
 // pages run them two at a time (one at a time for an odd count, so no run
-// reads a page only to mask it out).
+// reads a page only to mask it out).  fp32 pages hold twice the K/V
+// registers: runs of two would take 252 + 32 registers per lane and leave a
+// SIMD one wave, so fp32 splits run one page at a time (32k positions: 30.0
+// against 31.2 us per call; 64k: 52.7 against 55.0).
 template <typename T> DecodeKernel pick_mfma(int ppw, bool args, bool full) {
     if (args) return ppw == 1 ? pick_full<T, 1, false, true>(full) : pick_full<T, 2, false, true>(full);
     switch (ppw) {
     case 1: return pick_full<T, 1, false, false>(full);
     case 2: return pick_full<T, 2, false, false>(full);
-    default: return ppw % 2 == 0 ? pick_full<T, 2, true, false>(full) : pick_full<T, 1, true, false>(full);
+    default:
+        if constexpr (sizeof(typename T::storage) == 2) {
+            if (ppw % 2 == 0) return pick_full<T, 2, true, false>(full);
+        }
+        return pick_full<T, 1, true, false>(full);
     }
 }
 

@@ -84,13 +84,14 @@ def test_config5_long_context_outliers(oracle, hip_available, L):
 
 
 @pytest.mark.parametrize("dtype,pos", [("f16", 20480), ("bf16", 24639), ("f32", 40000), ("f16", 65600),
-                                       ("bf16", 16448)])
+                                       ("bf16", 16448), ("f32", 32000)])
 def test_decode_page_runs(oracle, hip_available, dtype, pos):
     """Past 256 cached pages each split takes its pages in runs: 2 at a time
     for an even count per split (24639 -> 385 pages, 4 per split, the last
     split holding one), 1 at a time for an odd one (20480 -> 3 per split,
     65600 -> 9, the last split holding 8); 16448 (257 pages) is the first
-    context past the 2-page splits."""
+    context past the 2-page splits.  fp32 caches always take runs of one
+    (32000 -> 500 pages, 4 per split)."""
     dt = DT[dtype]
     got, ref, (kd, vd), (kr, vr) = run_case(oracle, dt, pos, "gamma", salt=pos)
     assert max_rel(got, ref) <= TOL, max_rel(got, ref)
