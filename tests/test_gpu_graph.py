@@ -32,8 +32,11 @@ def dev_inputs(be, arrays):
     return ptrs
 
 
-def test_recorded_decode_step_replays_exactly(hip_available):
-    layers, pos = 3, 700
+@pytest.mark.parametrize("pos", [700, 20480])
+def test_recorded_decode_step_replays_exactly(hip_available, pos):
+    """700: page ids in the kernel arguments; 20480: page ids from the
+    device table, splits taking their pages in runs."""
+    layers = 3
     be = backend(layers, pos + 1, F16)
     try:
         kb, vb = cache_rows(11, pos)
