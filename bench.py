@@ -24,7 +24,10 @@ launches on the backend's stream (a second pass over the same calls on a
 context's quiet timing mode, hymt_timing_enable); `roofline.call` prices the whole
 call (both launches) the same way; `traffic` is read from
 profiles/traffic.json (rocprofv3 FETCH_SIZE + WRITE_SIZE per call) when
-present.  `prefill` carries the prefill TFLOP/s with the flash kernel's MFMA
+present.  `decode.step_spread` / `prefill.call_spread` are the median and
+p10/p90 of 200 launches timed one by one after 20 untimed ones; after them
+the replayed step's first layer is compared bit for bit with an eager call
+on the same inputs (`decode.replay_vs_eager`).  `prefill` carries the prefill TFLOP/s with the flash kernel's MFMA
 roofline; `config1`, `config4` and `config5` are the other configurations;
 `gemv` times the weight GEMVs at the decode step's shapes; `ceilings` are
 rates measured on this GPU (launch gap, HBM stream read, MFMA, LDS); `model`
@@ -98,6 +101,31 @@ class HipEvents:
 
     def destroy(self, e):
         self.L.hipEventDestroy(e)
+
+
+SPREAD_LAUNCHES = 200           # per-launch spread: launches timed one by one ...
+SPREAD_WARMUP = 20              # ... after this many untimed ones
+
+
+def spread(ev, fn, n=SPREAD_LAUNCHES, warm=SPREAD_WARMUP):
+    """Median and p10/p90 (microseconds) of `n` back-to-back launches of
+    fn() after `warm` untimed ones, each bracketed by its own pair of HIP
+    events on the backend's stream (the launches still run back to back: the
+    events are recorded between them, not waited on until the end)."""
+    for _ in range(warm):
+        fn()
+    evs = [(ev.new(), ev.new()) for _ in range(n)]
+    for a, b in evs:
+        ev.record(a)
+        fn()
+        ev.record(b)
+    us = np.array([ev.elapsed_ms(a, b) * 1e3 for a, b in evs])
+    for a, b in evs:
+        ev.destroy(a)
+        ev.destroy(b)
+    p10, med, p90 = np.percentile(us, [10, 50, 90])
+    return {"n": n, "warmup": warm, "median_us": round(float(med), 3), "p10_us": round(float(p10), 3),
+            "p90_us": round(float(p90), 3), "mean_us": round(float(us.mean()), 3)}
 
 
 def kernel_means(be, names):
@@ -194,6 +222,25 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     gpu_ms = ev.elapsed_ms(e0, e1)
     ev.destroy(e0)
     ev.destroy(e1)
+    # per-step spread over SPREAD_LAUNCHES steps, rotating the KV sets as above
+    it = iter(range(1 << 30))
+    step_spread = spread(ev, lambda: step(next(it)))
+    be.sync()
+    # the last step replayed set `last`; its first layer's output must be the
+    # bits an eager call on the same inputs gives (the call rewrites the same
+    # cache row with the same values)
+    last = (SPREAD_LAUNCHES + SPREAD_WARMUP - 1) % nsets
+    i0 = last * layers_per_step
+    replayed = np.empty(HQ * D, np.float32)
+    be.download(replayed, dout + i0 * HQ * D * 4)
+    dchk = be.alloc(HQ * D * 4)
+    be.decode_dev(i0, ctx, dq + i0 * HQ * D * 4, dk + i0 * HKV * D * 4, dv + i0 * HKV * D * 4,
+                  dgq + i0 * D * 4 if norm else None, dgk + i0 * D * 4 if norm else None, dchk)
+    eager_out = np.empty(HQ * D, np.float32)
+    be.download(eager_out, dchk)
+    be.free(dchk)
+    replay_bits_equal = bool(np.array_equal(replayed.view(np.uint32), eager_out.view(np.uint32)))
+    assert replay_bits_equal, "the timed step's output differs from an eager call on the same inputs"
     for g in graphs:
         be.graph_destroy(g)
     kernels = None
@@ -226,6 +273,10 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         "layers_resident": nl,
         "tokens_per_s": 1e3 / (gpu_ms / steps),
         "kernels": kernels,
+        "step_spread": step_spread,
+        "call_spread_us": {k: round(step_spread[k] / layers_per_step, 3)
+                           for k in ("median_us", "p10_us", "p90_us")},
+        "replay_vs_eager": "bit-identical" if replay_bits_equal else "differs",
     }
 
 
@@ -267,6 +318,8 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     ms = ev.elapsed_ms(e0, e1) / steps
     ev.destroy(e0)
     ev.destroy(e1)
+    call_spread = spread(ev, run)
+    be.sync()
     kernels = None
     if kernel_timing:
         be.timing_enable(2)
@@ -283,7 +336,8 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     be.Dispose()
     fl = prefill_flops(p0, seq)
     return {"ms_per_call": ms, "tflops": fl / (ms * 1e-3) / 1e12, "flops": fl,
-            "tokens_per_s": seq / (ms * 1e-3), "kernels": kernels}
+            "tokens_per_s": seq / (ms * 1e-3), "kernels": kernels, "call_spread": call_spread,
+            "tflops_at_median": fl / (call_spread["median_us"] * 1e-6) / 1e12}
 
 
 GEMV_CASES = [  # (name, weight type, rows, cols): the decode step's matrix shapes
@@ -864,6 +918,8 @@ def main():
                                       "bf16 MFMA fp32 acc, empty cache",
                           "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
                           "ms_per_call": round(pre["ms_per_call"], 4),
+                          "call_spread": pre["call_spread"],
+                          "tflops_at_median": round(pre["tflops_at_median"], 2),
                           "tokens_per_s": round(pre["tokens_per_s"], 1),
                           "call_roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",

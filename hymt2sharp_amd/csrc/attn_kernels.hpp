@@ -148,6 +148,10 @@ hipError_t launch_decode(int kv_dtype, const DecodeArgs &a, hipStream_t s);
 // `device` (call with that device current, once per device), then fetch it.
 hipError_t decode_scratch_init(int device);
 hipError_t decode_scratch(int device, float **part_ml, float **part_acc, int *max_heads);
+// Ownership of a device's static decode workspace: claim succeeds for the
+// owner or when the device has none; release clears it (owner only).
+bool decode_scratch_claim(int device, const void *owner);
+void decode_scratch_release(int device, const void *owner);
 hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s);
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s);
 hipError_t launch_prefill_merge(int kv_dtype, const FlashArgs &a, hipStream_t s);

@@ -684,9 +684,11 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(MergeArgs a) {
 // that a decode call needs no device allocation.  Every GPU that loads the
 // library holds its own copy until the process ends; its address on a
 // device comes from hipGetSymbolAddress with that device current (in host
-// code the array's name is not a device address).  Every call on one GPU
-// shares the array: the splits overwrite every partial the merge reads, so
-// nothing needs clearing, and calls that overlap on one GPU race.
+// code the array's name is not a device address).  The splits overwrite
+// every partial the merge reads, so nothing needs clearing.  One context at
+// a time owns a device's array (decode_scratch_claim): its calls run in its
+// stream's order, and another context's calls are refused until the owner is
+// destroyed.
 constexpr int kScratchHeads = 32;
 constexpr size_t kScratchMl = (size_t)kScratchHeads * kMaxSplits * 2;        // floats
 constexpr size_t kScratchAcc = (size_t)kScratchHeads * kMaxSplits * kHeadDim;  // floats
@@ -696,7 +698,25 @@ namespace {
 constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
 float *g_scratch[kScratchDevices] = {};
+// the context whose calls use a device's array (nullptr: none yet); another
+// context is refused until the owner releases it, so two contexts' calls can
+// never overwrite each other's partials
+const void *g_scratch_owner[kScratchDevices] = {};
 }  // namespace
+
+bool decode_scratch_claim(int device, const void *owner) {
+    if (device < 0 || device >= kScratchDevices || !owner) return false;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_owner[device] && g_scratch_owner[device] != owner) return false;
+    g_scratch_owner[device] = owner;
+    return true;
+}
+
+void decode_scratch_release(int device, const void *owner) {
+    if (device < 0 || device >= kScratchDevices) return;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_owner[device] == owner) g_scratch_owner[device] = nullptr;
+}
 
 hipError_t decode_scratch_init(int device) {
     if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;

@@ -350,6 +350,7 @@ int hymt_destroy(hymt_ctx *c) {
         timer_destroy(c->timer);
         c->timer = nullptr;
         (void)hipStreamDestroy(c->stream);
+        decode_scratch_release(c->device, c);  // its work has drained (synchronised above)
     }
     delete c;
     return HYMT_OK;
@@ -627,6 +628,9 @@ int hymt_attn_decode_noalloc(hymt_ctx *c, int layer, int pos, const float *q, co
     if (c->heads > max_heads)
         return fail(HYMT_E_UNSUPPORTED, "the static decode workspace holds " + std::to_string(max_heads) +
                                             " q heads; the context has " + std::to_string(c->heads));
+    if (!decode_scratch_claim(c->device, c))
+        return fail(HYMT_E_STATE, "the static decode workspace of device " + std::to_string(c->device) +
+                                      " is held by another live context (destroy it first)");
     TimedCall timed(call_timer(c), "attn_decode_noalloc", pos);
     return decode_impl(c, layer, pos, q, k, v, qnw, knw, out, HYMT_FLAG_DEVICE_PTRS, ml, acc);
 }

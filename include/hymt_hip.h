@@ -172,9 +172,11 @@ int hymt_attn_decode(hymt_ctx *ctx, int layer, int pos, const float *q, const fl
  * it never calls hipMalloc or hipFree: the split partials live in a static
  * device array of the library (4.06 MiB per GPU, held until the process
  * ends; room for 32 q heads, a larger head count is HYMT_E_UNSUPPORTED), and
- * the RoPE table is built for the whole cache by hymt_kv_create.  All
- * contexts on one GPU share that array: calls that overlap on one GPU (two
- * contexts' streams) race, so callers serialise them.
+ * the RoPE table is built for the whole cache by hymt_kv_create.  One
+ * context at a time owns a GPU's array: the first context to call this on a
+ * GPU holds it until hymt_destroy, and a call from any other live context on
+ * that GPU returns HYMT_E_STATE instead of racing on it.  The owner's calls
+ * run in its stream's order; the array keeps the last call's partials.
  */
 int hymt_attn_decode_noalloc(hymt_ctx *ctx, int layer, int pos, const float *q, const float *k,
                              const float *v, const float *qnw, const float *knw, float *out);

@@ -222,7 +222,9 @@ int orc_cpu_q8k_gemv(int type, const void *w, int rows, int cols, const float *x
 int orc_cpu_decode_step(const orc_cpu_model *m, int token, int pos, float *logits, int threads)
 {
     const int H = m->hidden, F = m->ffn, qd = m->heads * m->head_dim, kd = m->kv_heads * m->head_dim;
-    const int maxc = F > H ? F : H;
+    /* the Q8_K buffer holds the widest projection input: hidden, ffn or the
+       attention output (heads * head_dim, quantised for the o projection) */
+    const int maxc = F > H ? (F > qd ? F : qd) : (H > qd ? H : qd);
     float *h = malloc(sizeof(float) * H), *n = malloc(sizeof(float) * H);
     float *q = malloc(sizeof(float) * qd), *k = malloc(sizeof(float) * kd), *v = malloc(sizeof(float) * kd);
     float *ao = malloc(sizeof(float) * qd), *g = malloc(sizeof(float) * F), *u = malloc(sizeof(float) * F);

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 from hymt2sharp_amd import BF16, F16, F32, HipBackend
-from tests.attn_cases import (BASE, D, EPS, HKV, HQ, cache_rows, max_rel, new_token,
+from hymt2sharp_amd import synth as S
+from tests.attn_cases import (BASE, D, EPS, HKV, HQ, SCALE, cache_rows, max_rel, new_token,
                               oracle_cache)
 
 pytestmark = pytest.mark.gpu
@@ -158,3 +159,96 @@ def test_decode_partial_rotary(oracle, hip_available, rope_dim, dtype, pos):
                                                     salt=rope_dim + pos, rope_dim=rope_dim)
     assert max_rel(got, ref) <= TOL, max_rel(got, ref)
     assert ulp_close(kr, kr_ref, dt) and ulp_close(vr, vr_ref, dt)
+
+
+def _appended_rows(oracle, k, v, knw, dtype, rope_dim=D):
+    """The rows DecodeAttention appends for new k/v rows k[t], v[t] at
+    positions t = 0..n-1: K after RoPE at t (Ops.cs:98-168) and, with a gamma,
+    RMSNorm (Ops.cs:12-90), both rounded to the cache dtype; V raw, rounded."""
+    n = k.shape[0]
+    kr = oracle.neox_rope(k.reshape(n, HKV, D), 0, BASE, rope_dim)
+    if knw is not None:
+        kr = oracle.rmsnorm(kr, knw, EPS)
+    return oracle.to_storage(kr.reshape(n, HKV * D), dtype), oracle.to_storage(v, dtype)
+
+
+def _not_bf16(a):
+    """Fraction of fp32 elements with a nonzero low half (not bf16-representable)."""
+    bits = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return float(np.mean((bits & 0xFFFF) != 0))
+
+
+@pytest.mark.parametrize("norm", [None, "ones"])
+def test_config1_fp32_cache_filled_by_appends(oracle, hip_available, norm):
+    """Config 1 with a genuinely fp32 cache: the 512 cached rows come from 512
+    decode appends (the Forward([token]) loop), so K and V hold fp32 values
+    whose low halves are not zero and the kernel's bf16 hi + lo split of the
+    cached operands carries both halves.  Every step, and the config-1 step at
+    position 512 (L = 513, one split of 8 pages), within max rel 1e-3 of the
+    oracle run step by step over its own fp32 cache."""
+    steps = 512
+    be = make_backend(1, steps + 1, F32)
+    ck, cv = oracle_cache(np.zeros((0, HKV * D), np.uint16), np.zeros((0, HKV * D), np.uint16),
+                          steps + 1, F32)
+    worst = 0.0
+    try:
+        for p in range(steps):
+            q, k, v, qnw, knw = new_token(11, p, norm)
+            got = be.DecodeAttention(0, p, q[0], k[0], v[0], qnw, knw)
+            ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, F32, HQ, HKV, D,
+                                          BASE, EPS, p)
+            worst = max(worst, max_rel(got, ref))
+        kd, vd = be.ReadKv(0, 0, steps)
+        assert _not_bf16(kd) > 0.99 and _not_bf16(vd) > 0.99, (_not_bf16(kd), _not_bf16(vd))
+        q, k, v, qnw, knw = new_token(1, 0, norm)
+        got = be.DecodeAttention(0, steps, q[0], k[0], v[0], qnw, knw)
+    finally:
+        be.Dispose()
+    ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, F32, HQ, HKV, D, BASE, EPS, steps)
+    assert worst <= TOL, worst
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)
+    assert all(ulp_close(kd[p], ck[p], F32) for p in range(steps))
+    assert np.array_equal(vd, cv[:steps])
+
+
+@pytest.mark.parametrize("pos", [16500, 20551])
+def test_fp32_cache_runs_filled_by_appends(oracle, hip_available, pos):
+    """The fp32 run path (past 256 cached pages every split takes its pages
+    one at a time: 16500 -> 258 pages, 3 per split; 20551 -> 322 pages, 3 per
+    split, the last holding one) over a cache written only by decode appends,
+    so every cached K and V row holds fp32 values with nonzero low halves.
+    The device cache is checked row by row against the oracle's appended rows
+    and the step at `pos` against the oracle's decode over its own cache."""
+    salt = pos
+    be = make_backend(1, pos + 1, F32)
+    kin = S.normal(S.seed(12, S.KNEW, salt), (pos, HKV * D), SCALE)
+    vin = S.normal(S.seed(12, S.VNEW, salt), (pos, HKV * D), SCALE)
+    _, _, _, qnw, knw = new_token(12, salt, "gamma")
+    qfill = S.normal(S.seed(12, S.Q, salt), (HQ * D,), SCALE)
+    try:
+        dq, dk, dv = be.alloc(qfill.nbytes), be.alloc(kin.nbytes), be.alloc(vin.nbytes)
+        dg, dout = be.alloc(2 * D * 4), be.alloc(HQ * D * 4)
+        be.upload(dq, qfill)
+        be.upload(dk, kin)
+        be.upload(dv, vin)
+        be.upload(dg, np.concatenate([qnw, knw]).astype(np.float32))
+        row = HKV * D * 4
+        for p in range(pos):  # enqueued back to back; one output buffer
+            be.decode_dev(0, p, dq, dk + p * row, dv + p * row, dg, dg + D * 4, dout)
+        be.sync()
+        kd, vd = be.ReadKv(0, 0, pos)
+        q, k, v, _, _ = new_token(12, salt + 1, None)
+        got = be.DecodeAttention(0, pos, q[0], k[0], v[0], qnw, knw)
+    finally:
+        be.Dispose()
+    kref, vref = _appended_rows(oracle, kin, vin, knw, F32)
+    assert _not_bf16(kd) > 0.99 and _not_bf16(vd) > 0.99, (_not_bf16(kd), _not_bf16(vd))
+    assert np.array_equal(vd, vref)
+    kerr = np.max(np.abs(kd.astype(np.float64) - kref) / np.max(np.abs(kref), axis=1, keepdims=True))
+    assert kerr <= 8 * 2.0 ** -24, kerr
+    ck = oracle.new_cache(pos + 1, HKV, D, F32)
+    cv = oracle.new_cache(pos + 1, HKV, D, F32)
+    ck[:pos] = kref
+    cv[:pos] = vref
+    ref = oracle.decode_attention(q[0], k[0], v[0], qnw, knw, ck, cv, F32, HQ, HKV, D, BASE, EPS, pos)
+    assert max_rel(got, ref) <= TOL, max_rel(got, ref)

@@ -5,11 +5,15 @@ rounding points (tests/mfma_model.py).
 
 Stated bound for the MFMA path against the fp32 oracle.  The kernel rounds
 q (after RoPE/norm and the log2(e)/sqrt(D) scale) and the softmax weights P
-to the operand type, unit roundoff u = 2^-9 (bf16) or 2^-11 (f16); K and V
-are stored in the cache dtype identically on both sides.  Rounding P moves
-each output by at most u * max|V| (the weights sum to 1); rounding q moves
-the logits by u * sum|q_d k_d| * scale, which for RMS-normalised q and k is a
-few u and enters the output through the same weights.  The tests assert
+to the operand type, whose unit roundoff is 2^-8 (bf16) or 2^-11 (f16); K
+and V are stored in the cache dtype identically on both sides.  Rounding P
+moves each output by at most u_op * max|V| (the weights sum to 1); rounding
+q moves the logits by u_op * sum|q_d k_d| * scale, which for RMS-normalised q
+and k is a few u_op and enters the output through the same weights.  The
+bound constant u is 2^-9 for bf16 (half its unit roundoff: the rounding
+errors of P are independent and largely cancel in the weighted sum, and the
+measured errors sit well inside the tighter constant) and 2^-11 for f16.
+The tests assert
   max |a - b|  <= 4 u max|V|     and     mean |a - b| <= u mean|V|
 and report the reference's metric rel = |a-b| / max(1e-3, |a|, |b|)
 (AttentionTests.cs:151-164) alongside.  Against the rounding model the GPU
@@ -29,7 +33,7 @@ from tests.mfma_model import prefill_model
 
 pytestmark = pytest.mark.gpu
 
-U = {BF16: 2.0 ** -9, F16: 2.0 ** -11}
+U = {BF16: 2.0 ** -9, F16: 2.0 ** -11}  # bound constants: bf16 half its unit roundoff, f16 its unit roundoff
 
 
 def make_backend(layers, cap, dtype, rope_dim=D):
