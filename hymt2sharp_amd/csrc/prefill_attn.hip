@@ -623,13 +623,13 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // nphys >= 0: the tile this wave stages next (into buffer buf ^ 1); its
     // K page copy is issued after the S MFMAs, its V page copy after the
     // softmax, so that the copies queue behind work instead of in one burst
-    auto tile_body = [&](auto qq0_tag, int t, int j, int buf, int nphys) {
+    auto tile_body = [&](auto qq0_tag, auto first_tag, int t, int buf, int nphys) {
         constexpr int QQ0 = decltype(qq0_tag)::value;
+        constexpr bool first = decltype(first_tag)::value;
         const uint16_t *kt = sKV + (buf * 2 + half) * KT + lane * 8;
         const uint16_t *vt = sKV + (4 + buf * 2 + half) * KT + grp * 1024 + c * 8;
         // ---- S^T - m = K Q^T - m (64 kv x 16 q per block), accumulated onto
         // -m; the half's first tile starts from 0 and sets m from its scores
-        const bool first = j == 0;
         f32x4 sacc[4][2];
 #pragma unroll
         for (int qq = QQ0; qq < 2; qq++) {
@@ -674,7 +674,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
                 for (int i = 0; i < 4; i++) v = fmaxf(v, sacc[kb][qq][i]);
             mx[qq] = v;
         }
-        if (first) {
+        if constexpr (first) {
 #pragma unroll
             for (int qq = QQ0; qq < 2; qq++) {
                 mrun[qq] = fmaxf(pf_xrow_max(mx[qq]), kFloor2);
@@ -734,7 +734,23 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // jA on the long block runs alone, in a loop of its own where the short
     // block's q rows and scores are dead.
     const int jA = min(max(0, lenA - it.t0 + 1) >> 1, (nt + 1) >> 1);
-    int j = 0;
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using FT = std::integral_constant<bool, true>;
+    using FF = std::integral_constant<bool, false>;
+    // the parity's first tile (j = 0) sets m from its scores: peeled, so the
+    // loops below carry only the lazy-rescale branch
+    {
+        const int t = it.t0 + half;
+        const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
+        if (t < it.t1) {
+            if (t < lenA) tile_body(I0{}, FT{}, t, 0, nphys);
+            else tile_body(I1{}, FT{}, t, 0, nphys);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    }
+    int j = 1;
     for (; j < jA; j++) {
         const int buf = j & 1;
         const int t = it.t0 + 2 * j + half;  // this wave's tile
@@ -742,8 +758,8 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         // reading before the previous barrier
         const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
         if (t < it.t1) {
-            if (t < lenA) tile_body(std::integral_constant<int, 0>{}, t, j, buf, nphys);
-            else tile_body(std::integral_constant<int, 1>{}, t, j, buf, nphys);
+            if (t < lenA) tile_body(I0{}, FF{}, t, buf, nphys);
+            else tile_body(I1{}, FF{}, t, buf, nphys);
         }
         __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
         __syncthreads();
@@ -752,7 +768,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         const int buf = j & 1;
         const int t = it.t0 + 2 * j + half;
         const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
-        if (t < it.t1) tile_body(std::integral_constant<int, 1>{}, t, j, buf, nphys);
+        if (t < it.t1) tile_body(I1{}, FF{}, t, buf, nphys);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
