@@ -1,8 +1,7 @@
 // gemm.cpp -- the prefill GEMMs: y[m][n] (+)= x[m][k] . W[n][k]^T with bf16
-// operands and fp32 accumulation, on this library's MFMA kernel
-// (gemm_mfma.hip) or on hipBLASLt, whichever the first call of a shape
-// times faster (the fused work around them lives in rows.hip and the
-// attention kernels).
+// operands and fp32 accumulation, on hipBLASLt or on this library's MFMA
+// kernel (gemm_mfma.hip) (the fused work around them lives in rows.hip and
+// the attention kernels).
 //
 // hipBLASLt is column-major.  The row-major buffers map onto it without
 // copies: W [n][k] is a k x n column-major matrix (ld k) used transposed,
@@ -15,15 +14,19 @@
 // on one device never share a workspace, and no lock is needed (calls on one
 // context come from one thread, in stream order).
 //
-// Algorithm choice.  hipBLASLt's first heuristic choice is not always its
-// fastest at the prefill shapes, so the first call of a shape in an m bucket
-// (m rounded up to a power of two, at least 256) times up to kCandidates of
-// its candidates and the MFMA kernel on the call's operands and keeps the
-// fastest.  A later m in the same bucket reuses that choice (for hipBLASLt,
-// when the heuristic offers the algorithm for the new m, else its first
-// choice): no timing runs and no scratch allocation for each new prompt
-// length.  HYMT_HIP_GEMM=mfma (the MFMA kernel wherever its shape rules
-// allow) or =hipblaslt, read when the state is created, skips the timing.
+// Algorithm choice, by HYMT_HIP_GEMM (read when the state is created):
+//  unset   hipBLASLt's first heuristic choice for the call's exact shape: no
+//          timing, so identical inputs give identical bits in every context
+//          and process (for one library version and device);
+//  auto    the first call of a shape in an m bucket (m rounded up to a power
+//          of two, at least 256) times up to kCandidates of hipBLASLt's
+//          candidates and the MFMA kernel on the call's operands and keeps
+//          the fastest; a later m in the same bucket reuses that choice (for
+//          hipBLASLt, when the heuristic offers the algorithm for the new m,
+//          else its first choice).  The pick can differ between processes
+//          with timing noise, and with it the summation order and the bits;
+//  hipblaslt  as auto over hipBLASLt's candidates only;
+//  mfma    the MFMA kernel wherever its shape rules allow, else the default.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -56,7 +59,7 @@ struct Choice {
     bool mfma = false;             // the MFMA kernel timed fastest
 };
 
-enum GemmMode { kAuto = 0, kMfmaOnly = 1, kLibOnly = 2 };
+enum GemmMode { kHeuristic = 0, kAuto = 1, kMfmaOnly = 2, kLibTimed = 3 };
 
 void destroy_layouts(Layouts &l) {
     if (l.a) hipblasLtMatrixLayoutDestroy(l.a);
@@ -90,7 +93,7 @@ bool same_algo(const hipblasLtMatmulAlgo_t &x, const hipblasLtMatmulAlgo_t &y) {
 }  // namespace
 
 struct GemmState {
-    int mode = kAuto;
+    int mode = kHeuristic;
     hipblasLtHandle_t handle = nullptr;
     void *workspace = nullptr;
     void *scratch = nullptr;  // timing output of the candidate runs
@@ -105,8 +108,9 @@ GemmState *gemm_state_create() {
     GemmState *g = new (std::nothrow) GemmState();
     if (g) {
         const char *e = std::getenv("HYMT_HIP_GEMM");
+        if (e && !std::strcmp(e, "auto")) g->mode = kAuto;
         if (e && !std::strcmp(e, "mfma")) g->mode = kMfmaOnly;
-        if (e && !std::strcmp(e, "hipblaslt")) g->mode = kLibOnly;
+        if (e && !std::strcmp(e, "hipblaslt")) g->mode = kLibTimed;
     }
     return g;
 }
@@ -280,7 +284,12 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
             return as_hip(st);
         }
         int pick = 0;
-        if (first_in_bucket) {
+        const bool timed = g->mode == kAuto || g->mode == kLibTimed;
+        if (!timed) {
+            // the heuristic's first choice for this exact shape
+            ch.mfma = false;
+            ch.algo = res[0].algo;
+        } else if (first_in_bucket) {
             const bool with_mfma = fits && g->mode == kAuto;
             if (found > 1 || with_mfma) {
                 e = time_candidates(*g, ch.desc, l, res, found, W, x, n, k, m, ldy, y_bf16, accumulate, with_mfma, s,

@@ -18,11 +18,13 @@
 // Output: MFMA row = feature, column = token, so lane (grp, c) holds features
 // 4 grp .. 4 grp + 3 of token c: one 16-byte store per tile (8 for bf16).
 //
-// Measured on the MI355X at m = 2048 (gemm.cpp times it against hipBLASLt's
-// candidates on a shape's first call and keeps the faster): 0.44-0.52
-// PFLOP/s, below hipBLASLt's 0.6-1.2, so the library serves the model's
-// shapes.  What bounds it, from variants timed on the o projection (2048^3,
-// 39 us): without the copies 22 us -- 64 x 64 wave tiles read 0.5 operand
+// Measured on the MI355X at m = 2048 (with HYMT_HIP_GEMM=auto gemm.cpp times
+// it against hipBLASLt's candidates on a shape's first call and keeps the
+// faster): 0.44-0.52 PFLOP/s, below hipBLASLt's 0.6-1.2, so the library
+// serves the model's shapes; at m <= 1024 a shape has too few 128 x 128
+// tiles to fill the chip (16 at m = 128 for the o projection), where
+// hipBLASLt splits k.  What bounds it, from variants timed on the o
+// projection (2048^3, 39 us): without the copies 22 us -- 64 x 64 wave tiles read 0.5 operand
 // fragments per MFMA, 128 bytes per clock per CU at the MFMA rate, about the
 // LDS read rate; the copies add 17 us.  Larger wave tiles (tried up to
 // 128 x 128 per wave with 256-token workgroups) cut the LDS reads but not

@@ -113,9 +113,23 @@ def test_mfma_gemm_runs_and_falls_back(monkeypatch, hip_available):
 
 
 def test_auto_choice_is_correct(monkeypatch, hip_available):
-    """Unforced, the first call of a shape times the MFMA kernel against
-    hipBLASLt's candidates; whichever wins, the results hold the bound."""
-    monkeypatch.delenv("HYMT_HIP_GEMM", raising=False)
+    """HYMT_HIP_GEMM=auto: the first call of a shape times the MFMA kernel
+    against hipBLASLt's candidates; whichever wins, the results hold the bound."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "auto")
     out, _, ref, mag, y0 = run_case(1024, 2048, 300, 77, MFMA)
     check(out, ref, mag, y0)
+
+
+@pytest.mark.parametrize("rows,cols,m", [(2048, 2048, 2048), (1024, 6144, 300)])
+def test_default_choice_is_reproducible(monkeypatch, hip_available, rows, cols, m):
+    """Unset HYMT_HIP_GEMM: hipBLASLt's first heuristic choice, with no
+    timing, so two contexts (each choosing on its own) give the same bits
+    for the same inputs, and the results hold the bound."""
+    monkeypatch.delenv("HYMT_HIP_GEMM", raising=False)
+    a, counts, ref, mag, y0 = run_case(rows, cols, m, 91, MFMA)
+    b, _, _, _, _ = run_case(rows, cols, m, 91, MFMA)
+    check(a, ref, mag, y0)
+    assert not any(counts.values()), counts  # the default never times or runs the MFMA kernel
+    for key in a:
+        assert np.array_equal(a[key], b[key]), key
 
