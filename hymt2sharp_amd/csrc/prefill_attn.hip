@@ -881,10 +881,12 @@ hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_item
 // ------------------------------------------------------------------ merge
 // Combine the split items of a block pair: one workgroup per (pair, kv head,
 // head in group, 8-row quarter of the pair's 32 rows); thread -> (row, 4
-// dims).  All (m, l) of the row are read first, then the partial rows
-// O_s / l_s (type T) stream with up to 8 loads in flight per thread:
-// out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s, w_s = 2^(m_s - max m).
-template <typename T>
+// dims).  out = sum_s w_s l_s (O_s / l_s) / sum_s w_s l_s, w_s = 2^(m_s - max
+// m).  With at most PER splits every (m, l) and partial row O_s / l_s (type
+// T) of the thread is loaded at once, one memory round trip (slots past the
+// pair's splits load the last split again and are masked); PER = 0 takes any
+// split count, the (m, l) first and then the rows up to 8 at a time.
+template <typename T, int PER>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     constexpr int D = kHeadDim, G = kGroup;
     int b = blockIdx.x;
@@ -908,19 +910,35 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
     const float *pm = a.part_ml + ((slot0 * G + g) * 32 + r) * 2;
     const uint16_t *po = (const uint16_t *)a.part_o + ((slot0 * G + g) * 32 + r) * D + d;
     const size_t ml_stride = (size_t)G * 32 * 2, o_stride = (size_t)G * 32 * D;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, pm[s * ml_stride]);
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     float Ls = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < ns; s++) {
-        const float wl = exp2f(pm[s * ml_stride] - M) * pm[s * ml_stride + 1];
+    auto add = [&](float wl, uint2 u) {
         Ls += wl;
-        const uint2 u = *(const uint2 *)(po + s * o_stride);
         acc.x = fmaf(wl, from_elem<T>((uint16_t)(u.x & 0xFFFF)), acc.x);
         acc.y = fmaf(wl, from_elem<T>((uint16_t)(u.x >> 16)), acc.y);
         acc.z = fmaf(wl, from_elem<T>((uint16_t)(u.y & 0xFFFF)), acc.z);
         acc.w = fmaf(wl, from_elem<T>((uint16_t)(u.y >> 16)), acc.w);
+    };
+    if constexpr (PER > 0) {
+        float2 ml[PER];
+        uint2 ov[PER];
+#pragma unroll
+        for (int s = 0; s < PER; s++) {
+            const int ss = min(s, ns - 1);
+            ml[s] = *(const float2 *)(pm + ss * ml_stride);
+            ov[s] = *(const uint2 *)(po + ss * o_stride);
+        }
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < PER; s++) M = fmaxf(M, ml[s].x);  // repeats of the last split change no maximum
+#pragma unroll
+        for (int s = 0; s < PER; s++)
+            if (s < ns) add(exp2f(ml[s].x - M) * ml[s].y, ov[s]);
+    } else {
+        float M = -INFINITY;
+        for (int s = 0; s < ns; s++) M = fmaxf(M, pm[s * ml_stride]);
+#pragma unroll 8
+        for (int s = 0; s < ns; s++) add(exp2f(pm[s * ml_stride] - M) * pm[s * ml_stride + 1], *(const uint2 *)(po + s * o_stride));
     }
     const float inv = Ls > 0.f ? 1.0f / Ls : 0.f;
     const size_t off = (size_t)row * a.heads * D + (size_t)(kvh * G + g) * D + d;
@@ -932,12 +950,20 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(FlashArgs a) {
         *(float4 *)(a.out + off) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
-hipError_t launch_prefill_merge(int kv_dtype, const FlashArgs &a, hipStream_t s) {
+template <typename T> void launch_merge(const FlashArgs &a, dim3 grid, hipStream_t s) {
+    // the largest split count of any pair (pair 0 is the longest)
+    const int ns = flash_splits(pair_tiles(a.pos0, 0, a.nb16, a.seq), a.cap);
     KernelSpan span("prefill_merge", s, true);
+    if (ns <= 8) launch(span, prefill_merge_kernel<T, 8>, grid, dim3(256), 0, s, a);
+    else if (ns <= 16) launch(span, prefill_merge_kernel<T, 16>, grid, dim3(256), 0, s, a);
+    else launch(span, prefill_merge_kernel<T, 0>, grid, dim3(256), 0, s, a);
+}
+
+hipError_t launch_prefill_merge(int kv_dtype, const FlashArgs &a, hipStream_t s) {
     const dim3 grid(a.npairs * a.kv_heads * kGroup * 4);
     switch (kv_dtype) {
-    case 1: launch(span, prefill_merge_kernel<F16>, grid, dim3(256), 0, s, a); break;
-    case 2: launch(span, prefill_merge_kernel<BF16>, grid, dim3(256), 0, s, a); break;
+    case 1: launch_merge<F16>(a, grid, s); break;
+    case 2: launch_merge<BF16>(a, grid, s); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
