@@ -86,13 +86,32 @@ def run_prefill(oracle, dtype, pos, seq, norm, config, salt=0, io_bf16=False, wi
     return got, ref, model, vf, (kd, vd), (kf[pos:pos + seq], vf[pos:pos + seq])
 
 
+def rel_distribution(got, ref):
+    """Percentiles of the reference's per-element metric
+    rel = |a - b| / max(1e-3, |a|, |b|) (AttentionTests.cs:151-164) and the
+    share of outputs whose magnitude is under its 1e-3 floor."""
+    a = np.asarray(got, np.float64).ravel()
+    b = np.asarray(ref, np.float64).ravel()
+    rel = np.abs(a - b) / np.maximum(1e-3, np.maximum(np.abs(a), np.abs(b)))
+    p50, p90, p99, p999 = np.percentile(rel, [50, 90, 99, 99.9])
+    return {"p50": p50, "p90": p90, "p99": p99, "p99.9": p999, "max": rel.max(),
+            "below_floor": float(np.mean(np.abs(b) < 1e-3))}
+
+
 def test_config3_prefill_2048_bf16(oracle, hip_available):
-    """Config 3: 2048 tokens at positions 0..2047, bf16 inputs, bf16 cache."""
+    """Config 3: 2048 tokens at positions 0..2047, bf16 inputs, bf16 cache.
+    Besides the stated bound, the distribution of the reference's metric is
+    printed and held under the levels measured on the MI355X."""
     got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, BF16, 0, 2048, None, 3,
                                                               io_bf16=True)
     check(got, ref, vf, BF16, model)
     assert np.array_equal(vd, vref)
     assert max_rel(kd, kref) <= 2.0 ** -7
+    dist = rel_distribution(got, ref)
+    print("config 3 rel metric:", {k: float(f"{v:.3g}") for k, v in dist.items()})
+    # measured: p50 1.0e-3, p99 9.0e-3, max 0.15 (a quarter of the outputs sit
+    # under the metric's 1e-3 floor, where it reads absolute error x 1000)
+    assert dist["p50"] <= 3e-3 and dist["p99"] <= 2e-2, dist
 
 
 def test_config4_chunk_256_over_8192_fp16(oracle, hip_available):
@@ -101,6 +120,9 @@ def test_config4_chunk_256_over_8192_fp16(oracle, hip_available):
     got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, F16, 8192, 256, None, 4)
     check(got, ref, vf, F16, model)
     assert np.array_equal(vd, vref)
+    dist = rel_distribution(got, ref)
+    print("config 4 rel metric:", {k: float(f"{v:.3g}") for k, v in dist.items()})
+    assert dist["max"] <= 2e-2, dist  # measured 1.2e-3
 
 
 @pytest.mark.parametrize("dtype", [BF16, F16])
