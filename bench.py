@@ -639,6 +639,16 @@ def measure_ceilings():
             ck(L.hc_dispatch_duration(kind, nbytes, iso, ctypes.byref(d)))
             disp[f"{label}_us_{name}"] = round(d.value, 3)
     out["dispatch_stamped"] = disp
+    # split partials handed to a merge (4 groups x 64 workgroups streaming
+    # 32 KiB each, 2 KiB partials): the split kernel alone, with a second
+    # dependent merge launch, and with the last-arriving workgroup merging in
+    # the same launch over device-coherent stores, ticket and loads
+    L.hc_handoff.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    hand = {}
+    for mode, label in ((0, "split_only"), (1, "second_launch"), (2, "in_kernel_ticket")):
+        ck(L.hc_handoff(mode, ctypes.byref(d)))
+        hand[f"{label}_us"] = round(d.value, 3)
+    out["handoff"] = hand
     mf = {}
     for w in (1, 2, 4):
         ck(L.hc_mfma_bf16(w, ctypes.byref(d)))

@@ -1,8 +1,9 @@
 // ceilings.hip -- measured ceilings of one MI355X (gfx950), reported by
 // bench.py beside the vendor peaks: the cost of a dependent kernel launch,
 // the time to stream a buffer of a given size from HBM (the floor under a
-// decode call of that many bytes), the dense bf16 MFMA rate and the LDS read
-// rate.  libhymt_ceilings.so is a measurement tool of the benchmark, not part
+// decode call of that many bytes), the cost of handing split partials to a
+// merge (a second launch against a last-arriving workgroup in the same
+// launch), the dense bf16 MFMA rate and the LDS read rate.  libhymt_ceilings.so is a measurement tool of the benchmark, not part
 // of the attention path's C ABI.  Every function allocates what it times,
 // times it with HIP events on its own stream and frees it; all return 0 on
 // success or the hipError_t of the first failing call.
@@ -38,6 +39,92 @@ __global__ __launch_bounds__(256) void stream_kernel(const uint4 *src, uint32_t 
 #pragma unroll
     for (int i = 0; i < PER_THREAD; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
     if (x == never) sink[blockIdx.x] = x;
+}
+
+// Handing split partials to a merge, on a 4k-position decode call's shape: 4
+// groups (kv heads) of 64 workgroups (splits), each streaming 32 KiB and
+// writing a 2 KiB partial, then
+//   MODE 0  nothing more (the split kernel alone);
+//   MODE 1  plain stores; a second, dependent launch merges (merge_kernel);
+//   MODE 2  device-coherent (sc1) stores, a device-scope ticket per group,
+//           and the workgroup holding a group's last ticket merges its 64
+//           partials with device-coherent loads in the same launch.
+// The merge is a sum (its cost is the reads), written to out[group][512];
+// `done` counts the in-kernel merges so the host can check that every call
+// merged every group.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t hc_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, 0x7fffffff, 0x00020000);
+}
+typedef unsigned hc_u4 __attribute__((ext_vector_type(4)));
+template <int MODE>
+__global__ __launch_bounds__(256) void split_kernel(const uint4 *src, float4 *part, unsigned *ticket, float4 *out,
+                                                    unsigned *done) {
+    const int grp = blockIdx.x & 3, idx = blockIdx.x >> 2, tid = threadIdx.x;
+    const uint4 *p = src + (size_t)blockIdx.x * 2048 + tid;
+    uint4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = p[256 * i];
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    const float f = (float)(x & 0xFFFF) * 1e-6f + (float)idx;
+    __shared__ float4 red[128];
+    __shared__ int last;
+    float4 *pp = part + (size_t)(grp * 64 + idx) * 128;
+    if (MODE != 2) {
+        if (tid < 128) pp[tid] = make_float4(f, f, f, f);
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t r = hc_rsrc(part + (size_t)grp * 64 * 128);
+    if (tid < 128) {
+        const hc_u4 u = {__float_as_uint(f), __float_as_uint(f), __float_as_uint(f), __float_as_uint(f)};
+        __builtin_amdgcn_raw_buffer_store_b128(u, r, (idx * 128 + tid) * 16, 0, 16);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0)
+        last = __hip_atomic_fetch_add(ticket + grp * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 63u;
+    __syncthreads();
+    if (!last) return;
+    // 64 partials of 128 float4: thread (split parity h, float4 c), 32 loads at once
+    const int c = tid & 127, h = tid >> 7;
+    float4 a[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const hc_u4 u = __builtin_amdgcn_raw_buffer_load_b128(r, ((h + 2 * i) * 128 + c) * 16, 0, 16);
+        a[i] = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+    }
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 32; i++) sum = make_float4(sum.x + a[i].x, sum.y + a[i].y, sum.z + a[i].z, sum.w + a[i].w);
+    if (h) red[c] = sum;
+    __syncthreads();
+    if (!h) {
+        const float4 b = red[c];
+        out[grp * 128 + c] = make_float4(sum.x + b.x, sum.y + b.y, sum.z + b.z, sum.w + b.w);
+    }
+    if (tid == 0) {
+        __hip_atomic_store(ticket + grp * 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(done + grp * 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+// MODE 1's second launch: workgroup (group, 8-float4 slice); thread (split
+// group of 32, float4 of the slice) sums two splits, then the 32 split
+// groups through LDS
+__global__ __launch_bounds__(256) void merge_kernel(const float4 *part, float4 *out) {
+    const int grp = blockIdx.x >> 4, sl = blockIdx.x & 15, tid = threadIdx.x, f4 = tid & 7, sg = tid >> 3;
+    const float4 *pp = part + (size_t)grp * 64 * 128 + sl * 8 + f4;
+    const float4 a = pp[(size_t)sg * 128], b = pp[(size_t)(sg + 32) * 128];
+    __shared__ float4 red[32][8];
+    red[sg][f4] = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    __syncthreads();
+    if (tid < 8) {
+        float4 s = red[0][tid];
+        for (int g = 1; g < 32; g++) s = make_float4(s.x + red[g][tid].x, s.y + red[g][tid].y, s.z + red[g][tid].z, s.w + red[g][tid].w);
+        out[grp * 128 + sl * 8 + tid] = s;
+    }
 }
 
 // Independent MFMA chains: each wave keeps 8 accumulators of
@@ -251,6 +338,57 @@ int hc_dispatch_duration(int kind, size_t bytes, int isolated, double *us) {
     if (rc) return rc;
     *us = sum * 1e3 / kN;
     return 0;
+}
+
+// Microseconds per call of the split-partial handoff (split_kernel, MODE
+// 0/1/2 above), calls back to back in a recorded graph, each over its own
+// 8 MiB of inputs (> 1 GiB in all).  MODE 2 checks afterwards that every call
+// merged every group (returns hipErrorUnknown otherwise).
+int hc_handoff(int mode, double *us) {
+    if (mode < 0 || mode > 2) return (int)hipErrorInvalidValue;
+    constexpr int kWg = 256;
+    const size_t buf_bytes = (size_t)kWg * 32768;
+    const int nbuf = (int)(((size_t)1 << 30) / buf_bytes) + 1;
+    Timer t;
+    if (int e = t.init()) return e;
+    std::vector<void *> bufs(nbuf, nullptr);
+    float4 *part = nullptr, *out = nullptr;
+    unsigned *ticket = nullptr, *done = nullptr;
+    int rc = 0;
+    for (int i = 0; i < nbuf && !rc; i++) {
+        rc = (int)hipMalloc(&bufs[i], buf_bytes);
+        if (!rc) rc = (int)hipMemsetAsync(bufs[i], i & 0xff, buf_bytes, t.s);
+    }
+    if (!rc) rc = (int)hipMalloc((void **)&part, (size_t)4 * 64 * 128 * 16);
+    if (!rc) rc = (int)hipMalloc((void **)&out, (size_t)4 * 128 * 16);
+    if (!rc) rc = (int)hipMalloc((void **)&ticket, 4 * 128);
+    if (!rc) rc = (int)hipMalloc((void **)&done, 4 * 128);
+    if (!rc) rc = (int)hipMemsetAsync(ticket, 0, 4 * 128, t.s);
+    if (!rc) rc = (int)hipMemsetAsync(done, 0, 4 * 128, t.s);
+    if (!rc) rc = (int)hipStreamSynchronize(t.s);
+    const int reps = nbuf >= 32 ? 4 : 64 / nbuf + 1;
+    if (!rc)
+        rc = time_launches(t, nbuf, reps, true, [&](int i) {
+            const uint4 *src = (const uint4 *)bufs[i];
+            if (mode == 2) {
+                hipLaunchKernelGGL(split_kernel<2>, dim3(kWg), dim3(256), 0, t.s, src, part, ticket, out, done);
+            } else {
+                hipLaunchKernelGGL(split_kernel<0>, dim3(kWg), dim3(256), 0, t.s, src, part, ticket, out, done);
+                if (mode == 1) hipLaunchKernelGGL(merge_kernel, dim3(64), dim3(256), 0, t.s, part, out);
+            }
+        }, us);
+    if (!rc && mode == 2) {
+        unsigned h[4 * 32] = {};
+        rc = (int)hipMemcpy(h, done, sizeof(h), hipMemcpyDeviceToHost);
+        const unsigned calls = (unsigned)nbuf * (3 + reps);  // time_launches: 3 warm-up runs, then reps
+        for (int g = 0; g < 4 && !rc; g++)
+            if (h[g * 32] != calls) rc = (int)hipErrorUnknown;
+    }
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    for (void *b : {(void *)part, (void *)out, (void *)ticket, (void *)done})
+        if (b) (void)hipFree(b);
+    return rc;
 }
 
 // Dense bf16 MFMA rate (TFLOP/s) with `waves_per_simd` waves on every SIMD of
