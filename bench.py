@@ -149,7 +149,7 @@ def decode_pool(config, ctx, n=8):
 
 
 def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, min_bytes=1 << 30,
-                norm=True, graph=True, kernel_timing=False):
+                norm=True, graph=True, kernel_timing=False, with_spread=True):
     """Decode attention at position `ctx` (L = ctx + 1) over distinct layers.
 
     A step is `layers_per_step` decode calls, one per layer, in stream order
@@ -223,13 +223,16 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
     ev.destroy(e0)
     ev.destroy(e1)
     # per-step spread over SPREAD_LAUNCHES steps, rotating the KV sets as above
-    it = iter(range(1 << 30))
-    step_spread = spread(ev, lambda: step(next(it)))
-    be.sync()
+    last = (steps - 1) % nsets
+    step_spread = None
+    if with_spread:
+        it = iter(range(1 << 30))
+        step_spread = spread(ev, lambda: step(next(it)))
+        be.sync()
+        last = (SPREAD_LAUNCHES + SPREAD_WARMUP - 1) % nsets
     # the last step replayed set `last`; its first layer's output must be the
     # bits an eager call on the same inputs gives (the call rewrites the same
     # cache row with the same values)
-    last = (SPREAD_LAUNCHES + SPREAD_WARMUP - 1) % nsets
     i0 = last * layers_per_step
     replayed = np.empty(HQ * D, np.float32)
     be.download(replayed, dout + i0 * HQ * D * 4)
@@ -275,12 +278,12 @@ def time_decode(config, ctx, kv_dtype, steps, warmup, layers_per_step=LAYERS, mi
         "kernels": kernels,
         "step_spread": step_spread,
         "call_spread_us": {k: round(step_spread[k] / layers_per_step, 3)
-                           for k in ("median_us", "p10_us", "p90_us")},
+                           for k in ("median_us", "p10_us", "p90_us")} if step_spread else None,
         "replay_vs_eager": "bit-identical" if replay_bits_equal else "differs",
     }
 
 
-def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timing=False):
+def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timing=False, with_spread=True):
     """One prefill chunk of `seq` tokens at positions [p0, p0+seq) over a cache
     holding `p0` seeded positions: the chunk's K/V are appended and every row
     attends causally over [0, p0+row].  Repeating the call rewrites the same
@@ -318,7 +321,7 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     ms = ev.elapsed_ms(e0, e1) / steps
     ev.destroy(e0)
     ev.destroy(e1)
-    call_spread = spread(ev, run)
+    call_spread = spread(ev, run) if with_spread else None
     be.sync()
     kernels = None
     if kernel_timing:
@@ -337,7 +340,7 @@ def time_prefill(config, p0, seq, kv_dtype, io_dtype, steps, warmup, kernel_timi
     fl = prefill_flops(p0, seq)
     return {"ms_per_call": ms, "tflops": fl / (ms * 1e-3) / 1e12, "flops": fl,
             "tokens_per_s": seq / (ms * 1e-3), "kernels": kernels, "call_spread": call_spread,
-            "tflops_at_median": fl / (call_spread["median_us"] * 1e-6) / 1e12}
+            "tflops_at_median": fl / (call_spread["median_us"] * 1e-6) / 1e12 if call_spread else None}
 
 
 GEMV_CASES = [  # (name, weight type, rows, cols): the decode step's matrix shapes
@@ -800,6 +803,9 @@ def main():
                          "whole-model decode step or the measured ceilings")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
+    ap.add_argument("--no-spread", action="store_true",
+                    help="skip the per-launch spread statistics (the profiled runs: rocprofv3's kernel trace "
+                         "crashed in hipGraphLaunch during those 220 back-to-back replays with event records)")
     ap.add_argument("--no-graph", action="store_true",
                     help="submit decode steps call by call instead of replaying a recorded step "
                          "(for counter collection, which times dispatches one by one)")
@@ -814,25 +820,30 @@ def main():
     dec = pre = None
     extra = {}
     if args.only in (None, "decode"):
+        sp = not args.no_spread
         dec = time_decode(2, CTX, F16, args.steps, args.warmup, graph=not args.no_graph,
-                          kernel_timing=True)
+                          kernel_timing=True, with_spread=sp)
         eager = dec if args.no_graph else time_decode(2, CTX, F16, args.steps, args.warmup,
-                                                      graph=False)
+                                                      graph=False, with_spread=sp)
     if args.only in (None, "prefill"):
-        pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup, kernel_timing=True)
+        pre = time_prefill(3, 0, 2048, BF16, BF16, args.steps, args.warmup, kernel_timing=True,
+                           with_spread=not args.no_spread)
     if args.only in (None, "configs"):
-        c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False, graph=not args.no_graph)
+        c1 = time_decode(1, 512, F32, args.steps, args.warmup, norm=False, graph=not args.no_graph,
+                         with_spread=not args.no_spread)
         extra["config1"] = {"workload": "decode L=513, fp32 q and KV cache, QK norm off "
                                         "(the configuration names none)",
                             "unit": "GB/s", "value": round(c1["gbs"], 1), **r4(c1)}
-        c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup, kernel_timing=True)
+        c4 = time_prefill(4, 8192, 256, F16, F32, args.steps, args.warmup, kernel_timing=True,
+                          with_spread=not args.no_spread)
         extra["config4"] = {"workload": "prefill chunk 256 at positions 8192..8447 over an "
                                         "8192-position fp16 cache, fp32 in",
                             "unit": "TFLOP/s", "value": round(c4["tflops"], 2), **r4(c4)}
         sweep = {}
         for ctx in (1024, 4096, 16384, 32768):
             r = time_decode(5, ctx, F16, max(4, args.steps // 4), args.warmup,
-                            layers_per_step=8, graph=not args.no_graph, kernel_timing=True)
+                            layers_per_step=8, graph=not args.no_graph, kernel_timing=True,
+                            with_spread=not args.no_spread)
             kd = (r["kernels"] or {}).get("decode_attn")
             sweep[str(ctx)] = {"gbs": round(r["gbs"], 1), "call_us": round(r["call_us"], 3),
                                "frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
@@ -929,7 +940,7 @@ def main():
                           "value": round(pre["tflops"], 2), "unit": "TFLOP/s",
                           "ms_per_call": round(pre["ms_per_call"], 4),
                           "call_spread": pre["call_spread"],
-                          "tflops_at_median": round(pre["tflops_at_median"], 2),
+                          "tflops_at_median": round(pre["tflops_at_median"], 2) if pre["tflops_at_median"] else None,
                           "tokens_per_s": round(pre["tokens_per_s"], 1),
                           "call_roofline": {"bound": "mfma", "achieved": round(pre["tflops"], 2),
                                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
