@@ -135,6 +135,19 @@ def test_prefill_shapes(oracle, hip_available, dtype, pos, seq):
     assert np.array_equal(vd, vref)
 
 
+@pytest.mark.parametrize("dtype,pos,seq", [(F16, 8192, 128), (BF16, 4000, 100), (F16, 8192, 16),
+                                           (BF16, 20000, 40)])
+def test_prefill_split_merge_widths(oracle, hip_available, dtype, pos, seq):
+    """Short chunks over long caches split each block pair's kv range over
+    many workgroups; the merge loads every split at once for up to 8 or 16
+    splits and loops past that: 15 and 13 splits (the 16-wide form), 33 and
+    32 (the general one)."""
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, dtype, pos, seq, "gamma", 14,
+                                                              salt=pos + seq)
+    check(got, ref, vf, dtype, model)
+    assert np.array_equal(vd, vref)
+
+
 def test_decode_equals_prefill_row(oracle, hip_available):
     """Benchmark --verify-prefill invariant (Benchmark/Program.cs:124-145):
     decoding token p over a cache of p rows equals row p of a prefill, up to
