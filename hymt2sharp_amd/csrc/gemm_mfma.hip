@@ -6,33 +6,39 @@
 //
 // Workgroup tile: 128 features x 128 tokens, 4 waves of 64 x 64 (2 x 2), so a
 // wave runs 16 MFMAs per 32-k step from 8 operand fragments.  k advances in
-// stages of 64; a stage is 32 fragments of 1 KiB (16 of W, 16 of x), copied
-// from global memory straight into LDS (global_load_lds_dwordx4) four stages
-// deep, so that three stages of loads are in flight behind the MFMAs.
+// stages of 64; a stage is 16 row blocks of 2 KiB (16 rows x 64 k; 8 of W,
+// 8 of x), copied from global memory straight into LDS
+// (global_load_lds_dwordx4) four stages deep, so that three stages of loads
+// are in flight behind the MFMAs.
 //
-// A fragment (16 rows x 32 k) sits in LDS in operand order: lane (grp, c) =
-// 16 grp + c holds row c, k 8 grp .. 8 grp + 7 at byte 16 lane.  Staging and
-// operand reads are then both linear 1 KiB wave accesses (no bank conflicts),
-// and a lane's staging load is 16 contiguous bytes of one row.
+// Each copy instruction reads 8 whole 128-byte lines (8 rows x 64 k), and
+// its lanes take the 16-byte pieces of a row in an XOR order that places
+// them in LDS so that the operand reads are conflict-free.  The copy pattern
+// sets the operand rate: on the o projection (2048^3) the same kernel took
+// 36 us with each instruction reading 16 rows x 64 bytes (the same half of
+// 16 lines), 29 us with the halves alternating by row, and 25 us with whole
+// lines, with identical output bits; padding the rows by 64 bytes had the
+// alternating form's effect.  A tile alone on its CU streams its operand
+// rows at about 21 bytes per clock this way, against 11 before.
 //
 // Output: MFMA row = feature, column = token, so lane (grp, c) holds features
 // 4 grp .. 4 grp + 3 of token c: one 16-byte store per tile (8 for bf16).
 //
-// Measured on the MI355X at m = 2048 (with HYMT_HIP_GEMM=auto gemm.cpp times
-// it against hipBLASLt's candidates on a shape's first call and keeps the
-// faster): 0.44-0.52 PFLOP/s, below hipBLASLt's 0.6-1.2, so the library
-// serves the model's shapes; at m <= 1024 a shape has too few 128 x 128
-// tiles to fill the chip (16 at m = 128 for the o projection), where
-// hipBLASLt splits k.  What bounds it, from variants timed on the o
-// projection (2048^3, 39 us): without the copies 22 us -- 64 x 64 wave tiles read 0.5 operand
-// fragments per MFMA, 128 bytes per clock per CU at the MFMA rate, about the
-// LDS read rate; the copies add 17 us.  Larger wave tiles (tried up to
-// 128 x 128 per wave with 256-token workgroups) cut the LDS reads but not
-// the copy time.  A tile alone on its CU (m = 512) takes 34 us at k = 2048:
-// its 1 MB of operand rows arrives at about 11 bytes per clock whether the
-// ring holds 4 or 5 stages, the copies go through registers instead, or
-// each load instruction covers whole 128-byte lines; hipBLASLt's
-// 128 x 128 x 128 kernel streams the same rows at about 17.
+// Measured on the MI355X at m = 2048, per call (with HYMT_HIP_GEMM=auto
+// gemm.cpp times it against hipBLASLt's candidates on a shape's first call
+// and keeps the faster): o 29.2 us against hipBLASLt's 26.4, down 73.4
+// against 58.9, so the library still serves the model's shapes; at
+// m <= 1024 a shape has too few 128 x 128 tiles to fill the chip (16 at
+// m = 128 for the o projection), where hipBLASLt splits k.  What bounds it,
+// from timing-only variants of the o projection (2048^3, 25 us without
+// accumulation): the operand stream.  Without the copies 15.7 us, without
+// the LDS operand reads 23.7 (the reads hide under the MFMAs), without the
+// output stores 20.6 (16 MB arriving as one wave of tiles ends; staging the
+// output through LDS into whole-line stores did not change that).  In the
+// steady state a 64-k stage takes about 1730 clocks with the copies and 750
+// without, i.e. 32 KB per CU arrives at about 19 bytes per clock with every
+// CU busy (25 with a tile alone on its CU), whether the ring holds 4 or 5
+// stages or the copies go through registers (33 us, slower).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -49,7 +55,8 @@ constexpr int kTT = 128;                  // tokens per workgroup
 constexpr int kBK = 64;                   // k per stage
 constexpr int kStages = 4;                // LDS ring depth (stages of kBK)
 constexpr int kFrag = 1024;               // bytes of one 16 x 32 operand fragment
-constexpr int kStageBytes = 32 * kFrag;   // W fragments 0..15, x fragments 16..31
+constexpr int kPair = 2 * kFrag;          // one row block's 16 rows x 64 k of a stage
+constexpr int kStageBytes = 32 * kFrag;   // W row blocks 0..7, x row blocks 8..15
 constexpr int kGroupF = 4;                // feature tiles walked together (L2 reuse)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -98,14 +105,15 @@ typedef bf16x8 Frags[2][4];  // [k step of 32][row block of 16]
 // operand reads of the next stage (LDS at sb, this lane's bytes) into (nw,
 // nx) interleaved, one read per two MFMAs, so that the LDS and the matrix
 // pipe work at the same time.
-__device__ __forceinline__ void stage_step(const uint8_t *sb, int wf, int wt, const Frags &cw, const Frags &cx,
-                                           Frags &nw, Frags &nx, f32x4 (&acc)[4][4]) {
+__device__ __forceinline__ void stage_step(const uint8_t *sb, const uint32_t (&off)[2], int wf, int wt,
+                                           const Frags &cw, const Frags &cx, Frags &nw, Frags &nx,
+                                           f32x4 (&acc)[4][4]) {
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            nw[ks][i] = *(const bf16x8 *)(sb + ((4 * wf + i) * 2 + ks) * kFrag);
-            nx[ks][i] = *(const bf16x8 *)(sb + (16 + (4 * wt + i) * 2 + ks) * kFrag);
+            nw[ks][i] = *(const bf16x8 *)(sb + off[ks] + (4 * wf + i) * kPair);
+            nx[ks][i] = *(const bf16x8 *)(sb + off[ks] + (8 + 4 * wt + i) * kPair);
         }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
@@ -130,25 +138,39 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
     tile_of(a, blockIdx.x, tf, tt);
     const int f0 = tf * kTF, t0 = tt * kTT;
 
-    // staging: wave w copies fragments 8 w .. 8 w + 7 of each stage, i.e.
-    // row blocks rb = 4 (w & 1) + j/2 (j < 8) at k step j & 1 of W (w < 2) or
-    // of x (w >= 2); lane (grp, c) loads row 16 rb + c, k 8 (4 ks + grp) + [0, 8)
+    // Staging: wave w copies row blocks rb = 4 (w & 1) + [0, 4) of W (w < 2)
+    // or of x (w >= 2), one block's 2 KiB in two loads, each of 8 whole
+    // rows: load j takes rows 16 rb + 8 (j & 1) + [0, 8), lane l row l >> 3
+    // and the 16-byte piece (l & 7) ^ (l >> 3) ^ (j & 1) of the row's
+    // 128-byte stage.  Each load reads 8 whole 128-byte lines, and lands in
+    // LDS slot l of the block's half j & 1.  Row c of a block (i = c >> 3,
+    // r = c & 7) thus keeps piece p in slot 64 i + 8 r + (p ^ r ^ i); see
+    // the operand offsets below.
     const bool stage_x = wave >= 2;
-    const uint16_t *src[4];
+    const uint16_t *src[8];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int row = (wave & 1) * 64 + j * 16 + c;
-        src[j] = stage_x ? a.x + (size_t)min(t0 + row, a.m - 1) * a.k : a.W + (size_t)(f0 + row) * a.k;
-        src[j] += grp * 8;
+    for (int j = 0; j < 8; j++) {
+        const int row = (wave & 1) * 64 + (j >> 1) * 16 + 8 * (j & 1) + (lane >> 3);
+        const int piece = (lane & 7) ^ (lane >> 3) ^ (j & 1);
+        src[j] = (stage_x ? a.x + (size_t)min(t0 + row, a.m - 1) * a.k : a.W + (size_t)(f0 + row) * a.k) + 8 * piece;
     }
     const uint32_t lds0 = lds_addr(lds) + wave * 8 * kFrag;
     auto issue = [&](int s) {
         const uint32_t dst = lds0 + (s % STAGES) * kStageBytes;
         const int kk = s * kBK;
 #pragma unroll
-        for (int j = 0; j < 8; j++) lds_dma16(src[j >> 1] + kk + (j & 1) * 32, dst + j * kFrag);
+        for (int j = 0; j < 8; j++) lds_dma16(src[j] + kk, dst + j * kFrag);
     };
-    const uint8_t *lane_lds = lds + lane * 16;
+    // Operand reads: lane (grp, c) takes row c, k 8 grp + [0, 8) of k step
+    // ks, i.e. piece 4 ks + grp, at byte off[ks] of each row block.  The 16
+    // lanes of one grp hit 16 distinct slots mod 16 (and any 8 consecutive
+    // ones distinct slots mod 8), so the reads are free of bank conflicts.
+    uint32_t off[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const int i = c >> 3, r = c & 7;
+        off[ks] = 16 * (64 * i + 8 * r + ((4 * ks + grp) ^ r ^ i));
+    }
 
     const int wf = wave & 1, wt = wave >> 1;
     f32x4 acc[4][4];
@@ -169,8 +191,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            aw[ks][i] = *(const bf16x8 *)(lane_lds + ((4 * wf + i) * 2 + ks) * kFrag);
-            ax[ks][i] = *(const bf16x8 *)(lane_lds + (16 + (4 * wt + i) * 2 + ks) * kFrag);
+            aw[ks][i] = *(const bf16x8 *)(lds + off[ks] + (4 * wf + i) * kPair);
+            ax[ks][i] = *(const bf16x8 *)(lds + off[ks] + (8 + 4 * wt + i) * kPair);
         }
     // Stage s: its operands are in registers; make stage s + 1 visible (this
     // wave's copies landed, then a barrier for every wave's, which also
@@ -183,7 +205,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
             asm volatile("s_barrier" ::: "memory");
             if (s + STAGES - 1 < kt) issue(s + STAGES - 1);
         }
-        stage_step(lane_lds + ((s + 1) % STAGES) * kStageBytes, wf, wt, cw, cx, nw, nx, acc);
+        stage_step(lds + ((s + 1) % STAGES) * kStageBytes, off, wf, wt, cw, cx, nw, nx, acc);
     };
     for (int s = 0; s < kt; s += 2) {
         step(s, aw, ax, bw, bx);
