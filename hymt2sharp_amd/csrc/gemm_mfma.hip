@@ -26,8 +26,8 @@
 //
 // Measured on the MI355X at m = 2048, per call (with HYMT_HIP_GEMM=auto
 // gemm.cpp times it against hipBLASLt's candidates on a shape's first call
-// and keeps the faster): o 29.2 us against hipBLASLt's 26.4, down 73.4
-// against 58.9, so the library still serves the model's shapes; at
+// and keeps the faster): o 27.8-28.9 us against hipBLASLt's 26.4, down
+// 68-75 against 58.9, so the library still serves the model's shapes; at
 // m <= 1024 a shape has too few 128 x 128 tiles to fill the chip (16 at
 // m = 128 for the o projection), where hipBLASLt splits k.  What bounds it,
 // from timing-only variants of the o projection (2048^3, 25 us without
@@ -75,17 +75,6 @@ struct GemmArgs {
 // bits 3:0 and 15:14, expcnt and lgkmcnt at their "no wait" maxima)
 #define HYMT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
-// Wait until at most `later` stages of this wave's copies (8 each) are
-// outstanding: the copies retire in order, so every earlier stage has landed.
-__device__ __forceinline__ void wait_stages(int later) {
-    switch (later) {
-    case 0: HYMT_WAIT_VM(0); break;
-    case 1: HYMT_WAIT_VM(8); break;
-    case 2: HYMT_WAIT_VM(16); break;
-    default: HYMT_WAIT_VM(24); break;
-    }
-}
-
 // Workgroup b runs on XCD b % 8 (dispatch is round-robin over the 8 XCDs).
 // Tile order: groups of group_f feature tiles, walked token tile by token
 // tile, so that the 32 workgroups an XCD holds at a time cover about 4 x 8
@@ -131,6 +120,7 @@ __device__ __forceinline__ void stage_step(const uint8_t *sb, const uint32_t (&o
 
 template <bool YBF16, bool ACC, int STAGES>
 __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
+    static_assert(STAGES == 4, "the copy waits below count stages of a 4-slot ring");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * kStageBytes];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int grp = lane >> 4, c = lane & 15;
@@ -183,8 +173,13 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++)
         if (s < kt) issue(s);
-    // stage 0 into registers
-    wait_stages(min(STAGES - 2, kt - 1));
+    // stage 0 into registers.  A wave's copies (8 a stage) retire in order,
+    // so a wait for at most 8 n outstanding copies lands all but the last n
+    // stages issued.  Each wait is one straight-line s_waitcnt: choosing the
+    // count through a switch compiled to a branch tree that cost 5-10 % of
+    // the kernel (o projection 24.9 -> 23.6 us, identical output bits).
+    if (kt > 2) HYMT_WAIT_VM(16);
+    else HYMT_WAIT_VM(8);
     asm volatile("s_barrier" ::: "memory");
     Frags aw, ax, bw, bx;
 #pragma unroll
@@ -201,7 +196,9 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
     // last stage the reads fetch a stale slot, unused.
     auto step = [&](int s, const Frags &cw, const Frags &cx, Frags &nw, Frags &nx) {
         if (s + 1 < kt) {
-            wait_stages(min(s + STAGES - 2, kt - 1) - (s + 1));
+            // stage s + 2 may stay in flight, none at the last refill
+            if (s + 2 < kt) HYMT_WAIT_VM(8);
+            else HYMT_WAIT_VM(0);
             asm volatile("s_barrier" ::: "memory");
             if (s + STAGES - 1 < kt) issue(s + STAGES - 1);
         }
