@@ -98,6 +98,7 @@ struct GemmState {
     void *workspace = nullptr;
     void *scratch = nullptr;  // timing output of the candidate runs
     size_t scratch_bytes = 0;
+    GemmSplitWs split{};      // the MFMA kernel's split-k partials and tickets
     // (n, k, m bucket, y_bf16, accumulate) -> descriptor and timed algorithm
     std::map<std::tuple<int, int, int, bool, bool>, Choice> choices;
     // (n, k, m, ldy, y_bf16, accumulate) -> layouts and the algorithm used
@@ -122,11 +123,46 @@ void gemm_state_destroy(GemmState *g) {
         if (kv.second.desc) hipblasLtMatmulDescDestroy(kv.second.desc);
     if (g->workspace) (void)hipFree(g->workspace);
     if (g->scratch) (void)hipFree(g->scratch);
+    if (g->split.part) (void)hipFree(g->split.part);
+    if (g->split.ticket) (void)hipFree(g->split.ticket);
     if (g->handle) hipblasLtDestroy(g->handle);
     delete g;
 }
 
 namespace {
+
+// The MFMA kernel with its plan for the shape; a split plan first makes sure
+// the state holds room for its partials and tickets (allocated on the stream's
+// first such call, zeroed once; every call leaves the tickets zero).
+hipError_t run_mfma(GemmState &g, const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy,
+                    bool y_bf16, bool acc, hipStream_t s) {
+    const GemmPlan p = gemm_mfma_plan(n, k, m);
+    if (p.split == 2) {
+        const size_t need = gemm_split_bytes(n, m, p);
+        const int tickets = (int)(need / (128 * 128 * 4)) + 1;  // at least one per tile
+        hipError_t e = hipSuccess;
+        if (need > g.split.part_bytes) {
+            e = hipStreamSynchronize(s);
+            if (e == hipSuccess && g.split.part) e = hipFree(g.split.part);
+            g.split.part = nullptr;
+            g.split.part_bytes = 0;
+            if (e == hipSuccess) e = hipMalloc(&g.split.part, need);
+            if (e != hipSuccess) return e;
+            g.split.part_bytes = need;
+        }
+        if (tickets > g.split.tickets) {
+            e = hipStreamSynchronize(s);
+            if (e == hipSuccess && g.split.ticket) e = hipFree(g.split.ticket);
+            g.split.ticket = nullptr;
+            g.split.tickets = 0;
+            if (e == hipSuccess) e = hipMalloc(&g.split.ticket, (size_t)tickets * 32 * sizeof(unsigned));
+            if (e == hipSuccess) e = hipMemsetAsync(g.split.ticket, 0, (size_t)tickets * 32 * sizeof(unsigned), s);
+            if (e != hipSuccess) return e;
+            g.split.tickets = tickets;
+        }
+    }
+    return gemm_bf16_mfma(W, n, k, x, m, y, ldy, y_bf16, acc, s, p, &g.split);
+}
 
 hipblasStatus_t make_desc(hipblasLtMatmulDesc_t &desc) {
     hipblasStatus_t st = hipblasLtMatmulDescCreate(&desc, HIPBLAS_COMPUTE_32F, HIP_R_32F);
@@ -190,7 +226,7 @@ hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layou
     const float alpha = 1.0f, beta = acc ? 1.0f : 0.0f;
     // candidate i >= 0: hipBLASLt's res[i]; -1: the MFMA kernel
     auto run = [&](int i) -> bool {
-        if (i < 0) return gemm_bf16_mfma(W, n, k, x, m, g.scratch, ldy, y_bf16, acc, s) == hipSuccess;
+        if (i < 0) return run_mfma(g, W, n, k, x, m, g.scratch, ldy, y_bf16, acc, s) == hipSuccess;
         return hipblasLtMatmul(g.handle, desc, &alpha, W, l.a, x, l.b, &beta, g.scratch, l.c, g.scratch, l.c,
                                &res[i].algo, g.workspace, res[i].workspaceSize, s) == HIPBLAS_STATUS_SUCCESS;
     };
@@ -238,7 +274,7 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
     if (!g || n < 1 || k < 1 || m < 0 || ldy < n || (accumulate && y_bf16)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const bool fits = gemm_mfma_fits(W, n, k, x, m, y, ldy);
-    if (g->mode == kMfmaOnly && fits) return gemm_bf16_mfma(W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
+    if (g->mode == kMfmaOnly && fits) return run_mfma(*g, W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     hipError_t e = hipSuccess;
     if (!g->handle) {
         hipblasStatus_t st = hipblasLtCreate(&g->handle);
@@ -317,7 +353,7 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
         lit = g->layouts.emplace(lkey, l).first;
     }
     const Layouts &l = lit->second;
-    if (l.mfma && fits) return gemm_bf16_mfma(W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
+    if (l.mfma && fits) return run_mfma(*g, W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     const float alpha = 1.0f, beta = accumulate ? 1.0f : 0.0f;
     KernelSpan span(y_bf16 ? "gemm_bf16_out_bf16" : "gemm_bf16_out_f32", s);
     hipblasStatus_t st = hipblasLtMatmul(g->handle, ch.desc, &alpha, W, l.a, x, l.b, &beta, y, l.c, y, l.c, &l.algo,

@@ -4,44 +4,47 @@
 // shaders (pf_gemm_t32.comp, dispatched at VulkanBackend.cs:782-856): W is a
 // layer's bf16 dense copy (features x k), x the prompt rows (tokens x k).
 //
-// Workgroup tile: 128 features x 128 tokens, 4 waves of 64 x 64 (2 x 2), so a
-// wave runs 16 MFMAs per 32-k step from 8 operand fragments.  k advances in
-// stages of 64; a stage is 16 row blocks of 2 KiB (16 rows x 64 k; 8 of W,
-// 8 of x), copied from global memory straight into LDS
-// (global_load_lds_dwordx4) four stages deep, so that three stages of loads
-// are in flight behind the MFMAs.
+// Workgroup tile: TF = 32 IF features x TT = 32 JT tokens, 4 waves of
+// (TF / 2) x (TT / 2) (2 x 2), so a wave runs IF x JT MFMAs per 32-k step from
+// IF + JT operand fragments.  The tile sizes are template arguments
+// (128 x 128, 256 x 128, 128 x 256, 192 x 128, 192 x 256): a tile of TF x TT reads
+// (TF + TT) / (TF TT) operand bytes per flop from L2, and the rate at which a
+// CU receives operand rows is what bounds these GEMMs (below), so larger tiles
+// are faster wherever there are enough of them to fill the chip.
 //
-// Each copy instruction reads 8 whole 128-byte lines (8 rows x 64 k), and
-// its lanes take the 16-byte pieces of a row in an XOR order that places
-// them in LDS so that the operand reads are conflict-free.  The copy pattern
-// sets the operand rate: on the o projection (2048^3) the same kernel took
-// 36 us with each instruction reading 16 rows x 64 bytes (the same half of
-// 16 lines), 29 us with the halves alternating by row, and 25 us with whole
-// lines, with identical output bits; padding the rows by 64 bytes had the
-// alternating form's effect.  A tile alone on its CU streams its operand
-// rows at about 21 bytes per clock this way, against 11 before.
+// k advances in stages of 64: a stage is (TF + TT) / 16 row blocks of 2 KiB
+// (16 rows x 64 k; the W blocks first, then the x blocks), copied from global
+// memory straight into an LDS ring of S stages (global_load_lds_dwordx4).
+// Each copy instruction reads 8 whole 128-byte lines (8 rows x 64 k), and its
+// lanes take the 16-byte pieces of a row in an XOR order that places them in
+// LDS so that the operand reads are conflict-free.  The copy pattern sets the
+// operand rate: on the o projection (2048^3) the 128 x 128 kernel took 36 us
+// with each instruction reading 16 rows x 64 bytes (the same half of 16
+// lines), 29 us with the halves alternating by row, and 25 us with whole
+// lines, with identical output bits.
+//
+// The operands of one 32-k step are read from LDS into registers while the
+// MFMAs of the previous step run.  Between
+// the two steps of a stage the waves meet at a barrier once the next stage's
+// copies have landed, and refill a free slot of the ring.
+//
+// Split k (SPLIT = 2, for outputs too small to give every CU a large tile):
+// the two workgroups of a tile take the two halves of k.  The first to finish
+// (a device-scope ticket per tile) stores its fp32 partial with
+// device-coherent stores and marks it ready; the second adds it to its own
+// with one fp32 addition per element, which is commutative, so the bits do
+// not depend on which half finished first, and writes the tile.  The second
+// waits only for a workgroup that is already running its stores, and that
+// wait is bounded: past the bound the tile is written as NaN.
 //
 // Output: MFMA row = feature, column = token, so lane (grp, c) holds features
-// 4 grp .. 4 grp + 3 of token c: one 16-byte store per tile (8 for bf16).
-//
-// Measured on the MI355X at m = 2048, per call (with HYMT_HIP_GEMM=auto
-// gemm.cpp times it against hipBLASLt's candidates on a shape's first call
-// and keeps the faster): o 27.8-28.9 us against hipBLASLt's 26.4, down
-// 68-75 against 58.9, so the library still serves the model's shapes; at
-// m <= 1024 a shape has too few 128 x 128 tiles to fill the chip (16 at
-// m = 128 for the o projection), where hipBLASLt splits k.  What bounds it,
-// from timing-only variants of the o projection (2048^3, 25 us without
-// accumulation): the operand stream.  Without the copies 15.7 us, without
-// the LDS operand reads 23.7 (the reads hide under the MFMAs), without the
-// output stores 20.6 (16 MB arriving as one wave of tiles ends; staging the
-// output through LDS into whole-line stores did not change that).  In the
-// steady state a 64-k stage takes about 1730 clocks with the copies and 750
-// without, i.e. 32 KB per CU arrives at about 19 bytes per clock with every
-// CU busy (25 with a tile alone on its CU), whether the ring holds 4 or 5
-// stages or the copies go through registers (33 us, slower).
+// 4 grp .. 4 grp + 3 of token c: one 16-byte store per 16 x 16 block (8 for
+// bf16).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
 
 #include "device_common.hpp"
 #include "ktimer.hpp"
@@ -50,17 +53,15 @@
 namespace hymt {
 namespace {
 
-constexpr int kTF = 128;                  // features per workgroup
-constexpr int kTT = 128;                  // tokens per workgroup
-constexpr int kBK = 64;                   // k per stage
-constexpr int kStages = 4;                // LDS ring depth (stages of kBK)
-constexpr int kFrag = 1024;               // bytes of one 16 x 32 operand fragment
-constexpr int kPair = 2 * kFrag;          // one row block's 16 rows x 64 k of a stage
-constexpr int kStageBytes = 32 * kFrag;   // W row blocks 0..7, x row blocks 8..15
-constexpr int kGroupF = 4;                // feature tiles walked together (L2 reuse)
+constexpr int kBK = 64;               // k per stage
+constexpr int kFrag = 1024;           // bytes of one 16 x 32 operand fragment
+constexpr int kPair = 2 * kFrag;      // one row block's 16 rows x 64 k of a stage
+constexpr int kGroupF = 4;            // feature tiles walked together (L2 reuse)
+constexpr unsigned kSpinLimit = 1u << 22;  // polls of a split tile's ready mark
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
     const uint16_t *W;  // [n][k]
@@ -68,88 +69,154 @@ struct GemmArgs {
     void *y;            // [m][ldy], fp32 or bf16
     int n, k, m, ldy;
     int tiles_f, tiles_t, group_f;
-    int xcd_per;        // tiles per XCD run, 0: identity order
+    int xcd_per;        // workgroups per XCD run, 0: identity order
+    int kt;             // stages per workgroup (k / SPLIT / 64)
+    float *part;        // SPLIT: partial tiles [tile][TF TT] in lane order
+    unsigned *ticket;   // SPLIT: one per tile, 32 words apart, zero between calls
 };
 
-// s_waitcnt with only vmcnt (<= 63) constrained (gfx9 encoding: vmcnt in
-// bits 3:0 and 15:14, expcnt and lgkmcnt at their "no wait" maxima)
+// s_waitcnt with vmcnt (<= 63) constrained and lgkmcnt left at its "no wait"
+// maximum, or (the _L form) waited to zero too (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 #define HYMT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define HYMT_WAIT_VM_L(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
+
+// Wait until at most C min(n, MAXN) of a wave's copies are outstanding (with
+// LGKM, its LDS reads done too): one straight-line s_waitcnt per branch, the
+// common case (n >= MAXN) first.
+template <int C, int MAXN, bool LGKM>
+__device__ __forceinline__ void wait_stages(int n) {
+    if constexpr (MAXN > 0) {
+        if (n >= MAXN) {
+            if constexpr (LGKM) HYMT_WAIT_VM_L(C * MAXN);
+            else HYMT_WAIT_VM(C * MAXN);
+            return;
+        }
+        wait_stages<C, MAXN - 1, LGKM>(n);
+    } else {
+        if constexpr (LGKM) HYMT_WAIT_VM_L(0);
+        else HYMT_WAIT_VM(0);
+    }
+}
+
+// 16 bytes per lane from global memory straight into LDS, addressed as a
+// uniform base (SGPR pair) plus a 32-bit per-lane byte offset: lane i writes
+// LDS bytes lds_base + 16 i.  Inline assembly for the reason lds_dma16 gives
+// (device_common.hpp); m0 is written here and declared clobbered.
+__device__ __forceinline__ void lds_dma16_sv(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, 0x7fffffff, 0x00020000);
+}
+constexpr int kSc1 = 16;  // buffer cache policy: device-coherent (sc1)
 
 // Workgroup b runs on XCD b % 8 (dispatch is round-robin over the 8 XCDs).
 // Tile order: groups of group_f feature tiles, walked token tile by token
-// tile, so that the 32 workgroups an XCD holds at a time cover about 4 x 8
-// tiles and share their W and x rows in that XCD's L2; each XCD takes one
-// contiguous run of that order.
-__device__ __forceinline__ void tile_of(const GemmArgs &a, int b, int &tf, int &tt) {
+// tile, so that the workgroups an XCD holds at a time share their W and x
+// rows in that XCD's L2; each XCD takes one contiguous run of that order (of
+// workgroups: the two k halves of a split tile are neighbours).
+template <int SPLIT>
+__device__ __forceinline__ void tile_of(const GemmArgs &a, int b, int &tile, int &tf, int &tt, int &kz) {
     const int L = a.xcd_per ? (b & 7) * a.xcd_per + (b >> 3) : b;
+    tile = L / SPLIT;
+    kz = L - tile * SPLIT;
     const int per_group = a.group_f * a.tiles_t;
-    const int g = L / per_group, r = L - g * per_group;
+    const int g = tile / per_group, r = tile - g * per_group;
     tt = r / a.group_f;
     tf = g * a.group_f + (r - tt * a.group_f);
 }
 
-typedef bf16x8 Frags[2][4];  // [k step of 32][row block of 16]
-
-// One stage of a wave: the 32 MFMAs of the operands in (cw, cx), with the 16
-// operand reads of the next stage (LDS at sb, this lane's bytes) into (nw,
-// nx) interleaved, one read per two MFMAs, so that the LDS and the matrix
-// pipe work at the same time.
-__device__ __forceinline__ void stage_step(const uint8_t *sb, const uint32_t (&off)[2], int wf, int wt,
-                                           const Frags &cw, const Frags &cx, Frags &nw, Frags &nx,
-                                           f32x4 (&acc)[4][4]) {
+// One 32-k step of a wave: the IF x JT MFMAs of the operands in (w, cx),
+// row by row, with the operand reads of the next step (LDS at nsb + noff,
+// this lane's bytes) interleaved: W fragment i of the next step replaces w[i]
+// as soon as row i's MFMAs have issued, and the x fragments go to nx, so a
+// wave holds IF + 2 JT fragments (a 256 x 256 tile's 128 x 128 wave tile
+// fits beside its 256 accumulators).
+template <int IF, int JT>
+__device__ __forceinline__ void substep(bf16x8 (&w)[IF], const bf16x8 (&cx)[JT], const uint8_t *nsb,
+                                        uint32_t noff, int wf, int wt, bf16x8 (&nx)[JT], f32x4 (&acc)[IF][JT]) {
+    constexpr int NBF = 2 * IF;  // W row blocks of a stage
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
+    for (int i = 0; i < IF; i++) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            nw[ks][i] = *(const bf16x8 *)(sb + off[ks] + (4 * wf + i) * kPair);
-            nx[ks][i] = *(const bf16x8 *)(sb + off[ks] + (8 + 4 * wt + i) * kPair);
+        for (int j = 0; j < JT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], cx[j], acc[i][j], 0, 0, 0);
+        w[i] = *(const bf16x8 *)(nsb + noff + (IF * wf + i) * kPair);
+#pragma unroll
+        for (int j = i * JT / IF; j < (i + 1) * JT / IF; j++)
+            nx[j] = *(const bf16x8 *)(nsb + noff + (NBF + JT * wt + j) * kPair);
+    }
+    if constexpr (JT >= IF) {
+#pragma unroll
+        for (int i = 0; i < IF; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, JT, 0);            // row i's MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x100, 1 + JT / IF, 0);   // its reads
         }
+    } else {
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cw[ks][i], cx[ks][j], acc[i][j], 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // 2 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 DS read
+        for (int g = 0; g < JT; g++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, IF, 0);            // IF / JT rows' MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x100, IF / JT + 1, 0);   // their reads
+        }
     }
 }
 
-template <bool YBF16, bool ACC, int STAGES>
-__global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
-    static_assert(STAGES == 4, "the copy waits below count stages of a 4-slot ring");
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * kStageBytes];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// The 4 waves' MFMAs of a tile (IF x JT 16 x 16 blocks per wave) over the
+// workgroup's k range.  S stages in the LDS ring; LGKM: a stage's slot is
+// refilled at the barrier right after its last operand reads (each wave first
+// waits for its own reads: lgkmcnt(0)), so S - 1 stages are ahead of the one
+// being read; else one barrier later, with S - 2 stages ahead and no wait on
+// the reads.
+template <int IF, int JT, int S, bool LGKM, int SPLIT, bool YBF16, bool ACC>
+__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
+    constexpr int TF = 32 * IF, TT = 32 * JT;
+    constexpr int NBF = TF / 16, NB = (TF + TT) / 16, NBW = NB / 4;  // row blocks: W, all, per wave
+    constexpr int C = 2 * NBW;                                         // copy instructions per wave per stage
+    constexpr int kStageBytes = NB * kPair;
+    constexpr int AHEAD = LGKM ? S : S - 1;  // stages issued ahead of the one being read, plus one
+    static_assert(NB % 4 == 0 && AHEAD >= 2 && C * (AHEAD - 1) <= 63, "tile shape");
+    static_assert(S * kStageBytes <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[S * kStageBytes];
+    unsigned &s_role = *(unsigned *)lds;  // split role, once the ring is idle
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = lane >> 4, c = lane & 15;
-    int tf, tt;
-    tile_of(a, blockIdx.x, tf, tt);
-    const int f0 = tf * kTF, t0 = tt * kTT;
+    int tile, tf, tt, kz;
+    tile_of<SPLIT>(a, blockIdx.x, tile, tf, tt, kz);
+    const int f0 = tf * TF, t0 = tt * TT;
+    const int kt = a.kt;
+    const size_t kbase = (size_t)kz * kt * kBK;
 
-    // Staging: wave w copies row blocks rb = 4 (w & 1) + [0, 4) of W (w < 2)
-    // or of x (w >= 2), one block's 2 KiB in two loads, each of 8 whole
-    // rows: load j takes rows 16 rb + 8 (j & 1) + [0, 8), lane l row l >> 3
-    // and the 16-byte piece (l & 7) ^ (l >> 3) ^ (j & 1) of the row's
-    // 128-byte stage.  Each load reads 8 whole 128-byte lines, and lands in
-    // LDS slot l of the block's half j & 1.  Row c of a block (i = c >> 3,
-    // r = c & 7) thus keeps piece p in slot 64 i + 8 r + (p ^ r ^ i); see
-    // the operand offsets below.
-    const bool stage_x = wave >= 2;
-    const uint16_t *src[8];
+    // Staging: wave w copies row blocks gb = NBW w + [0, NBW) (W blocks
+    // first, then x), one block's 2 KiB in two loads, each of 8 whole rows:
+    // load h takes rows 16 rb + 8 h + [0, 8), lane l row l >> 3 and the
+    // 16-byte piece (l & 7) ^ (l >> 3) ^ h of the row's 128-byte stage.  Each
+    // load reads 8 whole 128-byte lines, and lands in LDS slot l of the
+    // block's half h.  Row c of a block (i = c >> 3, r = c & 7) thus keeps
+    // piece p in slot 64 i + 8 r + (p ^ r ^ i); see the operand offsets below.
+    uint32_t voff[C];
+    const uint16_t *sbase[C];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int row = (wave & 1) * 64 + (j >> 1) * 16 + 8 * (j & 1) + (lane >> 3);
-        const int piece = (lane & 7) ^ (lane >> 3) ^ (j & 1);
-        src[j] = (stage_x ? a.x + (size_t)min(t0 + row, a.m - 1) * a.k : a.W + (size_t)(f0 + row) * a.k) + 8 * piece;
+    for (int j = 0; j < C; j++) {
+        const int gb = wave * NBW + (j >> 1), h = j & 1;
+        const int rl = 8 * h + (lane >> 3);
+        const int piece = (lane & 7) ^ (lane >> 3) ^ h;
+        const bool isw = gb < NBF;
+        const int row = isw ? f0 + 16 * gb + rl : min(t0 + 16 * (gb - NBF) + rl, a.m - 1);
+        voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
+        sbase[j] = (isw ? a.W : a.x) + kbase;
     }
-    const uint32_t lds0 = lds_addr(lds) + wave * 8 * kFrag;
+    const uint32_t lds0 = lds_addr(lds) + wave * NBW * kPair;
     auto issue = [&](int s) {
-        const uint32_t dst = lds0 + (s % STAGES) * kStageBytes;
+        const uint32_t dst = lds0 + (s % S) * kStageBytes;
         const int kk = s * kBK;
 #pragma unroll
-        for (int j = 0; j < 8; j++) lds_dma16(src[j] + kk, dst + j * kFrag);
+        for (int j = 0; j < C; j++) lds_dma16_sv(sbase[j] + kk, voff[j], dst + j * kFrag);
     };
     // Operand reads: lane (grp, c) takes row c, k 8 grp + [0, 8) of k step
     // ks, i.e. piece 4 ks + grp, at byte off[ks] of each row block.  The 16
@@ -163,60 +230,113 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
     }
 
     const int wf = wave & 1, wt = wave >> 1;
-    f32x4 acc[4][4];
+    f32x4 acc[IF][JT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < IF; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < JT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int kt = a.k / kBK;  // even, >= 2
+    // kt >= 2.  A wave's copies (C a stage) retire in order, so a wait for at
+    // most C n outstanding copies lands all but the last n stages issued.
+    // Each wait is one straight-line s_waitcnt: choosing the count through a
+    // switch compiled to a branch tree that cost 5-10 % of the kernel.
 #pragma unroll
-    for (int s = 0; s < STAGES - 1; s++)
+    for (int s = 0; s < AHEAD; s++)
         if (s < kt) issue(s);
-    // stage 0 into registers.  A wave's copies (8 a stage) retire in order,
-    // so a wait for at most 8 n outstanding copies lands all but the last n
-    // stages issued.  Each wait is one straight-line s_waitcnt: choosing the
-    // count through a switch compiled to a branch tree that cost 5-10 % of
-    // the kernel (o projection 24.9 -> 23.6 us, identical output bits).
-    if (kt > 2) HYMT_WAIT_VM(16);
-    else HYMT_WAIT_VM(8);
+    wait_stages<C, AHEAD - 1, false>(kt - 1);
     asm volatile("s_barrier" ::: "memory");
-    Frags aw, ax, bw, bx;
+    bf16x8 w[IF], ax[JT], bx[JT];
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++)
+    for (int i = 0; i < IF; i++) w[i] = *(const bf16x8 *)(lds + off[0] + (IF * wf + i) * kPair);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            aw[ks][i] = *(const bf16x8 *)(lds + off[ks] + (4 * wf + i) * kPair);
-            ax[ks][i] = *(const bf16x8 *)(lds + off[ks] + (8 + 4 * wt + i) * kPair);
-        }
-    // Stage s: its operands are in registers; make stage s + 1 visible (this
-    // wave's copies landed, then a barrier for every wave's, which also
-    // frees the slot of stage s - 1), refill that slot with stage
-    // s + STAGES - 1, then the MFMAs of s with the reads of s + 1.  After the
-    // last stage the reads fetch a stale slot, unused.
-    auto step = [&](int s, const Frags &cw, const Frags &cx, Frags &nw, Frags &nx) {
+    for (int j = 0; j < JT; j++) ax[j] = *(const bf16x8 *)(lds + off[0] + (NBF + JT * wt + j) * kPair);
+
+    for (int s = 0; s < kt; s++) {
+        const uint8_t *sb = lds + (s % S) * kStageBytes;
+        // step (s, 0): its operands in (w, ax); read step (s, 1) into (w, bx)
+        substep<IF, JT>(w, ax, sb, off[1], wf, wt, bx, acc);
         if (s + 1 < kt) {
-            // stage s + 2 may stay in flight, none at the last refill
-            if (s + 2 < kt) HYMT_WAIT_VM(8);
-            else HYMT_WAIT_VM(0);
+            // stage s + 1 landed: stages up to s - 1 + AHEAD are issued, and
+            // min(AHEAD - 2, kt - 2 - s) of them may stay in flight
+            wait_stages<C, AHEAD - 2, LGKM>(kt - 2 - s);
             asm volatile("s_barrier" ::: "memory");
-            if (s + STAGES - 1 < kt) issue(s + STAGES - 1);
+            if (s + AHEAD < kt) issue(s + AHEAD);
+            // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax)
+            substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc);
+        } else {
+#pragma unroll
+            for (int i = 0; i < IF; i++)
+#pragma unroll
+                for (int j = 0; j < JT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], bx[j], acc[i][j], 0, 0, 0);
         }
-        stage_step(lds + ((s + 1) % STAGES) * kStageBytes, off, wf, wt, cw, cx, nw, nx, acc);
-    };
-    for (int s = 0; s < kt; s += 2) {
-        step(s, aw, ax, bw, bx);
-        step(s + 1, bw, bx, aw, ax);
     }
 
-    // epilogue: lane (grp, c) of tile (i, j) holds features f .. f + 3 of token t
+    if constexpr (SPLIT == 2) {
+        // Ticket values of a tile within one call: the first arrival takes
+        // 0 -> 1 and, once its partial is stored, adds 2; the second arrival
+        // reads 1 (partial pending) or 3 (stored) and sets 0 for the next call.
+        unsigned *tk = a.ticket + (size_t)tile * 32;
+        __syncthreads();  // every wave's operand reads are done: the ring is idle
+        if (tid == 0) s_role = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        const unsigned role = s_role;
+        const __amdgpu_buffer_rsrc_t pr = part_rsrc(a.part + (size_t)tile * TF * TT);
+        if (role == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int t = t0 + 64 * wt + 16 * j + c;
+            for (int i = 0; i < IF; i++)
+#pragma unroll
+                for (int j = 0; j < JT; j++) {
+                    const f32x4 v = acc[i][j];
+                    const u32x4 u = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                                     __float_as_uint(v[3])};
+                    __builtin_amdgcn_raw_buffer_store_b128(u, pr, ((i * JT + j) * 256 + tid) * 16, 0, kSc1);
+                }
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);  // every store acknowledged
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __syncthreads();
+            if (tid == 0) __hip_atomic_fetch_add(tk, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+        if (tid == 0) {
+            unsigned v = role, spins = 0;
+            if (role == 1) {
+                do {
+                    __builtin_amdgcn_s_sleep(2);
+                    v = __hip_atomic_load(tk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } while (v != 4u && ++spins < kSpinLimit);
+                v = v == 4u ? 3u : 0u;
+            }
+            s_role = v;  // 3: the partial is stored; else the tile is written as NaN
+            __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        const bool ok = s_role == 3u;
+#pragma unroll
+        for (int i = 0; i < IF; i++) {
+            u32x4 p[JT];
+#pragma unroll
+            for (int j = 0; j < JT; j++)
+                p[j] = __builtin_amdgcn_raw_buffer_load_b128(pr, ((i * JT + j) * 256 + tid) * 16, 0, kSc1);
+#pragma unroll
+            for (int j = 0; j < JT; j++) {
+                f32x4 v = acc[i][j];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = ok ? v[e] + __uint_as_float(p[j][e]) : __builtin_nanf("");
+                acc[i][j] = v;
+            }
+        }
+    }
+
+    // epilogue: lane (grp, c) of block (i, j) holds features f .. f + 3 of token t
+#pragma unroll
+    for (int j = 0; j < JT; j++) {
+        const int t = t0 + (TT / 2) * wt + 16 * j + c;
         if (t >= a.m) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int f = f0 + 64 * wf + 16 * i + 4 * grp;
+        for (int i = 0; i < IF; i++) {
+            const int f = f0 + (TF / 2) * wf + 16 * i + 4 * grp;
             const f32x4 v = acc[i][j];
             if constexpr (YBF16) {
                 uint16_t *yp = (uint16_t *)a.y + (size_t)t * a.ldy + f;
@@ -226,8 +346,8 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
                 float4 *yp = (float4 *)((float *)a.y + (size_t)t * a.ldy + f);
                 float4 o = make_float4(v[0], v[1], v[2], v[3]);
                 if constexpr (ACC) {
-                    const float4 p = *yp;
-                    o = make_float4(p.x + o.x, p.y + o.y, p.z + o.z, p.w + o.w);
+                    const float4 q = *yp;
+                    o = make_float4(q.x + o.x, q.y + o.y, q.z + o.z, q.w + o.w);
                 }
                 *yp = o;
             }
@@ -235,17 +355,108 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_kernel(GemmArgs a) {
     }
 }
 
+// The tile shapes: IF, JT (features / 32, tokens / 32), ring depth, LGKM.
+struct TileShape {
+    const char *name;
+    int IF, JT;
+};
+constexpr TileShape kTiles[kGemmTiles] = {
+    {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}};
+
+template <int IF, int JT, int S, bool LGKM, int SPLIT>
+void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span) {
+    if (y_bf16) launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, true, false>, dim3(grid), dim3(256), 0, s, a);
+    else if (acc) launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, false, true>, dim3(grid), dim3(256), 0, s, a);
+    else launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, false, false>, dim3(grid), dim3(256), 0, s, a);
+}
+
+// Ring depths, measured at the model's shapes: deeper rings (128 x 128 with 5
+// stages, 4 ahead) were no faster, so the stream is not latency-bound.
+template <int SPLIT>
+void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s,
+                  const KernelSpan &span) {
+    switch (tile) {
+    case 0: launch_tile<4, 4, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 32 KiB stages
+    case 1: launch_tile<8, 4, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
+    case 2: launch_tile<4, 8, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
+    case 3: launch_tile<6, 4, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB
+    default: launch_tile<6, 8, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 56 KiB
+    }
+}
+
+int tiles_of(int tile, int n, int m) {
+    const int TF = 32 * kTiles[tile].IF, TT = 32 * kTiles[tile].JT;
+    if (n % TF) return 0;
+    return (n / TF) * ((m + TT - 1) / TT);
+}
+
 }  // namespace
+
+int gemm_tile_by_name(const char *name) {
+    for (int t = 0; t < kGemmTiles; t++)
+        if (!std::strcmp(name, kTiles[t].name)) return t;
+    return -1;
+}
+
+// The tile plan for a shape.  Measured at m = 2048 (us per call, this kernel
+// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 33.4
+// (128 x 128 42.7) / 28.7; gate/up 12288 x 2048 192 x 256 113.7 (128 x 128
+// 149) / 87.0; o 2048 x 2048 128 x 128 31.7 (split 128 x 256 34.3) / 24.6;
+// down 2048 x 6144 split 128 x 256 69.8 (128 x 128 78.2) / 54.9.  So: the
+// widest tile that still gives the chip 1.5 rounds of workgroups, 192 rows
+// where the width allows; a k split when one round of 128 x 128 tiles holds
+// every output and k is deep enough (>= 4096) to pay for the handoff.
+GemmPlan gemm_mfma_plan(int n, int k, int m) {
+    // forced by HYMT_HIP_GEMM_TILE=<tile>[,2] (a tuning knob; the shape rules
+    // still apply)
+    if (const char *e = std::getenv("HYMT_HIP_GEMM_TILE")) {
+        char buf[32];
+        std::strncpy(buf, e, sizeof(buf) - 1);
+        buf[sizeof(buf) - 1] = 0;
+        char *comma = std::strchr(buf, ',');
+        int split = 1;
+        if (comma) {
+            *comma = 0;
+            split = std::atoi(comma + 1) == 2 ? 2 : 1;
+        }
+        const int t = gemm_tile_by_name(buf);
+        if (t >= 0) return GemmPlan{t, split};
+    }
+    constexpr int kCUs = 256;
+    if (n % 192 == 0) {
+        if (tiles_of(4, n, m) * 2 >= 3 * kCUs) return GemmPlan{4, 1};
+        if (tiles_of(3, n, m) * 4 >= 3 * kCUs) return GemmPlan{3, 1};
+    }
+    if (tiles_of(0, n, m) <= kCUs && tiles_of(2, n, m) * 2 > kCUs / 2 && k >= 4096 && k % 256 == 0)
+        return GemmPlan{2, 2};
+    if (tiles_of(0, n, m) <= kCUs / 2 && k % 256 == 0) return GemmPlan{0, 2};  // a short prompt
+    return GemmPlan{0, 1};
+}
 
 bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, const void *y, int ldy) {
     auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
-    return n > 0 && n % kTF == 0 && k >= 2 * kBK && k % (2 * kBK) == 0 && m > 0 && ldy >= n && ldy % 4 == 0 && a16(W) &&
-           a16(x) && a16(y);
+    return n > 0 && n % 128 == 0 && k >= 2 * kBK && k % (2 * kBK) == 0 && m > 0 && ldy >= n && ldy % 4 == 0 &&
+           (size_t)n * k * 2 < (1ull << 31) && (size_t)m * k * 2 < (1ull << 31) && a16(W) && a16(x) && a16(y);
+}
+
+size_t gemm_split_bytes(int n, int m, GemmPlan p) {
+    if (p.split < 2) return 0;
+    return (size_t)tiles_of(p.tile, n, m) * 32 * kTiles[p.tile].IF * 32 * kTiles[p.tile].JT * 4;
 }
 
 hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,
-                          bool accumulate, hipStream_t s) {
+                          bool accumulate, hipStream_t s, GemmPlan p, const GemmSplitWs *ws) {
     if (!gemm_mfma_fits(W, n, k, x, m, y, ldy) || (accumulate && y_bf16)) return hipErrorInvalidValue;
+    if (p.tile < 0 || p.tile >= kGemmTiles) return hipErrorInvalidValue;
+    int tiles = tiles_of(p.tile, n, m);
+    if (!tiles) {  // n not a multiple of the tile's width
+        p = GemmPlan{0, p.split};
+        tiles = tiles_of(0, n, m);
+    }
+    // a split needs >= 2 stages per half and room for its partials and tickets
+    if (p.split == 2 && (k % (4 * kBK) || !ws || ws->part_bytes < gemm_split_bytes(n, m, p) || ws->tickets < tiles))
+        p.split = 1;
+    const int TF = 32 * kTiles[p.tile].IF;
     GemmArgs a;
     a.W = W;
     a.x = x;
@@ -254,15 +465,17 @@ hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, in
     a.k = k;
     a.m = m;
     a.ldy = ldy;
-    a.tiles_f = n / kTF;
-    a.tiles_t = (m + kTT - 1) / kTT;
+    a.tiles_f = n / TF;
+    a.tiles_t = tiles / a.tiles_f;
     a.group_f = a.tiles_f % kGroupF == 0 ? kGroupF : 1;
-    const int tiles = a.tiles_f * a.tiles_t;
-    a.xcd_per = tiles % 8 == 0 ? tiles / 8 : 0;
+    a.kt = k / p.split / kBK;
+    a.part = p.split == 2 ? (float *)ws->part : nullptr;
+    a.ticket = p.split == 2 ? ws->ticket : nullptr;
+    const int grid = tiles * p.split;
+    a.xcd_per = grid % 8 == 0 ? grid / 8 : 0;
     KernelSpan span(y_bf16 ? "gemm_mfma_out_bf16" : "gemm_mfma_out_f32", s, true);
-    if (y_bf16) launch(span, gemm_bf16_kernel<true, false, kStages>, dim3(tiles), dim3(256), 0, s, a);
-    else if (accumulate) launch(span, gemm_bf16_kernel<false, true, kStages>, dim3(tiles), dim3(256), 0, s, a);
-    else launch(span, gemm_bf16_kernel<false, false, kStages>, dim3(tiles), dim3(256), 0, s, a);
+    if (p.split == 2) launch_shape<2>(p.tile, a, grid, y_bf16, accumulate, s, span);
+    else launch_shape<1>(p.tile, a, grid, y_bf16, accumulate, s, span);
     return hipGetLastError();
 }
 

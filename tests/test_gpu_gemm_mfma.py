@@ -88,6 +88,37 @@ def test_mfma_gemm_forced(monkeypatch, hip_available, rows, cols, m):
     assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
 
 
+@pytest.mark.parametrize("tile", ["128x128", "256x128", "128x256", "192x128", "192x256"])
+@pytest.mark.parametrize("split", [1, 2])
+@pytest.mark.parametrize("cols,m", [(2048, 130), (6144, 257)])
+def test_mfma_gemm_tiles(monkeypatch, hip_available, tile, split, cols, m):
+    """Every workgroup tile, with and without the k split, on a width every
+    tile divides (768 = 3 x 256 = 4 x 192) and ragged token counts; a split
+    call gives the same bits on a second run (its halves meet in one
+    commutative addition)."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "mfma")
+    monkeypatch.setenv("HYMT_HIP_GEMM_TILE", tile + (",2" if split == 2 else ""))
+    out, counts, ref, mag, y0 = run_case(768, cols, m, 3000 + m + split, MFMA)
+    check(out, ref, mag, y0)
+    assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
+    if split == 2:
+        again, _, _, _, _ = run_case(768, cols, m, 3000 + m + split, MFMA)
+        for key in out:
+            assert np.array_equal(out[key], again[key]), key
+
+
+def test_mfma_gemm_default_plans(monkeypatch, hip_available):
+    """The shape rules' own choices at the model's shapes on a 512-row
+    prompt (the split 128 x 128 for q/k/v, o and down, 192 x 128 for
+    gate/up), against the fp64 product."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "mfma")
+    monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
+    for rows, cols in [(3072, 2048), (12288, 2048), (2048, 2048), (2048, 6144)]:
+        out, counts, ref, mag, y0 = run_case(rows, cols, 512, 4000 + rows + cols, MFMA)
+        check(out, ref, mag, y0)
+        assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
+
+
 def test_mfma_gemm_runs_and_falls_back(monkeypatch, hip_available):
     """Forced, the MFMA kernel serves every call its shape rules allow (the
     128-row range); a width that is not a multiple of 128 goes to hipBLASLt."""
