@@ -716,6 +716,12 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         f.out_bf16 = out_bf16;
         f.nb16 = (seq + 15) / 16;
         f.npairs = (f.nb16 + 1) / 2;
+        const int npages = (pos + seq + kPage - 1) / kPage;
+        f.pages_in_args = npages <= kArgPages;
+        if (f.pages_in_args) {
+            for (int b = 0; b < npages; b++) f.pages[b] = c->pages.phys(b);
+            for (int b = npages; b < kArgPages; b++) f.pages[b] = f.pages[npages - 1];
+        }
         // Work items: split the kv range of block pairs only when the (kv
         // head, pair) combinations fill less than half the GPU.  From half
         // up, the merge launch and its partials cost more than the idle CUs

@@ -487,7 +487,7 @@ constexpr float kLazy = 8.0f;
 // the 16 of its long block B (qq = 1); tiles past A's causal range run B
 // alone.  Tile pair j sits in LDS buffer j & 1 (one slot per parity); the
 // two halves' (m, l, O) are combined through LDS at the end.
-template <typename T, bool IN_BF16, int HK>
+template <typename T, bool IN_BF16, int HK, bool PAGES_ARG>
 __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // The arguments pass through one empty asm (scalars as outputs, pointers
     // as inputs, which keeps their global address space): the compiler then
@@ -566,7 +566,12 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     const int tab0 = a.tab[it.t0 + min(tid, nt - 1)];
     const int tab1 = a.tab[it.t0 + min(tid + 512, nt - 1)];
     const int half_u = __builtin_amdgcn_readfirstlane(half);
-    const int phys_first = __builtin_amdgcn_readfirstlane(a.tab[it.t0 + min(half_u, nt - 1)]);
+    // the page of this wave's first tile: from the argument list (a scalar
+    // load in the argument batch) when the host passes the pages there, so
+    // the first copy waits for no table load
+    int phys_first;
+    if constexpr (PAGES_ARG) phys_first = args.pages[min(it.t0 + min(half_u, nt - 1), kArgPages - 1)];
+    else phys_first = __builtin_amdgcn_readfirstlane(a.tab[it.t0 + min(half_u, nt - 1)]);
     QRaw<IN_BF16> raw;
     bool qok[2];
     q_load<IN_BF16>(a, h, rowq, okq, grp, c, raw, qok);
@@ -621,8 +626,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // One tile of this wave's parity for q blocks QQ0..1 (QQ0 = 0: both
     // blocks; QQ0 = 1: the long block alone).
     // nphys >= 0: the tile this wave stages next (into buffer buf ^ 1); its
-    // K page copy is issued after the S MFMAs, its V page copy after the
-    // softmax, so that the copies queue behind work instead of in one burst
+    // K page copy is issued before the S MFMAs, its V page copy after them,
+    // so that the copies queue behind work instead of in one burst (against
+    // K after S and V after the softmax: config 3's flash kernel 31.9 ->
+    // 30.7 us, interleaved runs on one box)
     auto tile_body = [&](auto qq0_tag, auto first_tag, int t, int buf, int nphys) {
         constexpr int QQ0 = decltype(qq0_tag)::value;
         constexpr bool first = decltype(first_tag)::value;
@@ -630,6 +637,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         const uint16_t *vt = sKV + (4 + buf * 2 + half) * KT + grp * 1024 + c * 8;
         // ---- S^T - m = K Q^T - m (64 kv x 16 q per block), accumulated onto
         // -m; the half's first tile starts from 0 and sets m from its scores
+        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 0);
         f32x4 sacc[4][2];
 #pragma unroll
         for (int qq = QQ0; qq < 2; qq++) {
@@ -648,7 +656,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         }
         lds_pipeline<QQ0>();
 
-        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 0);
+        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 1);
 
         // ---- online softmax (column c = q row); the causal mask only
         // touches tiles reaching past a block's first row ----
@@ -705,8 +713,6 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
             for (int qq = QQ0; qq < 2; qq++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) sacc[kb][qq][i] = __builtin_amdgcn_exp2f(sacc[kb][qq][i]);
-
-        if (nphys >= 0) fetch_page(nphys, buf ^ 1, 1);
 
         // ---- O^T += V^T P^T ----
 #pragma unroll
@@ -856,12 +862,16 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     }
 }
 
-template <typename T, bool IN_BF16> void launch_flash(const FlashArgs &a, dim3 grid, hipStream_t s) {
+template <typename T, bool IN_BF16, bool PA> void launch_flash_pa(const FlashArgs &a, dim3 grid, hipStream_t s) {
     const int hk = a.rope_half >> 5;
     KernelSpan span("prefill_flash", s, true);
-    if (hk == 2) launch(span, prefill_flash_kernel<T, IN_BF16, 2>, grid, dim3(512), 0, s, a);
-    else if (hk == 1) launch(span, prefill_flash_kernel<T, IN_BF16, 1>, grid, dim3(512), 0, s, a);
-    else launch(span, prefill_flash_kernel<T, IN_BF16, 0>, grid, dim3(512), 0, s, a);
+    if (hk == 2) launch(span, prefill_flash_kernel<T, IN_BF16, 2, PA>, grid, dim3(512), 0, s, a);
+    else if (hk == 1) launch(span, prefill_flash_kernel<T, IN_BF16, 1, PA>, grid, dim3(512), 0, s, a);
+    else launch(span, prefill_flash_kernel<T, IN_BF16, 0, PA>, grid, dim3(512), 0, s, a);
+}
+template <typename T, bool IN_BF16> void launch_flash(const FlashArgs &a, dim3 grid, hipStream_t s) {
+    if (a.pages_in_args) launch_flash_pa<T, IN_BF16, true>(a, grid, s);
+    else launch_flash_pa<T, IN_BF16, false>(a, grid, s);
 }
 
 hipError_t launch_prefill_flash(int kv_dtype, const FlashArgs &a, int total_items, hipStream_t s) {
