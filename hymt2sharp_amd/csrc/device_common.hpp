@@ -70,6 +70,15 @@ __device__ __forceinline__ void lds_dma16(const void *src, uint32_t lds_base) {
                  : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(src)
                  : "memory", "m0");
 }
+// The same copy addressed as a uniform base (an SGPR pair) plus a 32-bit
+// per-lane byte offset: the per-lane part stays in one VGPR across copies,
+// and a new base costs scalar instructions only.
+__device__ __forceinline__ void lds_dma16_sv(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(sbase)
+                 : "memory", "m0");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p;
 }

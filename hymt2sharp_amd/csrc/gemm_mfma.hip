@@ -99,17 +99,6 @@ __device__ __forceinline__ void wait_stages(int n) {
     }
 }
 
-// 16 bytes per lane from global memory straight into LDS, addressed as a
-// uniform base (SGPR pair) plus a 32-bit per-lane byte offset: lane i writes
-// LDS bytes lds_base + 16 i.  Inline assembly for the reason lds_dma16 gives
-// (device_common.hpp); m0 is written here and declared clobbered.
-__device__ __forceinline__ void lds_dma16_sv(const void *sbase, uint32_t voff, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(sbase)
-                 : "memory", "m0");
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void *base) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, 0x7fffffff, 0x00020000);
 }

@@ -510,7 +510,9 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     __shared__ __attribute__((aligned(16))) uint16_t sKV[8 * KT];
     __shared__ int32_t sTab[kItemTiles];  // physical pages of the item's tiles
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index is uniform: tile indices, the page ids and the branches
+    // on them stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hw = wave & 3, half = wave >> 2;
     const int grp = lane >> 4, c = lane & 15;
     const int Hkv = a.kv_heads;
@@ -543,11 +545,15 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // kernel, so whole pages are copied.
     const uint32_t lds_kv = __builtin_amdgcn_readfirstlane(lds_addr(sKV) + hw * 1024);
     // page 0 = K, 1 = V of the tile in physical page `phys`
+    // (the page base is uniform and goes in SGPRs; the lane's byte offset
+    // within each 4 KiB quarter is one VGPR for every copy)
+    const uint32_t dma_off = (hw * 64 + lane) * 16;
     auto fetch_page = [&](int phys, int buf, int page) __attribute__((always_inline)) {
-        const uint16_t *src = (page ? vpool : kpool) + ((size_t)phys * Hkv + kvh) * page_elems + (hw * 64 + lane) * 8;
+        const uint16_t *base =
+            (page ? vpool : kpool) + ((size_t)__builtin_amdgcn_readfirstlane(phys) * Hkv + kvh) * page_elems;
         const uint32_t dst = lds_kv + ((page ? 4 : 0) + buf * 2 + half) * KT * 2;
 #pragma unroll
-        for (int i = 0; i < 4; i++) lds_dma16(src + i * 2048, dst + i * 4096);
+        for (int i = 0; i < 4; i++) lds_dma16_sv(base + i * 2048, dma_off, dst + i * 4096);
     };
     auto fetch = [&](int phys, int buf) __attribute__((always_inline)) {
         fetch_page(phys, buf, 0);
