@@ -742,10 +742,14 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         lds_pipeline<QQ0>();
     };
 
-    // Tile pairs j < jA hold a tile of both blocks on parity 0 at least; from
-    // jA on the long block runs alone, in a loop of its own where the short
-    // block's q rows and scores are dead.
-    const int jA = min(max(0, lenA - it.t0 + 1) >> 1, (nt + 1) >> 1);
+    // nbA: the item's tiles (from t0) that hold both blocks (t < lenA).  Tile
+    // pairs j < nbA / 2 hold both blocks on both parities; when nbA is odd,
+    // pair nbA / 2 holds both on parity 0 and the long block alone on parity
+    // 1, and is peeled out of the loops, so that no loop joins the two forms
+    // (at such a join the compiler moved O between registers on every
+    // iteration); after it the long block runs alone, in a loop of its own
+    // where the short block's q rows and scores are dead.
+    const int nbA = min(max(0, lenA - it.t0), nt);
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
     using FT = std::integral_constant<bool, true>;
@@ -763,18 +767,27 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         __syncthreads();
     }
     int j = 1;
-    for (; j < jA; j++) {
+    for (; j < (nbA >> 1); j++) {
         const int buf = j & 1;
-        const int t = it.t0 + 2 * j + half;  // this wave's tile
+        const int t = it.t0 + 2 * j + half;  // this wave's tile: t < lenA and t < t1
         // tile t + 2 goes into the other buffer, which every wave finished
         // reading before the previous barrier
+        const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
+        tile_body(I0{}, FF{}, t, buf, nphys);
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
+        __syncthreads();
+    }
+    if ((nbA & 1) && j == (nbA >> 1)) {
+        const int buf = j & 1;
+        const int t = it.t0 + 2 * j + half;
         const int nphys = t + 2 < it.t1 ? sTab[t + 2 - it.t0] : -1;
         if (t < it.t1) {
             if (t < lenA) tile_body(I0{}, FF{}, t, buf, nphys);
             else tile_body(I1{}, FF{}, t, buf, nphys);
         }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t + 2 have landed
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        j++;
     }
     for (; 2 * j < nt; j++) {
         const int buf = j & 1;
