@@ -393,6 +393,116 @@ def time_gemv(reps=200, min_bytes=320 << 20):
     return out
 
 
+GEMM_SHAPES = [  # (name, n features, k, flags): the prefill GEMMs of the model (hidden 2048, FFN 6144)
+    ("qkv", 3072, 2048, "bf16"), ("o", 2048, 2048, "acc"), ("gate_up", 12288, 2048, "bf16"),
+    ("down", 2048, 6144, "acc"),
+]
+GEMM_TILES = ["128x128", "256x128", "128x256", "192x128", "192x256", "128x128,2", "128x256,2"]
+
+
+def time_gemm(ms=(512, 2048), reps=10, rounds=5):
+    """The prefill GEMMs y (+)= x W^T at the model's shapes: hipBLASLt's first
+    heuristic choice (the default), the hand-written MFMA kernel with its own
+    tile plan (HYMT_HIP_GEMM=mfma), and the MFMA kernel with each tile forced
+    (HYMT_HIP_GEMM_TILE).  HIP events around `reps` back-to-back calls on
+    the backend's stream, `rounds` rounds interleaving every candidate, the
+    median per candidate (one pass per candidate in turn let clock drift move
+    one kernel by 10-15 % between candidates); o and down accumulate into
+    fp32, q/k/v and gate/up write bf16 (as hymt_model_prefill calls them).
+    Each context reads HYMT_HIP_GEMM when its first GEMM makes its GEMM
+    state, so each mode gets a context of its own."""
+    out = {}
+    saved = {k: os.environ.get(k) for k in ("HYMT_HIP_GEMM", "HYMT_HIP_GEMM_TILE")}
+    bes = {}
+    try:
+        for mode in ("hipblaslt", "mfma"):
+            if mode == "mfma":
+                os.environ["HYMT_HIP_GEMM"] = "mfma"
+            else:
+                os.environ.pop("HYMT_HIP_GEMM", None)
+            os.environ.pop("HYMT_HIP_GEMM_TILE", None)
+            be = HipBackend(0)
+            bes[mode] = be
+            # the first GEMM makes the state under this mode
+            w0 = be.weight_upload(N.W_Q4_K, 128, 2048, S.random_weight(1, N.W_Q4_K, 128, 2048))
+            be.weight_dense(w0)
+            dx, dy = be.alloc(2048 * 2), be.alloc(128 * 4)
+            be.upload(dx, np.zeros(2048, np.uint16))
+            be.gemm(w0, dx, 1, dy)
+            be.sync()
+            be.free(dx)
+            be.free(dy)
+            be.weight_free(w0)
+        os.environ.pop("HYMT_HIP_GEMM", None)
+        for name, n, k, kind in GEMM_SHAPES:
+            raw = S.random_weight(S.seed(7, n, k), N.W_Q4_K, n, k)
+            ws = {}
+            bufs = {}
+            mmax = max(ms)
+            x = S.f32_to_bf16_bits(S.normal(S.seed(7, k, 1), (mmax, k), 1.0))
+            for mode, be in bes.items():
+                w = be.weight_upload(N.W_Q4_K, n, k, raw)
+                be.weight_dense(w)
+                dx = be.alloc(x.nbytes)
+                dy = be.alloc(mmax * n * (2 if kind == "bf16" else 4))
+                be.upload(dx, x)
+                be.upload(dy, np.zeros(mmax * n * (1 if kind == "bf16" else 2), np.uint16) if kind == "bf16"
+                          else np.zeros(mmax * n, np.float32))
+                ws[mode] = w
+                bufs[mode] = (dx, dy)
+
+            def run(mode, m, tile, calls):
+                be = bes[mode]
+                if tile is None:
+                    os.environ.pop("HYMT_HIP_GEMM_TILE", None)
+                else:
+                    os.environ["HYMT_HIP_GEMM_TILE"] = tile
+                dx, dy = bufs[mode]
+                ev = HipEvents(be.stream())
+                call = lambda: be.gemm(ws[mode], dx, m, dy, accumulate=kind == "acc", out_bf16=kind == "bf16")
+                call()
+                e0, e1 = ev.new(), ev.new()
+                ev.record(e0)
+                for _ in range(calls):
+                    call()
+                ev.record(e1)
+                us = ev.elapsed_ms(e0, e1) / calls * 1e3
+                ev.destroy(e0)
+                ev.destroy(e1)
+                os.environ.pop("HYMT_HIP_GEMM_TILE", None)
+                return us
+
+            for m in ms:
+                flop = 2.0 * n * k * m
+                cands = [("hipblaslt", None), ("mfma", None)] + [("mfma", t) for t in GEMM_TILES]
+                for c in cands:  # warm-up: every candidate once
+                    run(c[0], m, c[1], 2)
+                samples = {c: [] for c in cands}
+                for _ in range(rounds):  # interleaved, so clock drift weighs on all alike
+                    for c in cands:
+                        samples[c].append(run(c[0], m, c[1], reps))
+                med = {c: round(float(np.median(v)), 2) for c, v in samples.items()}
+                rec = {"n": n, "k": k, "m": m, "out": kind, "hipblaslt_us": med[("hipblaslt", None)],
+                       "mfma_plan_us": med[("mfma", None)],
+                       "mfma_tiles_us": {t: med[("mfma", t)] for t in GEMM_TILES}}
+                rec["hipblaslt_tflops"] = round(flop / (rec["hipblaslt_us"] * 1e-6) / 1e12, 1)
+                rec["mfma_plan_tflops"] = round(flop / (rec["mfma_plan_us"] * 1e-6) / 1e12, 1)
+                out[f"{name}_m{m}"] = rec
+            for mode, be in bes.items():
+                be.weight_free(ws[mode])
+                for b in bufs[mode]:
+                    be.free(b)
+    finally:
+        for be in bes.values():
+            be.Dispose()
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    return out
+
+
 def time_model(ctx=CTX, steps=20, warmup=3, kv_dtype=F16, prompt_len=2048, prefill_reps=5,
                cpu_tokens=0):
     """Whole decode step of the 32-layer hunyuan-dense model (synthetic Q4_K
@@ -796,11 +906,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv", "model", "ceilings"],
+    ap.add_argument("--only", choices=["decode", "prefill", "configs", "gemv", "gemm", "model", "ceilings"],
                     default=None,
                     help="run one leg: the config-2 decode step, the config-3 prefill, "
-                         "the other configurations (1, 4, 5), the weight GEMVs, the "
-                         "whole-model decode step or the measured ceilings")
+                         "the other configurations (1, 4, 5), the weight GEMVs, the prefill "
+                         "GEMMs, the whole-model decode step or the measured ceilings")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run 64 MiB device copies (counter calibration for profiles)")
     ap.add_argument("--no-spread", action="store_true",
@@ -857,6 +967,12 @@ def main():
         extra["gemv"] = {"workload": "decode weight GEMV y += W x (batch 1, fp32 x/y) at the "
                                      "decode step's shapes, W streamed from HBM",
                          "unit": "GB/s of GGUF weight bytes", "cases": time_gemv()}
+    if args.only in (None, "gemm"):
+        extra["gemm"] = {"workload": "prefill GEMMs y (+)= x W^T at the model's shapes (bf16 operands, "
+                                     "fp32 accumulation; o and down accumulate into fp32, q/k/v and "
+                                     "gate/up write bf16): hipBLASLt's first heuristic choice against "
+                                     "the hand-written MFMA kernel, its tile plan and each tile",
+                         "unit": "us per call", "shapes": time_gemm()}
     if args.only in (None, "ceilings"):
         extra["ceilings"] = measure_ceilings()
     if args.only in (None, "model"):
