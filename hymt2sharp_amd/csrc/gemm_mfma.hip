@@ -15,9 +15,9 @@
 // k advances in stages of 64: a stage is (TF + TT) / 16 row blocks of 2 KiB
 // (16 rows x 64 k; the W blocks first, then the x blocks), copied from global
 // memory straight into an LDS ring of S stages (global_load_lds_dwordx4).
-// Each copy instruction reads 8 whole 128-byte lines (8 rows x 64 k), and its
-// lanes take the 16-byte pieces of a row in an XOR order that places them in
-// LDS so that the operand reads are conflict-free.  The copy pattern sets the
+// Each copy instruction reads 8 whole 128-byte lines (8 rows x 64 k); the
+// rows' order and an XOR order of each row's 16-byte pieces place them in LDS
+// so that the operand reads are free of bank conflicts.  The copy pattern sets the
 // operand rate: on the o projection (2048^3) the 128 x 128 kernel took 36 us
 // with each instruction reading 16 rows x 64 bytes (the same half of 16
 // lines), 29 us with the halves alternating by row, and 25 us with whole
@@ -182,19 +182,22 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     const size_t kbase = (size_t)kz * kt * kBK;
 
     // Staging: wave w copies row blocks gb = NBW w + [0, NBW) (W blocks
-    // first, then x), one block's 2 KiB in two loads, each of 8 whole rows:
-    // load h takes rows 16 rb + 8 h + [0, 8), lane l row l >> 3 and the
-    // 16-byte piece (l & 7) ^ (l >> 3) ^ h of the row's 128-byte stage.  Each
-    // load reads 8 whole 128-byte lines, and lands in LDS slot l of the
-    // block's half h.  Row c of a block (i = c >> 3, r = c & 7) thus keeps
-    // piece p in slot 64 i + 8 r + (p ^ r ^ i); see the operand offsets below.
+    // first, then x), one block's 2 KiB in two loads, each of 8 whole rows.
+    // The block's 16 slot groups of 128 bytes hold its rows in the order
+    // 0, 8, 1, 9, ..., 7, 15: group a = 8 h + (l >> 3) of load h holds row
+    // (a >> 1) + 8 (a & 1), lane l taking that row's 16-byte piece
+    // (l & 7) ^ (a >> 1) and landing in LDS slot l of the block's half h.
+    // Each load reads 8 whole 128-byte lines.  Row c of a block (i = c >> 3,
+    // r = c & 7) thus keeps piece p in slot 16 r + 8 i + (p ^ r); see the
+    // operand offsets below.
     uint32_t voff[C];
     const uint16_t *sbase[C];
 #pragma unroll
     for (int j = 0; j < C; j++) {
         const int gb = wave * NBW + (j >> 1), h = j & 1;
-        const int rl = 8 * h + (lane >> 3);
-        const int piece = (lane & 7) ^ (lane >> 3) ^ h;
+        const int ga = 8 * h + (lane >> 3);
+        const int rl = (ga >> 1) + 8 * (ga & 1);
+        const int piece = (lane & 7) ^ (ga >> 1);
         const bool isw = gb < NBF;
         const int row = isw ? f0 + 16 * gb + rl : min(t0 + 16 * (gb - NBF) + rl, a.m - 1);
         voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
@@ -208,14 +211,17 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
         for (int j = 0; j < C; j++) lds_dma16_sv(sbase[j] + kk, voff[j], dst + j * kFrag);
     };
     // Operand reads: lane (grp, c) takes row c, k 8 grp + [0, 8) of k step
-    // ks, i.e. piece 4 ks + grp, at byte off[ks] of each row block.  The 16
-    // lanes of one grp hit 16 distinct slots mod 16 (and any 8 consecutive
-    // ones distinct slots mod 8), so the reads are free of bank conflicts.
+    // ks, i.e. piece 4 ks + grp, at byte off[ks] of each row block.  A
+    // 16-byte read of 16 lanes takes one LDS pass on gfx950 when lanes 0-7
+    // fall in one 128-byte half of a 256-byte bank row and lanes 8-15 in the
+    // other, each 8 on distinct 16-byte slots of their half: rows 0-7 sit in
+    // even slot groups at slot p ^ r, rows 8-15 in odd ones
+    // (SQ_LDS_BANK_CONFLICT reads 0; 4 cycles per read with rows in order).
     uint32_t off[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
         const int i = c >> 3, r = c & 7;
-        off[ks] = 16 * (64 * i + 8 * r + ((4 * ks + grp) ^ r ^ i));
+        off[ks] = 16 * (16 * r + 8 * i + ((4 * ks + grp) ^ r));
     }
 
     const int wf = wave & 1, wt = wave >> 1;
@@ -240,26 +246,27 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < JT; j++) ax[j] = *(const bf16x8 *)(lds + off[0] + (NBF + JT * wt + j) * kPair);
 
-    for (int s = 0; s < kt; s++) {
-        const uint8_t *sb = lds + (s % S) * kStageBytes;
+    // The last stage is peeled: with its branch inside the loop, the
+    // accumulators of the two paths met at the loop's join and the compiler
+    // staged every MFMA's accumulator input through one register quad (four
+    // v_accvgpr_mov_b32 per MFMA, 60 a stage at 128 x 128).
+    for (int s = 0; s < kt - 1; s++) {
         // step (s, 0): its operands in (w, ax); read step (s, 1) into (w, bx)
-        substep<IF, JT>(w, ax, sb, off[1], wf, wt, bx, acc);
-        if (s + 1 < kt) {
-            // stage s + 1 landed: stages up to s - 1 + AHEAD are issued, and
-            // min(AHEAD - 2, kt - 2 - s) of them may stay in flight
-            wait_stages<C, AHEAD - 2, LGKM>(kt - 2 - s);
-            asm volatile("s_barrier" ::: "memory");
-            if (s + AHEAD < kt) issue(s + AHEAD);
-            // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax)
-            substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc);
-        } else {
-#pragma unroll
-            for (int i = 0; i < IF; i++)
-#pragma unroll
-                for (int j = 0; j < JT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], bx[j], acc[i][j], 0, 0, 0);
-        }
+        substep<IF, JT>(w, ax, lds + (s % S) * kStageBytes, off[1], wf, wt, bx, acc);
+        // stage s + 1 landed: stages up to s - 1 + AHEAD are issued, and
+        // min(AHEAD - 2, kt - 2 - s) of them may stay in flight
+        wait_stages<C, AHEAD - 2, LGKM>(kt - 2 - s);
+        asm volatile("s_barrier" ::: "memory");
+        if (s + AHEAD < kt) issue(s + AHEAD);
+        // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax)
+        substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc);
     }
+    substep<IF, JT>(w, ax, lds + ((kt - 1) % S) * kStageBytes, off[1], wf, wt, bx, acc);
+#pragma unroll
+    for (int i = 0; i < IF; i++)
+#pragma unroll
+        for (int j = 0; j < JT; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], bx[j], acc[i][j], 0, 0, 0);
 
     if constexpr (SPLIT == 2) {
         // Ticket values of a tile within one call: the first arrival takes
@@ -388,13 +395,14 @@ int gemm_tile_by_name(const char *name) {
 }
 
 // The tile plan for a shape.  Measured at m = 2048 (us per call, this kernel
-// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 33.4
-// (128 x 128 42.7) / 28.7; gate/up 12288 x 2048 192 x 256 113.7 (128 x 128
-// 149) / 87.0; o 2048 x 2048 128 x 128 31.7 (split 128 x 256 34.3) / 24.6;
-// down 2048 x 6144 split 128 x 256 69.8 (128 x 128 78.2) / 54.9.  So: the
+// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 31.1
+// (128 x 128 39.7) / 28.6; gate/up 12288 x 2048 192 x 256 104 (128 x 128
+// 125) / 86.5; o 2048 x 2048 128 x 128 25.2 (split 128 x 256 32.8) / 24.7;
+// down 2048 x 6144 128 x 128 60 (split 128 x 256 65.8) / 55.8.  So: the
 // widest tile that still gives the chip 1.5 rounds of workgroups, 192 rows
-// where the width allows; a k split when one round of 128 x 128 tiles holds
-// every output and k is deep enough (>= 4096) to pay for the handoff.
+// where the width allows; a k split of 128 x 128 tiles when their one round
+// fills at most half the chip (a short prompt: at m = 512 o 16.5 against
+// 20.4 us unsplit, down 32.4 against 50.3).
 GemmPlan gemm_mfma_plan(int n, int k, int m) {
     // forced by HYMT_HIP_GEMM_TILE=<tile>[,2] (a tuning knob; the shape rules
     // still apply)
@@ -416,8 +424,6 @@ GemmPlan gemm_mfma_plan(int n, int k, int m) {
         if (tiles_of(4, n, m) * 2 >= 3 * kCUs) return GemmPlan{4, 1};
         if (tiles_of(3, n, m) * 4 >= 3 * kCUs) return GemmPlan{3, 1};
     }
-    if (tiles_of(0, n, m) <= kCUs && tiles_of(2, n, m) * 2 > kCUs / 2 && k >= 4096 && k % 256 == 0)
-        return GemmPlan{2, 2};
     if (tiles_of(0, n, m) <= kCUs / 2 && k % 256 == 0) return GemmPlan{0, 2};  // a short prompt
     return GemmPlan{0, 1};
 }
