@@ -81,24 +81,6 @@ struct GemmArgs {
 #define HYMT_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 #define HYMT_WAIT_VM_L(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4))
 
-// Wait until at most C min(n, MAXN) of a wave's copies are outstanding (with
-// LGKM, its LDS reads done too): one straight-line s_waitcnt per branch, the
-// common case (n >= MAXN) first.
-template <int C, int MAXN, bool LGKM>
-__device__ __forceinline__ void wait_stages(int n) {
-    if constexpr (MAXN > 0) {
-        if (n >= MAXN) {
-            if constexpr (LGKM) HYMT_WAIT_VM_L(C * MAXN);
-            else HYMT_WAIT_VM(C * MAXN);
-            return;
-        }
-        wait_stages<C, MAXN - 1, LGKM>(n);
-    } else {
-        if constexpr (LGKM) HYMT_WAIT_VM_L(0);
-        else HYMT_WAIT_VM(0);
-    }
-}
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(const void *base) {
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, 0, 0x7fffffff, 0x00020000);
 }
@@ -124,11 +106,12 @@ __device__ __forceinline__ void tile_of(const GemmArgs &a, int b, int &tile, int
 // row by row, with the operand reads of the next step (LDS at nsb + noff,
 // this lane's bytes) interleaved: W fragment i of the next step replaces w[i]
 // as soon as row i's MFMAs have issued, and the x fragments go to nx, so a
-// wave holds IF + 2 JT fragments (a 256 x 256 tile's 128 x 128 wave tile
-// fits beside its 256 accumulators).
-template <int IF, int JT>
+// wave holds IF + 2 JT fragments.  after_row(i) runs after row i's reads
+// (the stage copies spread over the step).
+template <int IF, int JT, typename F>
 __device__ __forceinline__ void substep(bf16x8 (&w)[IF], const bf16x8 (&cx)[JT], const uint8_t *nsb,
-                                        uint32_t noff, int wf, int wt, bf16x8 (&nx)[JT], f32x4 (&acc)[IF][JT]) {
+                                        uint32_t noff, int wf, int wt, bf16x8 (&nx)[JT], f32x4 (&acc)[IF][JT],
+                                        F &&after_row) {
     constexpr int NBF = 2 * IF;  // W row blocks of a stage
 #pragma unroll
     for (int i = 0; i < IF; i++) {
@@ -139,6 +122,7 @@ __device__ __forceinline__ void substep(bf16x8 (&w)[IF], const bf16x8 (&cx)[JT],
 #pragma unroll
         for (int j = i * JT / IF; j < (i + 1) * JT / IF; j++)
             nx[j] = *(const bf16x8 *)(nsb + noff + (NBF + JT * wt + j) * kPair);
+        after_row(i);
     }
     if constexpr (JT >= IF) {
 #pragma unroll
@@ -204,12 +188,37 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
         sbase[j] = (isw ? a.W : a.x) + kbase;
     }
     const uint32_t lds0 = lds_addr(lds) + wave * NBW * kPair;
-    auto issue = [&](int s) {
-        const uint32_t dst = lds0 + (s % S) * kStageBytes;
-        const int kk = s * kBK;
-#pragma unroll
-        for (int j = 0; j < C; j++) lds_dma16_sv(sbase[j] + kk, voff[j], dst + j * kFrag);
+    // copy j of stage t into its ring slot t % S.  Stages past the last
+    // (t >= kt) copy the last stage's rows again: their slots are never read
+    // (a stage t >= kt shares its slot only with stages >= kt, or, with LGKM,
+    // with the one stage whose reads ended before the barrier it follows), and
+    // every iteration then issues C copies, so every wait below is the
+    // steady-state count and the loop has no branch.
+    auto copy = [&](int t, int j) __attribute__((always_inline)) {
+        lds_dma16_sv(sbase[j] + min(t, kt - 1) * kBK, voff[j], lds0 + (t % S) * kStageBytes + j * kFrag);
     };
+    // A stage's copies are spread over the MFMA rows of two steps: copies
+    // [0, CB) in the step after the barrier that frees its slot, [CB, C) in
+    // the next one.  Issued back to back after the barrier, the 4 waves' C
+    // copies each held their wave for about 50 cycles a copy (the copy path
+    // taking about 12 cycles per 1 KiB copy of the CU), and the MFMAs
+    // waited.
+    // With two stages ahead (AHEAD = 2) the wait right after the next step
+    // lands the stage, so all its copies go in the step after the barrier.
+    constexpr int CB = AHEAD > 2 ? (C + 1) / 2 : C;
+    auto first_half = [&](int t) __attribute__((always_inline)) {
+        return [&, t](int i) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = i * CB / IF; j < (i + 1) * CB / IF; j++) copy(t, j);
+        };
+    };
+    auto second_half = [&](int t) __attribute__((always_inline)) {
+        return [&, t](int i) __attribute__((always_inline)) {
+#pragma unroll
+            for (int j = CB + i * (C - CB) / IF; j < CB + (i + 1) * (C - CB) / IF; j++) copy(t, j);
+        };
+    };
+    auto no_copy = [](int) {};
     // Operand reads: lane (grp, c) takes row c, k 8 grp + [0, 8) of k step
     // ks, i.e. piece 4 ks + grp, at byte off[ks] of each row block.  A
     // 16-byte read of 16 lanes takes one LDS pass on gfx950 when lanes 0-7
@@ -233,12 +242,15 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
 
     // kt >= 2.  A wave's copies (C a stage) retire in order, so a wait for at
     // most C n outstanding copies lands all but the last n stages issued.
-    // Each wait is one straight-line s_waitcnt: choosing the count through a
-    // switch compiled to a branch tree that cost 5-10 % of the kernel.
+    // The prologue issues stages [0, AHEAD - 1) and the first half of stage
+    // AHEAD - 1, whose second half the first step issues.
 #pragma unroll
-    for (int s = 0; s < AHEAD; s++)
-        if (s < kt) issue(s);
-    wait_stages<C, AHEAD - 1, false>(kt - 1);
+    for (int t = 0; t < AHEAD - 1; t++)
+#pragma unroll
+        for (int j = 0; j < C; j++) copy(t, j);
+#pragma unroll
+    for (int j = 0; j < CB; j++) copy(AHEAD - 1, j);
+    HYMT_WAIT_VM(C * (AHEAD - 2) + CB);
     asm volatile("s_barrier" ::: "memory");
     bf16x8 w[IF], ax[JT], bx[JT];
 #pragma unroll
@@ -251,22 +263,25 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     // staged every MFMA's accumulator input through one register quad (four
     // v_accvgpr_mov_b32 per MFMA, 60 a stage at 128 x 128).
     for (int s = 0; s < kt - 1; s++) {
-        // step (s, 0): its operands in (w, ax); read step (s, 1) into (w, bx)
-        substep<IF, JT>(w, ax, lds + (s % S) * kStageBytes, off[1], wf, wt, bx, acc);
+        // step (s, 0): its operands in (w, ax); read step (s, 1) into (w, bx);
+        // the second half of stage s - 1 + AHEAD
+        substep<IF, JT>(w, ax, lds + (s % S) * kStageBytes, off[1], wf, wt, bx, acc, second_half(s - 1 + AHEAD));
         // stage s + 1 landed: stages up to s - 1 + AHEAD are issued, and
-        // min(AHEAD - 2, kt - 2 - s) of them may stay in flight
-        wait_stages<C, AHEAD - 2, LGKM>(kt - 2 - s);
+        // AHEAD - 2 of them may stay in flight
+        if constexpr (LGKM) HYMT_WAIT_VM_L(C * (AHEAD - 2));
+        else HYMT_WAIT_VM(C * (AHEAD - 2));
         asm volatile("s_barrier" ::: "memory");
-        if (s + AHEAD < kt) issue(s + AHEAD);
-        // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax)
-        substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc);
+        // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax);
+        // the first half of stage s + AHEAD
+        substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc, first_half(s + AHEAD));
     }
-    substep<IF, JT>(w, ax, lds + ((kt - 1) % S) * kStageBytes, off[1], wf, wt, bx, acc);
+    substep<IF, JT>(w, ax, lds + ((kt - 1) % S) * kStageBytes, off[1], wf, wt, bx, acc, no_copy);
 #pragma unroll
     for (int i = 0; i < IF; i++)
 #pragma unroll
         for (int j = 0; j < JT; j++)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], bx[j], acc[i][j], 0, 0, 0);
+    HYMT_WAIT_VM(0);  // the copies past the last stage have landed before the ring is reused or freed
 
     if constexpr (SPLIT == 2) {
         // Ticket values of a tile within one call: the first arrival takes
