@@ -102,6 +102,17 @@ __device__ __forceinline__ void tile_of(const GemmArgs &a, int b, int &tile, int
     tf = g * a.group_f + (r - tt * a.group_f);
 }
 
+// The schedule of a step, row by row: row i's JT MFMAs, then its reads (W
+// fragment i and the x fragments the row loads).
+template <int IF, int JT, int I>
+__device__ __forceinline__ void sched_rows() {
+    if constexpr (I < IF) {
+        __builtin_amdgcn_sched_group_barrier(0x008, JT, 0);                                   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1 + (I + 1) * JT / IF - I * JT / IF, 0);  // DS read
+        sched_rows<IF, JT, I + 1>();
+    }
+}
+
 // One 32-k step of a wave: the IF x JT MFMAs of the operands in (w, cx),
 // row by row, with the operand reads of the next step (LDS at nsb + noff,
 // this lane's bytes) interleaved: W fragment i of the next step replaces w[i]
@@ -124,35 +135,27 @@ __device__ __forceinline__ void substep(bf16x8 (&w)[IF], const bf16x8 (&cx)[JT],
             nx[j] = *(const bf16x8 *)(nsb + noff + (NBF + JT * wt + j) * kPair);
         after_row(i);
     }
-    if constexpr (JT >= IF) {
-#pragma unroll
-        for (int i = 0; i < IF; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, JT, 0);            // row i's MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, 1 + JT / IF, 0);   // its reads
-        }
-    } else {
-#pragma unroll
-        for (int g = 0; g < JT; g++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, IF, 0);            // IF / JT rows' MFMAs
-            __builtin_amdgcn_sched_group_barrier(0x100, IF / JT + 1, 0);   // their reads
-        }
-    }
+    sched_rows<IF, JT, 0>();
 }
 
-// The 4 waves' MFMAs of a tile (IF x JT 16 x 16 blocks per wave) over the
-// workgroup's k range.  S stages in the LDS ring; LGKM: a stage's slot is
+// The MFMAs of a tile over the workgroup's k range by 2 x WT waves: wave
+// (wf, wt) takes the tile's feature half wf and token part wt, IF x BJ
+// 16 x 16 blocks (WT = 2: one wave per SIMD; WT = 4: two, each with half the
+// accumulators, for tiles whose 4-wave accumulators and operands would not
+// fit a wave's 256 VGPRs).  S stages in the LDS ring; LGKM: a stage's slot is
 // refilled at the barrier right after its last operand reads (each wave first
 // waits for its own reads: lgkmcnt(0)), so S - 1 stages are ahead of the one
 // being read; else one barrier later, with S - 2 stages ahead and no wait on
 // the reads.
-template <int IF, int JT, int S, bool LGKM, int SPLIT, bool YBF16, bool ACC>
-__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
+template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT, bool YBF16, bool ACC>
+__global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
     constexpr int TF = 32 * IF, TT = 32 * JT;
-    constexpr int NBF = TF / 16, NB = (TF + TT) / 16, NBW = NB / 4;  // row blocks: W, all, per wave
-    constexpr int C = 2 * NBW;                                         // copy instructions per wave per stage
+    constexpr int NW = 2 * WT, NT = 64 * NW, BJ = TT / (16 * WT);  // waves, threads, token blocks per wave
+    constexpr int NBF = TF / 16, NB = (TF + TT) / 16;               // row blocks: W, all
+    constexpr int C = 2 * NB / NW;                                   // copy instructions per wave per stage
     constexpr int kStageBytes = NB * kPair;
     constexpr int AHEAD = LGKM ? S : S - 1;  // stages issued ahead of the one being read, plus one
-    static_assert(NB % 4 == 0 && AHEAD >= 2 && C * (AHEAD - 1) <= 63, "tile shape");
+    static_assert((2 * NB) % NW == 0 && BJ >= 1 && AHEAD >= 2 && C * (AHEAD - 1) <= 63, "tile shape");
     static_assert(S * kStageBytes <= 160 * 1024, "LDS");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * kStageBytes];
     unsigned &s_role = *(unsigned *)lds;  // split role, once the ring is idle
@@ -165,8 +168,9 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     const int kt = a.kt;
     const size_t kbase = (size_t)kz * kt * kBK;
 
-    // Staging: wave w copies row blocks gb = NBW w + [0, NBW) (W blocks
-    // first, then x), one block's 2 KiB in two loads, each of 8 whole rows.
+    // Staging: wave w issues loads g = C w + [0, C) of a stage, load g the
+    // half h = g & 1 of row block gb = g >> 1 (W blocks first, then x): a
+    // block's 2 KiB in two loads, each of 8 whole rows.
     // The block's 16 slot groups of 128 bytes hold its rows in the order
     // 0, 8, 1, 9, ..., 7, 15: group a = 8 h + (l >> 3) of load h holds row
     // (a >> 1) + 8 (a & 1), lane l taking that row's 16-byte piece
@@ -178,7 +182,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     const uint16_t *sbase[C];
 #pragma unroll
     for (int j = 0; j < C; j++) {
-        const int gb = wave * NBW + (j >> 1), h = j & 1;
+        const int g = wave * C + j, gb = g >> 1, h = g & 1;
         const int ga = 8 * h + (lane >> 3);
         const int rl = (ga >> 1) + 8 * (ga & 1);
         const int piece = (lane & 7) ^ (ga >> 1);
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
         voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
         sbase[j] = (isw ? a.W : a.x) + kbase;
     }
-    const uint32_t lds0 = lds_addr(lds) + wave * NBW * kPair;
+    const uint32_t lds0 = lds_addr(lds) + wave * C * kFrag;
     // copy j of stage t into its ring slot t % S.  Stages past the last
     // (t >= kt) copy the last stage's rows again: their slots are never read
     // (a stage t >= kt shares its slot only with stages >= kt, or, with LGKM,
@@ -234,11 +238,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     }
 
     const int wf = wave & 1, wt = wave >> 1;
-    f32x4 acc[IF][JT];
+    f32x4 acc[IF][BJ];
 #pragma unroll
     for (int i = 0; i < IF; i++)
 #pragma unroll
-        for (int j = 0; j < JT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < BJ; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // kt >= 2.  A wave's copies (C a stage) retire in order, so a wait for at
     // most C n outstanding copies lands all but the last n stages issued.
@@ -252,11 +256,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     for (int j = 0; j < CB; j++) copy(AHEAD - 1, j);
     HYMT_WAIT_VM(C * (AHEAD - 2) + CB);
     asm volatile("s_barrier" ::: "memory");
-    bf16x8 w[IF], ax[JT], bx[JT];
+    bf16x8 w[IF], ax[BJ], bx[BJ];
 #pragma unroll
     for (int i = 0; i < IF; i++) w[i] = *(const bf16x8 *)(lds + off[0] + (IF * wf + i) * kPair);
 #pragma unroll
-    for (int j = 0; j < JT; j++) ax[j] = *(const bf16x8 *)(lds + off[0] + (NBF + JT * wt + j) * kPair);
+    for (int j = 0; j < BJ; j++) ax[j] = *(const bf16x8 *)(lds + off[0] + (NBF + BJ * wt + j) * kPair);
 
     // The last stage is peeled: with its branch inside the loop, the
     // accumulators of the two paths met at the loop's join and the compiler
@@ -265,7 +269,7 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
     for (int s = 0; s < kt - 1; s++) {
         // step (s, 0): its operands in (w, ax); read step (s, 1) into (w, bx);
         // the second half of stage s - 1 + AHEAD
-        substep<IF, JT>(w, ax, lds + (s % S) * kStageBytes, off[1], wf, wt, bx, acc, second_half(s - 1 + AHEAD));
+        substep<IF, BJ>(w, ax, lds + (s % S) * kStageBytes, off[1], wf, wt, bx, acc, second_half(s - 1 + AHEAD));
         // stage s + 1 landed: stages up to s - 1 + AHEAD are issued, and
         // AHEAD - 2 of them may stay in flight
         if constexpr (LGKM) HYMT_WAIT_VM_L(C * (AHEAD - 2));
@@ -273,13 +277,13 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
         asm volatile("s_barrier" ::: "memory");
         // step (s, 1): operands in (w, bx); read step (s + 1, 0) into (w, ax);
         // the first half of stage s + AHEAD
-        substep<IF, JT>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc, first_half(s + AHEAD));
+        substep<IF, BJ>(w, bx, lds + ((s + 1) % S) * kStageBytes, off[0], wf, wt, ax, acc, first_half(s + AHEAD));
     }
-    substep<IF, JT>(w, ax, lds + ((kt - 1) % S) * kStageBytes, off[1], wf, wt, bx, acc, no_copy);
+    substep<IF, BJ>(w, ax, lds + ((kt - 1) % S) * kStageBytes, off[1], wf, wt, bx, acc, no_copy);
 #pragma unroll
     for (int i = 0; i < IF; i++)
 #pragma unroll
-        for (int j = 0; j < JT; j++)
+        for (int j = 0; j < BJ; j++)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[i], bx[j], acc[i][j], 0, 0, 0);
     HYMT_WAIT_VM(0);  // the copies past the last stage have landed before the ring is reused or freed
 
@@ -297,11 +301,11 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < IF; i++)
 #pragma unroll
-                for (int j = 0; j < JT; j++) {
+                for (int j = 0; j < BJ; j++) {
                     const f32x4 v = acc[i][j];
                     const u32x4 u = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
                                      __float_as_uint(v[3])};
-                    __builtin_amdgcn_raw_buffer_store_b128(u, pr, ((i * JT + j) * 256 + tid) * 16, 0, kSc1);
+                    __builtin_amdgcn_raw_buffer_store_b128(u, pr, ((i * BJ + j) * NT + tid) * 16, 0, kSc1);
                 }
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0);  // every store acknowledged
@@ -326,12 +330,12 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
         const bool ok = s_role == 3u;
 #pragma unroll
         for (int i = 0; i < IF; i++) {
-            u32x4 p[JT];
+            u32x4 p[BJ];
 #pragma unroll
-            for (int j = 0; j < JT; j++)
-                p[j] = __builtin_amdgcn_raw_buffer_load_b128(pr, ((i * JT + j) * 256 + tid) * 16, 0, kSc1);
+            for (int j = 0; j < BJ; j++)
+                p[j] = __builtin_amdgcn_raw_buffer_load_b128(pr, ((i * BJ + j) * NT + tid) * 16, 0, kSc1);
 #pragma unroll
-            for (int j = 0; j < JT; j++) {
+            for (int j = 0; j < BJ; j++) {
                 f32x4 v = acc[i][j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) v[e] = ok ? v[e] + __uint_as_float(p[j][e]) : __builtin_nanf("");
@@ -342,8 +346,8 @@ __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs a) {
 
     // epilogue: lane (grp, c) of block (i, j) holds features f .. f + 3 of token t
 #pragma unroll
-    for (int j = 0; j < JT; j++) {
-        const int t = t0 + (TT / 2) * wt + 16 * j + c;
+    for (int j = 0; j < BJ; j++) {
+        const int t = t0 + (TT / WT) * wt + 16 * j + c;
         if (t >= a.m) continue;
 #pragma unroll
         for (int i = 0; i < IF; i++) {
@@ -374,11 +378,12 @@ struct TileShape {
 constexpr TileShape kTiles[kGemmTiles] = {
     {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}};
 
-template <int IF, int JT, int S, bool LGKM, int SPLIT>
+template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT>
 void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span) {
-    if (y_bf16) launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, true, false>, dim3(grid), dim3(256), 0, s, a);
-    else if (acc) launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, false, true>, dim3(grid), dim3(256), 0, s, a);
-    else launch(span, gemm_kernel<IF, JT, S, LGKM, SPLIT, false, false>, dim3(grid), dim3(256), 0, s, a);
+    const dim3 block(128 * WT);
+    if (y_bf16) launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, true, false>, dim3(grid), block, 0, s, a);
+    else if (acc) launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, false, true>, dim3(grid), block, 0, s, a);
+    else launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, false, false>, dim3(grid), block, 0, s, a);
 }
 
 // Ring depths, measured at the model's shapes: deeper rings (128 x 128 with 5
@@ -387,11 +392,14 @@ template <int SPLIT>
 void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s,
                   const KernelSpan &span) {
     switch (tile) {
-    case 0: launch_tile<4, 4, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 32 KiB stages
-    case 1: launch_tile<8, 4, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
-    case 2: launch_tile<4, 8, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
-    case 3: launch_tile<6, 4, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB
-    default: launch_tile<6, 8, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 56 KiB
+    case 0: launch_tile<4, 4, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 32 KiB stages
+    case 1: launch_tile<8, 4, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
+    case 2: launch_tile<4, 8, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
+    case 3: launch_tile<6, 4, 2, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB
+    // 8 waves: 4 waves' 192 accumulators and operands each need more than
+    // 256 VGPRs (the loop then moved accumulators through AGPRs); gate/up
+    // at m = 2048 108 -> 94 us.  An 8-wave 256 x 256 tile took 105 us.
+    default: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 56 KiB
     }
 }
 
