@@ -395,10 +395,12 @@ void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, 
     case 0: launch_tile<4, 4, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 32 KiB stages
     case 1: launch_tile<8, 4, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
     case 2: launch_tile<4, 8, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
-    case 3: launch_tile<6, 4, 2, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB
+    case 3: launch_tile<6, 4, 4, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB, 8 waves
     // 8 waves: 4 waves' 192 accumulators and operands each need more than
     // 256 VGPRs (the loop then moved accumulators through AGPRs); gate/up
-    // at m = 2048 108 -> 94 us.  An 8-wave 256 x 256 tile took 105 us.
+    // at m = 2048 108 -> 94 us.  An 8-wave 256 x 256 tile took 105 us.  At
+    // 192 x 128 8 waves gain 1-3 % (q/k/v at m = 2048, gate/up at 512); at
+    // 128 x 128 they were mixed (down at m = 2048 2 % slower).
     default: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 56 KiB
     }
 }
