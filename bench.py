@@ -397,7 +397,7 @@ GEMM_SHAPES = [  # (name, n features, k, flags): the prefill GEMMs of the model 
     ("qkv", 3072, 2048, "bf16"), ("o", 2048, 2048, "acc"), ("gate_up", 12288, 2048, "bf16"),
     ("down", 2048, 6144, "acc"),
 ]
-GEMM_TILES = ["128x128", "256x128", "128x256", "192x128", "192x256", "128x128,2", "128x256,2"]
+GEMM_TILES = ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64", "128x128,2", "128x256,2", "128x64,2"]
 
 
 def time_gemm(ms=(512, 2048), reps=10, rounds=5):

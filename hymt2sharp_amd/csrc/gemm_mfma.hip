@@ -376,7 +376,7 @@ struct TileShape {
     int IF, JT;
 };
 constexpr TileShape kTiles[kGemmTiles] = {
-    {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}};
+    {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}, {"128x64", 4, 2}};
 
 template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT>
 void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span) {
@@ -401,7 +401,12 @@ void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, 
     // at m = 2048 108 -> 94 us.  An 8-wave 256 x 256 tile took 105 us.  At
     // 192 x 128 8 waves gain 1-3 % (q/k/v at m = 2048, gate/up at 512); at
     // 128 x 128 they were mixed (down at m = 2048 2 % slower).
-    default: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 56 KiB
+    case 4: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 56 KiB
+    // 128 x 64: short prompts, where 128 x 128 tiles leave a quarter of the
+    // chip idle (at m = 512, split: o 11.4 against 15.0 us for 128 x 128 split,
+    // down 22.9 against 28.1, q/k/v unsplit 13.3 against 15.3); a 192 x 64
+    // tile was slower at every model shape
+    default: launch_tile<4, 2, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break; // 24 KiB
     }
 }
 
@@ -420,14 +425,15 @@ int gemm_tile_by_name(const char *name) {
 }
 
 // The tile plan for a shape.  Measured at m = 2048 (us per call, this kernel
-// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 31.1
-// (128 x 128 39.7) / 28.6; gate/up 12288 x 2048 192 x 256 104 (128 x 128
-// 125) / 86.5; o 2048 x 2048 128 x 128 25.2 (split 128 x 256 32.8) / 24.7;
-// down 2048 x 6144 128 x 128 60 (split 128 x 256 65.8) / 55.8.  So: the
-// widest tile that still gives the chip 1.5 rounds of workgroups, 192 rows
-// where the width allows; a k split of 128 x 128 tiles when their one round
-// fills at most half the chip (a short prompt: at m = 512 o 16.5 against
-// 20.4 us unsplit, down 32.4 against 50.3).
+// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 27.4
+// (128 x 128 34.9) / 28.1; gate/up 12288 x 2048 192 x 256 90.6 (128 x 128
+// 113) / 83.6; o 2048 x 2048 128 x 128 22.5 (split 128 x 256 29.9) / 24.0;
+// down 2048 x 6144 128 x 128 50.3 (split 128 x 256 56.0) / 53.4; at m = 512
+// q/k/v 128 x 64 13.3 / 13.0, o 128 x 64 split 11.4 / 11.6, gate/up 192 x 128
+// 27.4 / 28.2, down 128 x 64 split 22.9 / 26.6.  So: the widest tile that
+// gives the chip about 1.5 rounds of workgroups, 192 rows where the width
+// allows; 128 x 128 while its one round fills three quarters of the chip;
+// else 128 x 64, its k split when its tiles fill at most half.
 GemmPlan gemm_mfma_plan(int n, int k, int m) {
     // forced by HYMT_HIP_GEMM_TILE=<tile>[,2] (a tuning knob; the shape rules
     // still apply)
@@ -449,8 +455,9 @@ GemmPlan gemm_mfma_plan(int n, int k, int m) {
         if (tiles_of(4, n, m) * 2 >= 3 * kCUs) return GemmPlan{4, 1};
         if (tiles_of(3, n, m) * 4 >= 3 * kCUs) return GemmPlan{3, 1};
     }
-    if (tiles_of(0, n, m) <= kCUs / 2 && k % 256 == 0) return GemmPlan{0, 2};  // a short prompt
-    return GemmPlan{0, 1};
+    if (tiles_of(0, n, m) * 4 >= 3 * kCUs) return GemmPlan{0, 1};
+    if (tiles_of(5, n, m) * 2 <= kCUs && k % 256 == 0) return GemmPlan{5, 2};  // a short prompt
+    return GemmPlan{5, 1};
 }
 
 bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, const void *y, int ldy) {

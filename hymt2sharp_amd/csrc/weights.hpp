@@ -76,7 +76,7 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
 // a split call needs a GemmSplitWs with room for gemm_split_bytes of partials
 // and a ticket per tile (zeroed once: every call leaves them zero), else it
 // runs unsplit.
-constexpr int kGemmTiles = 5;
+constexpr int kGemmTiles = 6;
 struct GemmPlan {
     int tile;
     int split;  // 1 or 2

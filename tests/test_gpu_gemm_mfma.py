@@ -88,7 +88,7 @@ def test_mfma_gemm_forced(monkeypatch, hip_available, rows, cols, m):
     assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
 
 
-@pytest.mark.parametrize("tile", ["128x128", "256x128", "128x256", "192x128", "192x256"])
+@pytest.mark.parametrize("tile", ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64"])
 @pytest.mark.parametrize("split", [1, 2])
 @pytest.mark.parametrize("cols,m", [(2048, 130), (6144, 257)])
 def test_mfma_gemm_tiles(monkeypatch, hip_available, tile, split, cols, m):
@@ -109,8 +109,8 @@ def test_mfma_gemm_tiles(monkeypatch, hip_available, tile, split, cols, m):
 
 def test_mfma_gemm_default_plans(monkeypatch, hip_available):
     """The shape rules' own choices at the model's shapes on a 512-row
-    prompt (the split 128 x 128 for q/k/v, o and down, 192 x 128 for
-    gate/up), against the fp64 product."""
+    prompt (128 x 64 for q/k/v, 128 x 64 split for o and down, 192 x 128 on
+    8 waves for gate/up), against the fp64 product."""
     monkeypatch.setenv("HYMT_HIP_GEMM", "mfma")
     monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
     for rows, cols in [(3072, 2048), (12288, 2048), (2048, 2048), (2048, 6144)]:
