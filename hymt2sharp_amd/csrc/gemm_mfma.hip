@@ -344,6 +344,41 @@ __global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
         }
     }
 
+    // bf16 output: restaged through the (idle) ring as [token][feature] rows,
+    // then written as whole 128-byte lines, 16 bytes a lane.  Written from the
+    // MFMA layout, each 8-byte store reached 16 token rows, 32 bytes of each,
+    // and the stores cost gate/up at m = 2048 about 14 of its 93 us.
+    if constexpr (YBF16) {
+        if ((a.ldy & 7) == 0) {
+            constexpr int RS = TF + 8;        // row stride in bf16 elements (16 bytes of padding)
+            constexpr int CPR = TF / 8;       // 16-byte chunks of a token row
+            constexpr int NQ = TT * CPR / NT;  // chunks per thread
+            static_assert(TT * RS * 2 <= S * kStageBytes && (TT * CPR) % NT == 0, "restage");
+            uint16_t *st = (uint16_t *)lds;
+            __syncthreads();  // every wave's operand reads (and the split handshake) are done
+#pragma unroll
+            for (int j = 0; j < BJ; j++) {
+                const int tl = (TT / WT) * wt + 16 * j + c;
+#pragma unroll
+                for (int i = 0; i < IF; i++) {
+                    const f32x4 v = acc[i][j];
+                    *(uint2 *)(st + tl * RS + (TF / 2) * wf + 16 * i + 4 * grp) =
+                        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int n = 0; n < NQ; n++) {
+                const int q = n * NT + tid, row = q / CPR, col = q - row * CPR;
+                const int t = t0 + row;
+                if (t < a.m)
+                    *(uint4 *)((uint16_t *)a.y + (size_t)t * a.ldy + f0 + 8 * col) = *(const uint4 *)(st + row * RS + 8 * col);
+            }
+            return;
+        }
+    }
+
     // epilogue: lane (grp, c) of block (i, j) holds features f .. f + 3 of token t
 #pragma unroll
     for (int j = 0; j < BJ; j++) {
