@@ -397,13 +397,14 @@ GEMM_SHAPES = [  # (name, n features, k, flags): the prefill GEMMs of the model 
     ("qkv", 3072, 2048, "bf16"), ("o", 2048, 2048, "acc"), ("gate_up", 12288, 2048, "bf16"),
     ("down", 2048, 6144, "acc"),
 ]
-GEMM_TILES = ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64", "128x128,2", "128x256,2", "128x64,2"]
+GEMM_TILES = ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64", "128x96", "128x128,2", "128x256,2",
+              "128x64,2"]
 
 
 def time_gemm(ms=(512, 2048), reps=10, rounds=5):
     """The prefill GEMMs y (+)= x W^T at the model's shapes: hipBLASLt's first
-    heuristic choice (the default), the hand-written MFMA kernel with its own
-    tile plan (HYMT_HIP_GEMM=mfma), and the MFMA kernel with each tile forced
+    heuristic choice (HYMT_HIP_GEMM=library), the hand-written MFMA kernel with
+    its own tile plan (HYMT_HIP_GEMM=mfma), and the MFMA kernel with each tile forced
     (HYMT_HIP_GEMM_TILE).  HIP events around `reps` back-to-back calls on
     the backend's stream, `rounds` rounds interleaving every candidate, the
     median per candidate (one pass per candidate in turn let clock drift move
@@ -416,10 +417,7 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
     bes = {}
     try:
         for mode in ("hipblaslt", "mfma"):
-            if mode == "mfma":
-                os.environ["HYMT_HIP_GEMM"] = "mfma"
-            else:
-                os.environ.pop("HYMT_HIP_GEMM", None)
+            os.environ["HYMT_HIP_GEMM"] = "mfma" if mode == "mfma" else "library"
             os.environ.pop("HYMT_HIP_GEMM_TILE", None)
             be = HipBackend(0)
             bes[mode] = be
@@ -916,6 +914,8 @@ def main():
     ap.add_argument("--no-spread", action="store_true",
                     help="skip the per-launch spread statistics (the profiled runs: rocprofv3's kernel trace "
                          "crashed in hipGraphLaunch during those 220 back-to-back replays with event records)")
+    ap.add_argument("--gemm-m", default="512,2048",
+                    help="prompt row counts of the gemm leg, comma-separated")
     ap.add_argument("--no-graph", action="store_true",
                     help="submit decode steps call by call instead of replaying a recorded step "
                          "(for counter collection, which times dispatches one by one)")
@@ -972,7 +972,8 @@ def main():
                                      "fp32 accumulation; o and down accumulate into fp32, q/k/v and "
                                      "gate/up write bf16): hipBLASLt's first heuristic choice against "
                                      "the hand-written MFMA kernel, its tile plan and each tile",
-                         "unit": "us per call", "shapes": time_gemm()}
+                         "unit": "us per call",
+                         "shapes": time_gemm(ms=tuple(int(v) for v in args.gemm_m.split(",")))}
     if args.only in (None, "ceilings"):
         extra["ceilings"] = measure_ceilings()
     if args.only in (None, "model"):

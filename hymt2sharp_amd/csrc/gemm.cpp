@@ -15,9 +15,17 @@
 // context come from one thread, in stream order).
 //
 // Algorithm choice, by HYMT_HIP_GEMM (read when the state is created):
-//  unset   hipBLASLt's first heuristic choice for the call's exact shape: no
-//          timing, so identical inputs give identical bits in every context
-//          and process (for one library version and device);
+//  unset   the MFMA kernel wherever its shape rules allow, except a large
+//          weight (>= 32 MiB of bf16) over 1024 or more rows, and
+//          hipBLASLt's first heuristic choice for the call's exact shape
+//          otherwise: no timing, so identical inputs give identical bits in
+//          every context and process (for one library version and device).
+//          Measured per shape (us, MFMA plan / hipBLASLt's first choice, m =
+//          512, 1024, 1531, 2048): the MFMA kernel is faster for q/k/v, o and
+//          down at every m and for gate/up at 512, hipBLASLt for gate/up from
+//          1024 rows on (42.4 / 41.4, 69.0 / 65.6, 81.2 / 79.5; 91 / 82 with
+//          the weights cold from HBM, as the model step reads them);
+//  library hipBLASLt's first heuristic choice for every shape;
 //  auto    the first call of a shape in an m bucket (m rounded up to a power
 //          of two, at least 256) times up to kCandidates of hipBLASLt's
 //          candidates and the MFMA kernel on the call's operands and keeps
@@ -59,7 +67,10 @@ struct Choice {
     bool mfma = false;             // the MFMA kernel timed fastest
 };
 
-enum GemmMode { kHeuristic = 0, kAuto = 1, kMfmaOnly = 2, kLibTimed = 3 };
+enum GemmMode { kHeuristic = 0, kAuto = 1, kMfmaOnly = 2, kLibTimed = 3, kPlanned = 4 };
+
+// The planned default's choice of the MFMA kernel (given that it fits).
+bool mfma_preferred(int n, int k, int m) { return !((size_t)n * k * 2 >= (32u << 20) && m >= 1024); }
 
 void destroy_layouts(Layouts &l) {
     if (l.a) hipblasLtMatrixLayoutDestroy(l.a);
@@ -109,6 +120,8 @@ GemmState *gemm_state_create() {
     GemmState *g = new (std::nothrow) GemmState();
     if (g) {
         const char *e = std::getenv("HYMT_HIP_GEMM");
+        g->mode = kPlanned;
+        if (e && !std::strcmp(e, "library")) g->mode = kHeuristic;
         if (e && !std::strcmp(e, "auto")) g->mode = kAuto;
         if (e && !std::strcmp(e, "mfma")) g->mode = kMfmaOnly;
         if (e && !std::strcmp(e, "hipblaslt")) g->mode = kLibTimed;
@@ -139,7 +152,7 @@ hipError_t run_mfma(GemmState &g, const uint16_t *W, int n, int k, const uint16_
     const GemmPlan p = gemm_mfma_plan(n, k, m);
     if (p.split == 2) {
         const size_t need = gemm_split_bytes(n, m, p);
-        const int tickets = (int)(need / (128 * 128 * 4)) + 1;  // at least one per tile
+        const int tickets = gemm_split_tiles(n, m, p);  // one per tile
         hipError_t e = hipSuccess;
         if (need > g.split.part_bytes) {
             e = hipStreamSynchronize(s);
@@ -274,7 +287,8 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
     if (!g || n < 1 || k < 1 || m < 0 || ldy < n || (accumulate && y_bf16)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const bool fits = gemm_mfma_fits(W, n, k, x, m, y, ldy);
-    if (g->mode == kMfmaOnly && fits) return run_mfma(*g, W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
+    if (fits && (g->mode == kMfmaOnly || (g->mode == kPlanned && mfma_preferred(n, k, m))))
+        return run_mfma(*g, W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     hipError_t e = hipSuccess;
     if (!g->handle) {
         hipblasStatus_t st = hipblasLtCreate(&g->handle);

@@ -42,6 +42,7 @@
 // bf16).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
@@ -411,7 +412,8 @@ struct TileShape {
     int IF, JT;
 };
 constexpr TileShape kTiles[kGemmTiles] = {
-    {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}, {"128x64", 4, 2}};
+    {"128x128", 4, 4}, {"256x128", 8, 4}, {"128x256", 4, 8}, {"192x128", 6, 4}, {"192x256", 6, 8}, {"128x64", 4, 2},
+    {"128x96", 4, 3}};
 
 template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT>
 void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span) {
@@ -441,7 +443,8 @@ void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, 
     // chip idle (at m = 512, split: o 11.4 against 15.0 us for 128 x 128 split,
     // down 22.9 against 28.1, q/k/v unsplit 13.3 against 15.3); a 192 x 64
     // tile was slower at every model shape
-    default: launch_tile<4, 2, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break; // 24 KiB
+    case 5: launch_tile<4, 2, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 24 KiB
+    default: launch_tile<4, 3, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break; // 28 KiB
     }
 }
 
@@ -449,6 +452,14 @@ int tiles_of(int tile, int n, int m) {
     const int TF = 32 * kTiles[tile].IF, TT = 32 * kTiles[tile].JT;
     if (n % TF) return 0;
     return (n / TF) * ((m + TT - 1) / TT);
+}
+
+// The share of its last round of workgroups a launch fills on 256 CUs
+// (1: whole rounds).
+double round_fill(int wgs) {
+    if (wgs <= 0) return 0.0;
+    const int rounds = (wgs + 255) / 256;
+    return wgs / (256.0 * rounds);
 }
 
 }  // namespace
@@ -459,16 +470,19 @@ int gemm_tile_by_name(const char *name) {
     return -1;
 }
 
-// The tile plan for a shape.  Measured at m = 2048 (us per call, this kernel
-// / hipBLASLt's first heuristic choice): q/k/v 3072 x 2048 192 x 128 27.4
-// (128 x 128 34.9) / 28.1; gate/up 12288 x 2048 192 x 256 90.6 (128 x 128
-// 113) / 83.6; o 2048 x 2048 128 x 128 22.5 (split 128 x 256 29.9) / 24.0;
-// down 2048 x 6144 128 x 128 50.3 (split 128 x 256 56.0) / 53.4; at m = 512
-// q/k/v 128 x 64 13.3 / 13.0, o 128 x 64 split 11.4 / 11.6, gate/up 192 x 128
-// 27.4 / 28.2, down 128 x 64 split 22.9 / 26.6.  So: the widest tile that
-// gives the chip about 1.5 rounds of workgroups, 192 rows where the width
-// allows; 128 x 128 while its one round fills three quarters of the chip;
-// else 128 x 64, its k split when its tiles fill at most half.
+// The tile plan for a shape: the tile whose workgroups fill whole rounds of
+// the chip best, the larger tile on a tie, 192 rows where the width allows;
+// with deep k (>= 4096) a k split of 128 x 128 tiles when they alone would
+// fill less than three quarters of a round; else, for a short prompt, the
+// k split of 128 x 64 tiles.  Measured (us per call, the plan's tile /
+// hipBLASLt's first heuristic choice; `bench.py --only gemm`): at m = 2048
+// q/k/v 192 x 128 27.2 / 28.1, gate/up 192 x 256 84.9 / 83.9, o 128 x 128
+// 22.1 / 24.0, down 128 x 128 51.7 / 54.7; at m = 1531 q/k/v 192 x 128 21.5 /
+// 22.8, gate/up 192 x 128 67.9 / 64.8, o and down 128 x 96 17.1 / 19.3 and
+// 39.0 / 42.6; at m = 1024 q/k/v 128 x 128 17.6 / 18.6, gate/up 192 x 256
+// 42.8 / 42.2, o 128 x 64 15.1 / 16.9, down 128 x 128 split 30.7 / 36.8; at
+// m = 512 q/k/v 128 x 64 13.3 / 13.0, gate/up 192 x 128 27.4 / 28.2, o and
+// down 128 x 64 split 11.4 / 11.6 and 22.9 / 26.6.
 GemmPlan gemm_mfma_plan(int n, int k, int m) {
     // forced by HYMT_HIP_GEMM_TILE=<tile>[,2] (a tuning knob; the shape rules
     // still apply)
@@ -485,14 +499,22 @@ GemmPlan gemm_mfma_plan(int n, int k, int m) {
         const int t = gemm_tile_by_name(buf);
         if (t >= 0) return GemmPlan{t, split};
     }
-    constexpr int kCUs = 256;
+    auto fill = [&](int t, int split) { return round_fill(tiles_of(t, n, m) * split); };
     if (n % 192 == 0) {
-        if (tiles_of(4, n, m) * 2 >= 3 * kCUs) return GemmPlan{4, 1};
-        if (tiles_of(3, n, m) * 4 >= 3 * kCUs) return GemmPlan{3, 1};
+        const double e4 = fill(4, 1), e3 = fill(3, 1);
+        if (std::max(e4, e3) >= 0.75) return GemmPlan{e4 >= e3 ? 4 : 3, 1};
     }
-    if (tiles_of(0, n, m) * 4 >= 3 * kCUs) return GemmPlan{0, 1};
-    if (tiles_of(5, n, m) * 2 <= kCUs && k % 256 == 0) return GemmPlan{5, 2};  // a short prompt
-    return GemmPlan{5, 1};
+    int best = 0;  // 128 x 128, 128 x 96, 128 x 64: the best fill, the larger on a tie
+    double eb = fill(0, 1);
+    for (int t : {6, 5})
+        if (fill(t, 1) > eb + 1e-9) {
+            best = t;
+            eb = fill(t, 1);
+        }
+    const bool splittable = k % 256 == 0;
+    if (splittable && k >= 4096 && fill(0, 1) < 0.75 && fill(0, 2) >= 0.75) return GemmPlan{0, 2};
+    if (eb >= 0.75 || !splittable) return GemmPlan{best, 1};
+    return GemmPlan{5, 2};  // a short prompt
 }
 
 bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, const void *y, int ldy) {
@@ -504,6 +526,12 @@ bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, c
 size_t gemm_split_bytes(int n, int m, GemmPlan p) {
     if (p.split < 2) return 0;
     return (size_t)tiles_of(p.tile, n, m) * 32 * kTiles[p.tile].IF * 32 * kTiles[p.tile].JT * 4;
+}
+
+int gemm_split_tiles(int n, int m, GemmPlan p) {
+    if (p.tile < 0 || p.tile >= kGemmTiles) return 0;
+    const int t = tiles_of(p.tile, n, m);
+    return t ? t : tiles_of(0, n, m);
 }
 
 hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,

@@ -71,12 +71,12 @@ hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int 
 // the MFMA kernel alone (n a multiple of 128, k of 128, ldy of 4, 16-byte
 // aligned operands, operands under 2 GiB: gemm_mfma_fits).  A plan names the
 // workgroup tile (kTiles in gemm_mfma.hip: 0 128 x 128, 1 256 x 128, 2
-// 128 x 256, 3 192 x 128, 4 192 x 256, features x tokens) and whether k is
-// split in two;
+// 128 x 256, 3 192 x 128, 4 192 x 256, 5 128 x 64, 6 128 x 96, features x
+// tokens) and whether k is split in two;
 // a split call needs a GemmSplitWs with room for gemm_split_bytes of partials
-// and a ticket per tile (zeroed once: every call leaves them zero), else it
-// runs unsplit.
-constexpr int kGemmTiles = 6;
+// and gemm_split_tiles tickets (zeroed once: every call leaves them zero),
+// else it runs unsplit.
+constexpr int kGemmTiles = 7;
 struct GemmPlan {
     int tile;
     int split;  // 1 or 2
@@ -91,6 +91,7 @@ bool gemm_mfma_fits(const uint16_t *W, int n, int k, const uint16_t *x, int m, c
 int gemm_tile_by_name(const char *name);
 GemmPlan gemm_mfma_plan(int n, int k, int m);
 size_t gemm_split_bytes(int n, int m, GemmPlan p);
+int gemm_split_tiles(int n, int m, GemmPlan p);
 hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,
                           bool accumulate, hipStream_t s, GemmPlan p, const GemmSplitWs *ws);
 

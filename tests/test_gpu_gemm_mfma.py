@@ -88,7 +88,7 @@ def test_mfma_gemm_forced(monkeypatch, hip_available, rows, cols, m):
     assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
 
 
-@pytest.mark.parametrize("tile", ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64"])
+@pytest.mark.parametrize("tile", ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64", "128x96"])
 @pytest.mark.parametrize("split", [1, 2])
 @pytest.mark.parametrize("cols,m", [(2048, 130), (6144, 257)])
 def test_mfma_gemm_tiles(monkeypatch, hip_available, tile, split, cols, m):
@@ -151,16 +151,59 @@ def test_auto_choice_is_correct(monkeypatch, hip_available):
     check(out, ref, mag, y0)
 
 
-@pytest.mark.parametrize("rows,cols,m", [(2048, 2048, 2048), (1024, 6144, 300)])
-def test_default_choice_is_reproducible(monkeypatch, hip_available, rows, cols, m):
-    """Unset HYMT_HIP_GEMM: hipBLASLt's first heuristic choice, with no
-    timing, so two contexts (each choosing on its own) give the same bits
-    for the same inputs, and the results hold the bound."""
+@pytest.mark.parametrize("rows,cols,m,mfma", [
+    (2048, 2048, 2048, True),    # o at a 2048-row prompt: the MFMA kernel
+    (1024, 6144, 300, True),
+    (8192, 2048, 1024, False),   # a 32 MiB weight over 1024 rows: hipBLASLt's first choice
+])
+def test_default_choice_is_reproducible(monkeypatch, hip_available, rows, cols, m, mfma):
+    """Unset HYMT_HIP_GEMM: the MFMA kernel where it fits, except a weight of
+    32 MiB or more over 1024 or more rows, which takes hipBLASLt's first
+    heuristic choice; no timing either way, so two contexts (each choosing on
+    its own) give the same bits for the same inputs, and the results hold the
+    bound."""
     monkeypatch.delenv("HYMT_HIP_GEMM", raising=False)
+    monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
     a, counts, ref, mag, y0 = run_case(rows, cols, m, 91, MFMA)
     b, _, _, _, _ = run_case(rows, cols, m, 91, MFMA)
     check(a, ref, mag, y0)
-    assert not any(counts.values()), counts  # the default never times or runs the MFMA kernel
+    if mfma:
+        assert counts == {"gemm_mfma_out_f32": 2, "gemm_mfma_out_bf16": 1}
+    else:
+        assert not any(counts.values()), counts
     for key in a:
         assert np.array_equal(a[key], b[key]), key
 
+
+def test_library_choice_is_reproducible(monkeypatch, hip_available):
+    """HYMT_HIP_GEMM=library: hipBLASLt's first heuristic choice for every
+    shape, never the MFMA kernel, the same bits in two contexts."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "library")
+    a, counts, ref, mag, y0 = run_case(2048, 2048, 2048, 91, MFMA)
+    b, _, _, _, _ = run_case(2048, 2048, 2048, 91, MFMA)
+    check(a, ref, mag, y0)
+    assert not any(counts.values()), counts
+    for key in a:
+        assert np.array_equal(a[key], b[key]), key
+
+
+
+def test_planned_split_runs_split_in_a_fresh_context(monkeypatch, hip_available):
+    """The plan's k split of 128 x 64 tiles (the o projection on a 512-row
+    prompt) runs split on a context's first call: the split workspace holds a
+    ticket per tile of the plan's own tile (it was once sized for 128 x 128
+    tiles, and a call whose tiles outnumbered its tickets fell back to the
+    unsplit kernel, so the bits depended on which calls came before).  Each
+    case is a fresh context: the plan's bits equal the forced split's and
+    differ from the unsplit kernel's (a different fp32 summation order)."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "mfma")
+    monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
+    plan, _, ref, mag, y0 = run_case(2048, 2048, 512, 55, MFMA)
+    check(plan, ref, mag, y0)
+    monkeypatch.setenv("HYMT_HIP_GEMM_TILE", "128x64,2")
+    split, _, _, _, _ = run_case(2048, 2048, 512, 55, MFMA)
+    monkeypatch.setenv("HYMT_HIP_GEMM_TILE", "128x64")
+    whole, _, _, _, _ = run_case(2048, 2048, 512, 55, MFMA)
+    for key in plan:
+        assert np.array_equal(plan[key], split[key]), key
+    assert not np.array_equal(plan["f32"], whole["f32"])
