@@ -124,6 +124,7 @@ struct FlashArgs {
     int items_per_kvh;  // work items per kv head
     int q_ld;           // elements from one q row to the next, >= Hq*D
     int out_bf16;       // write out as bf16 (the input of a bf16 GEMM)
+    int split_ns;       // > 1: every pair splits into this many items (item = pair * split_ns + split)
     int pages_in_args;  // 1: pages[] holds tab[0, ceil((pos0+seq)/64)) (<= kArgPages)
     int32_t pages[kArgPages];  // physical page of each logical block (when
                                // pages_in_args): the first tile's copy then

@@ -736,13 +736,16 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         }
         cap = std::min(cap, kItemTiles);
         f.cap = cap;
-        int items = 0;
-        bool split = false;
+        int items = 0, ns0 = -1;
+        bool split = false, uniform = true;
         for (int pr = 0; pr < f.npairs; pr++) {
             const int ns = (pair_tiles(pos, pr, f.nb16, seq) + cap - 1) / cap;
             items += ns;
             split |= ns > 1;
+            uniform &= ns0 < 0 || ns == ns0;
+            ns0 = ns;
         }
+        f.split_ns = split && uniform ? ns0 : 0;
         f.items_per_kvh = items;
         if (split) {
             const size_t slots = (size_t)c->kv_heads * items;
