@@ -825,8 +825,21 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
         xo[16 * 64] = make_float4(mrun[0], mrun[1], lrun[0], lrun[1]);
     }
     __syncthreads();
-    if (half) return;
-    {
+    // A split item's partial tile ([G][32][D] of its slot, 32 KiB in one
+    // block) is restaged through LDS (past the hand-off above) and written as
+    // whole lines, 16 bytes a lane: from the MFMA layout each 8-byte store
+    // reached 16 rows, 32 bytes of each (config-4 flash kernel 29.4 -> 28.8
+    // us).  The same for the bf16 output rows (1 KiB of 4 heads each) was no
+    // faster at config 3.  Rows are padded by 16 bytes against bank
+    // conflicts on the restaging stores.
+    const bool restage = it.nsplit > 1;
+    constexpr int kStage = 36864;          // uint16 offset of the restaging area (72 KiB)
+    constexpr int RSP = D + 8;             // partial rows [G][32][D], padded
+    uint16_t *st = sKV + kStage;
+    static_assert(kStage + G * 32 * RSP <= 8 * KT, "restage");
+    const int qdim = a.heads * D;
+    const size_t slot = (size_t)kvh * a.items_per_kvh + item_idx;
+    if (!half) {
         const float4 ml = xo[16 * 64];
         const float m1[2] = {ml.x, ml.y}, l1[2] = {ml.z, ml.w};
 #pragma unroll
@@ -841,57 +854,61 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
                 o[db][qq] = o[db][qq] * a0 + f32x4{v.x, v.y, v.z, v.w} * a1;
             }
         }
-    }
 
-    // ---- finish: row sums across the 4 lane groups ----
+        // ---- finish: row sums across the 4 lane groups ----
 #pragma unroll
-    for (int qq = 0; qq < 2; qq++) lrun[qq] = pf_xrow_sum(lrun[qq]);
-    const int qdim = a.heads * D;
-    if (it.nsplit == 1) {
-#pragma unroll
-        for (int qq = 0; qq < 2; qq++) {
-            const int row = rowq[qq] + c;
-            if (!okq[qq] || row >= a.seq) continue;
-            const float inv = lrun[qq] > 0.f ? 1.0f / lrun[qq] : 0.f;
-            const size_t off = (size_t)row * qdim + (size_t)h * D + grp * 4;
-            if (a.out_bf16) {
-                uint16_t *orow = (uint16_t *)a.out + off;
-#pragma unroll
-                for (int db = 0; db < 8; db++) {
-                    f32x4 v = o[db][qq] * inv;
-                    *(uint2 *)(orow + db * 16) =
-                        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
-                                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
-                }
-            } else {
-                float *orow = a.out + off;
-#pragma unroll
-                for (int db = 0; db < 8; db++) {
-                    f32x4 v = o[db][qq] * inv;
-                    *(float4 *)(orow + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
-                }
-            }
-        }
-    } else {
-        // split item: O / l rounded to the operand type (the weights sum to 1,
-        // so |O / l| <= max |V| fits it), and (m, l) in fp32 for the merge
-        const size_t slot = (size_t)kvh * a.items_per_kvh + item_idx;
+        for (int qq = 0; qq < 2; qq++) lrun[qq] = pf_xrow_sum(lrun[qq]);
 #pragma unroll
         for (int qq = 0; qq < 2; qq++) {
             const int r = qq * 16 + c;
             const float inv = lrun[qq] > 0.f ? 1.0f / lrun[qq] : 0.f;
-            uint16_t *po = (uint16_t *)a.part_o + ((slot * G + hw) * 32 + r) * D + grp * 4;
+            if (it.nsplit > 1) {
+                // split item: O / l rounded to the operand type (the weights sum
+                // to 1, so |O / l| <= max |V| fits it), and (m, l) in fp32
 #pragma unroll
-            for (int db = 0; db < 8; db++) {
-                const f32x4 v = o[db][qq] * inv;
-                *(uint2 *)(po + db * 16) = make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
-            }
-            if (grp == 0) {
-                float *pm = a.part_ml + ((slot * G + hw) * 32 + r) * 2;
-                pm[0] = mrun[qq];
-                pm[1] = lrun[qq];
+                for (int db = 0; db < 8; db++) {
+                    const f32x4 v = o[db][qq] * inv;
+                    *(uint2 *)(st + (hw * 32 + r) * RSP + db * 16 + grp * 4) =
+                        make_uint2(pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3]));
+                }
+                if (grp == 0) {
+                    float *pm = a.part_ml + ((slot * G + hw) * 32 + r) * 2;
+                    pm[0] = mrun[qq];
+                    pm[1] = lrun[qq];
+                }
+            } else {
+                const int row = rowq[qq] + c;
+                if (!okq[qq] || row >= a.seq) continue;
+                const size_t off = (size_t)row * qdim + (size_t)h * D + grp * 4;
+                if (a.out_bf16) {
+                    uint16_t *orow = (uint16_t *)a.out + off;
+#pragma unroll
+                    for (int db = 0; db < 8; db++) {
+                        const f32x4 v = o[db][qq] * inv;
+                        *(uint2 *)(orow + db * 16) =
+                            make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                                       (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+                    }
+                } else {
+                    float *orow = a.out + off;
+#pragma unroll
+                    for (int db = 0; db < 8; db++) {
+                        const f32x4 v = o[db][qq] * inv;
+                        *(float4 *)(orow + db * 16) = make_float4(v[0], v[1], v[2], v[3]);
+                    }
+                }
             }
         }
+    }
+    if (!restage) return;
+    __syncthreads();
+    // 32 KiB: [G][32][D] of the item's slot, one contiguous block; 4 chunks
+    // of 16 bytes a thread
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+        const int q = n * 512 + tid, row = q >> 4, col = q & 15;
+        *(uint4 *)((uint16_t *)a.part_o + (slot * G * 32 + row) * D + col * 8) =
+            *(const uint4 *)(st + row * RSP + col * 8);
     }
 }
 
