@@ -58,11 +58,14 @@ hipError_t launch_rows_swiglu(const float *gu, int m, int n, uint16_t *out, hipS
 hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *out, hipStream_t s);
 hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s);
 // y[m][n] (+)= x[m][k] . W[n][k]^T, bf16 operands, fp32 accumulation
-// (gemm.cpp: this library's MFMA kernel, gemm_mfma.hip, or hipBLASLt,
-// whichever the first call of a shape times faster); y is fp32 or, with
-// y_bf16, bf16, rows ldy elements apart.  The GemmState (library handle,
-// workspace, chosen kernels) belongs to one context.  HYMT_HIP_GEMM=mfma or
-// =hipblaslt, read when the state is created, fixes the choice.
+// (gemm.cpp: this library's MFMA kernel, gemm_mfma.hip, wherever it fits,
+// except weights of 32 MiB or more over 1024 rows or more, which take
+// hipBLASLt's first heuristic choice); y is fp32 or, with y_bf16, bf16, rows
+// ldy elements apart.  The GemmState (library handle, workspace, chosen
+// kernels) belongs to one context.  HYMT_HIP_GEMM, read when the state is
+// created, changes the choice: =library hipBLASLt everywhere, =mfma the MFMA
+// kernel wherever it fits, =hipblaslt hipBLASLt's timed pick, =auto the faster
+// of the two on the first call of a shape.
 struct GemmState;
 GemmState *gemm_state_create();
 void gemm_state_destroy(GemmState *g);
