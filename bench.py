@@ -410,6 +410,9 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
     median per candidate (one pass per candidate in turn let clock drift move
     one kernel by 10-15 % between candidates); o and down accumulate into
     fp32, q/k/v and gate/up write bf16 (as hymt_model_prefill calls them).
+    For gate/up also the GEMM with its SwiGLU: hipBLASLt's or the MFMA
+    plan's GEMM followed by the row kernel (hymt_rows_swiglu_bf16), and the
+    fused launch (hymt_gemm_swiglu) that hymt_model_prefill runs.
     Each context reads HYMT_HIP_GEMM when its first GEMM makes its GEMM
     state, so each mode gets a context of its own."""
     out = {}
@@ -436,6 +439,8 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
             raw = S.random_weight(S.seed(7, n, k), N.W_Q4_K, n, k)
             ws = {}
             bufs = {}
+            acts = {}
+            swi = name == "gate_up"
             mmax = max(ms)
             x = S.f32_to_bf16_bits(S.normal(S.seed(7, k, 1), (mmax, k), 1.0))
             for mode, be in bes.items():
@@ -448,8 +453,10 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
                           else np.zeros(mmax * n, np.float32))
                 ws[mode] = w
                 bufs[mode] = (dx, dy)
+                if swi:
+                    acts[mode] = be.alloc(mmax * n)  # [m][n / 2] bf16
 
-            def run(mode, m, tile, calls):
+            def run(mode, m, tile, calls, op="gemm"):
                 be = bes[mode]
                 if tile is None:
                     os.environ.pop("HYMT_HIP_GEMM_TILE", None)
@@ -457,7 +464,13 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
                     os.environ["HYMT_HIP_GEMM_TILE"] = tile
                 dx, dy = bufs[mode]
                 ev = HipEvents(be.stream())
-                call = lambda: be.gemm(ws[mode], dx, m, dy, accumulate=kind == "acc", out_bf16=kind == "bf16")
+                gemm = lambda: be.gemm(ws[mode], dx, m, dy, accumulate=kind == "acc", out_bf16=kind == "bf16")
+                if op == "gemm":
+                    call = gemm
+                elif op == "rows":  # the GEMM, then the SwiGLU row kernel
+                    call = lambda: (gemm(), be.rows_swiglu_bf16(dy, m, n // 2, acts[mode]))
+                else:  # the fused launch
+                    call = lambda: be.gemm_swiglu(ws[mode], dx, m, acts[mode])
                 call()
                 e0, e1 = ev.new(), ev.new()
                 ev.record(e0)
@@ -472,17 +485,29 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
 
             for m in ms:
                 flop = 2.0 * n * k * m
-                cands = [("hipblaslt", None), ("mfma", None)] + [("mfma", t) for t in GEMM_TILES]
+                cands = [("hipblaslt", None, "gemm"), ("mfma", None, "gemm")] + \
+                    [("mfma", t, "gemm") for t in GEMM_TILES]
+                if swi:
+                    cands += [("hipblaslt", None, "rows"), ("mfma", None, "rows")]
+                    try:
+                        run("mfma", m, None, 1, "fused")
+                        cands.append(("mfma", None, "fused"))
+                    except N.NotSupportedError:
+                        pass
                 for c in cands:  # warm-up: every candidate once
-                    run(c[0], m, c[1], 2)
+                    run(c[0], m, c[1], 2, c[2])
                 samples = {c: [] for c in cands}
                 for _ in range(rounds):  # interleaved, so clock drift weighs on all alike
                     for c in cands:
-                        samples[c].append(run(c[0], m, c[1], reps))
+                        samples[c].append(run(c[0], m, c[1], reps, c[2]))
                 med = {c: round(float(np.median(v)), 2) for c, v in samples.items()}
-                rec = {"n": n, "k": k, "m": m, "out": kind, "hipblaslt_us": med[("hipblaslt", None)],
-                       "mfma_plan_us": med[("mfma", None)],
-                       "mfma_tiles_us": {t: med[("mfma", t)] for t in GEMM_TILES}}
+                rec = {"n": n, "k": k, "m": m, "out": kind, "hipblaslt_us": med[("hipblaslt", None, "gemm")],
+                       "mfma_plan_us": med[("mfma", None, "gemm")],
+                       "mfma_tiles_us": {t: med[("mfma", t, "gemm")] for t in GEMM_TILES}}
+                if swi:
+                    rec["with_swiglu_us"] = {"hipblaslt_then_rows": med[("hipblaslt", None, "rows")],
+                                             "mfma_then_rows": med[("mfma", None, "rows")],
+                                             "fused": med.get(("mfma", None, "fused"))}
                 rec["hipblaslt_tflops"] = round(flop / (rec["hipblaslt_us"] * 1e-6) / 1e12, 1)
                 rec["mfma_plan_tflops"] = round(flop / (rec["mfma_plan_us"] * 1e-6) / 1e12, 1)
                 out[f"{name}_m{m}"] = rec
@@ -490,6 +515,8 @@ def time_gemm(ms=(512, 2048), reps=10, rounds=5):
                 be.weight_free(ws[mode])
                 for b in bufs[mode]:
                     be.free(b)
+                if swi:
+                    be.free(acts[mode])
     finally:
         for be in bes.values():
             be.Dispose()

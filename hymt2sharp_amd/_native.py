@@ -112,6 +112,7 @@ SIGNATURES = {
     "hymt_rows_rmsnorm": [_vp, _vp, _i, _i, _vp, ctypes.c_float, _vp],
     "hymt_rows_swiglu": [_vp, _vp, _i, _i, _vp],
     "hymt_rows_swiglu_bf16": [_vp, _vp, _i, _i, _vp],
+    "hymt_gemm_swiglu": [_vp, _vp, _vp, _vp, _i, _vp],
     "hymt_to_bf16": [_vp, _vp, ctypes.c_size_t, _vp],
     "hymt_model_create": [_vp, _i, _i, _i, _i, ctypes.c_float, ctypes.POINTER(_vp)],
     "hymt_model_set_layer": [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp],

@@ -260,6 +260,13 @@ class HipBackend:
         flags = (N.GEMM_ACCUMULATE if accumulate else 0) | (N.GEMM_OUT_BF16 if out_bf16 else 0)
         N.check(self._lib.hymt_gemm(self._h, w, row0, nrows, x_dev, m, y_dev, flags))
 
+    def gemm_swiglu(self, gate, x_dev, m: int, act_dev, up=None):
+        """act[m][f] = bf16(silu(g) u) with g, u the bf16 products of x over the
+        gate and up rows (gate = one [gate; up] weight with up None, or the gate
+        rows with up the up rows), fused; NotSupportedError where the fused
+        launch would not give the bits of gemm(out_bf16) + rows_swiglu_bf16."""
+        N.check(self._lib.hymt_gemm_swiglu(self._h, gate, up, x_dev, m, act_dev))
+
     def embed_rows(self, w, rows, out_dev):
         r = np.ascontiguousarray(rows, dtype=np.int32)
         N.check(self._lib.hymt_embed_rows(self._h, w, _ptr(r), r.size, out_dev))

@@ -36,6 +36,30 @@ __device__ __forceinline__ uint16_t f32_to_f16(float x) {
 }
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
+// silu(g) = g / (1 + e^-g) from the hardware's base-2 exponential and
+// reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each): a few fp32 ulps from
+// the correctly rounded quotient, far inside the bf16 rounding of the result.
+// Large |g| behaves as the exact form: e^-g overflows to inf for g < -88 and
+// gives -0, and underflows to 0 for large g and gives g.
+__device__ __forceinline__ float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
+}
+
+// bf16 silu(g) u of 8 bf16 gate values g and 8 up values u, 16 bytes each
+// (Ops.SiLUMulRange, Ops.cs:1016-1052, over bf16 inputs)
+__device__ __forceinline__ uint4 swiglu8(uint4 gb, uint4 ub) {
+    const uint32_t gw[4] = {gb.x, gb.y, gb.z, gb.w};
+    const uint32_t uw[4] = {ub.x, ub.y, ub.z, ub.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const float g0 = bf16_to_f32(gw[k] & 0xFFFF), g1 = bf16_to_f32(gw[k] >> 16);
+        const float u0 = bf16_to_f32(uw[k] & 0xFFFF), u1 = bf16_to_f32(uw[k] >> 16);
+        o[k] = (uint32_t)f32_to_bf16(silu_fast(g0) * u0) | ((uint32_t)f32_to_bf16(silu_fast(g1) * u1) << 16);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <typename T> __device__ __forceinline__ typename T::storage to_elem(float x);
 template <> __device__ __forceinline__ float to_elem<F32>(float x) { return x; }
 template <> __device__ __forceinline__ uint16_t to_elem<F16>(float x) { return f32_to_f16(x); }

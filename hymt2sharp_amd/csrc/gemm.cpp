@@ -15,16 +15,16 @@
 // context come from one thread, in stream order).
 //
 // Algorithm choice, by HYMT_HIP_GEMM (read when the state is created):
-//  unset   the MFMA kernel wherever its shape rules allow, except a large
-//          weight (>= 32 MiB of bf16) over 1024 or more rows, and
-//          hipBLASLt's first heuristic choice for the call's exact shape
+//  unset   the MFMA kernel wherever its shape rules allow (gemm_mfma_fits),
+//  (=mfma) hipBLASLt's first heuristic choice for the call's exact shape
 //          otherwise: no timing, so identical inputs give identical bits in
-//          every context and process (for one library version and device).
-//          Measured per shape (us, MFMA plan / hipBLASLt's first choice, m =
-//          512, 1024, 1531, 2048): the MFMA kernel is faster for q/k/v, o and
-//          down at every m and for gate/up at 512, hipBLASLt for gate/up from
-//          1024 rows on (42.4 / 41.4, 69.0 / 65.6, 81.2 / 79.5; 91 / 82 with
-//          the weights cold from HBM, as the model step reads them);
+//          every context and process.  Measured per shape (us, MFMA plan /
+//          hipBLASLt's first choice): the MFMA kernel is faster for q/k/v, o
+//          and down at every m from 512 to 2048 and for gate/up at 512;
+//          hipBLASLt by 1-5 % for the gate/up GEMM alone from 1024 rows on,
+//          which the model's prefill runs fused with its SwiGLU on the MFMA
+//          kernel instead (gemm_swiglu: one launch, half the output bytes,
+//          no row kernel);
 //  library hipBLASLt's first heuristic choice for every shape;
 //  auto    the first call of a shape in an m bucket (m rounded up to a power
 //          of two, at least 256) times up to kCandidates of hipBLASLt's
@@ -33,8 +33,7 @@
 //          hipBLASLt, when the heuristic offers the algorithm for the new m,
 //          else its first choice).  The pick can differ between processes
 //          with timing noise, and with it the summation order and the bits;
-//  hipblaslt  as auto over hipBLASLt's candidates only;
-//  mfma    the MFMA kernel wherever its shape rules allow, else the default.
+//  hipblaslt  as auto over hipBLASLt's candidates only.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -67,10 +66,7 @@ struct Choice {
     bool mfma = false;             // the MFMA kernel timed fastest
 };
 
-enum GemmMode { kHeuristic = 0, kAuto = 1, kMfmaOnly = 2, kLibTimed = 3, kPlanned = 4 };
-
-// The planned default's choice of the MFMA kernel (given that it fits).
-bool mfma_preferred(int n, int k, int m) { return !((size_t)n * k * 2 >= (32u << 20) && m >= 1024); }
+enum GemmMode { kHeuristic = 0, kAuto = 1, kLibTimed = 3, kPlanned = 4 };
 
 void destroy_layouts(Layouts &l) {
     if (l.a) hipblasLtMatrixLayoutDestroy(l.a);
@@ -123,7 +119,6 @@ GemmState *gemm_state_create() {
         g->mode = kPlanned;
         if (e && !std::strcmp(e, "library")) g->mode = kHeuristic;
         if (e && !std::strcmp(e, "auto")) g->mode = kAuto;
-        if (e && !std::strcmp(e, "mfma")) g->mode = kMfmaOnly;
         if (e && !std::strcmp(e, "hipblaslt")) g->mode = kLibTimed;
     }
     return g;
@@ -282,12 +277,31 @@ hipError_t time_candidates(GemmState &g, hipblasLtMatmulDesc_t desc, const Layou
 
 }  // namespace
 
+bool gemm_swiglu(GemmState *g, hipStream_t s, const uint16_t *Wg, const uint16_t *Wu, bool separate, int f, int k,
+                 const uint16_t *x, int m, const uint16_t *gu, uint16_t *act, hipError_t &err) {
+    err = hipSuccess;
+    if (!g || m < 1 || f < 1) return false;
+    // gu (null: any 16-byte aligned buffer) and its up half gu + f: their
+    // alignment is all that enters (f % 8 == 0 below)
+    const bool gu_al = ((uintptr_t)gu & 15u) == 0;
+    auto mfma_unsplit = [&](const uint16_t *W, int n) {
+        return gemm_mfma_fits(W, n, k, x, m, act, 2 * f) && g->mode == kPlanned && gemm_mfma_plan(n, k, m).split == 1;
+    };
+    const bool unfused_mfma = separate ? mfma_unsplit(Wg, f) && mfma_unsplit(Wu, f)
+                                       : Wu == Wg + (size_t)f * k && mfma_unsplit(Wg, 2 * f);
+    // launch_rows_swiglu_bf16's 16-byte kernel
+    const bool rows_x8 = f % 8 == 0 && gu_al && ((uintptr_t)act & 15u) == 0 && (size_t)m * (f / 8) <= (1u << 30);
+    if (!unfused_mfma || !rows_x8 || !gemm_swiglu_fits(Wg, Wu, f, k, x, m, act, f)) return false;
+    err = gemm_swiglu_mfma(Wg, Wu, f, k, x, m, act, f, s, gemm_mfma_plan(2 * f, k, m));
+    return true;
+}
+
 hipError_t gemm_bf16(GemmState *g, hipStream_t s, const uint16_t *W, int n, int k, const uint16_t *x, int m,
                      void *y, int ldy, bool y_bf16, bool accumulate) {
     if (!g || n < 1 || k < 1 || m < 0 || ldy < n || (accumulate && y_bf16)) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
     const bool fits = gemm_mfma_fits(W, n, k, x, m, y, ldy);
-    if (fits && (g->mode == kMfmaOnly || (g->mode == kPlanned && mfma_preferred(n, k, m))))
+    if (fits && g->mode == kPlanned)
         return run_mfma(*g, W, n, k, x, m, y, ldy, y_bf16, accumulate, s);
     hipError_t e = hipSuccess;
     if (!g->handle) {

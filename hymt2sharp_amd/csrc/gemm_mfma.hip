@@ -65,7 +65,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
-    const uint16_t *W;  // [n][k]
+    const uint16_t *W;  // [n][k]; GLU: the gate rows [n / 2][k]
+    const uint16_t *W2; // GLU: the up rows [n / 2][k]
     const uint16_t *x;  // [m][k]
     void *y;            // [m][ldy], fp32 or bf16
     int n, k, m, ldy;
@@ -148,7 +149,13 @@ __device__ __forceinline__ void substep(bf16x8 (&w)[IF], const bf16x8 (&cx)[JT],
 // waits for its own reads: lgkmcnt(0)), so S - 1 stages are ahead of the one
 // being read; else one barrier later, with S - 2 stages ahead and no wait on
 // the reads.
-template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT, bool YBF16, bool ACC>
+//
+// GLU (the gate/up GEMM with SwiGLU fused, unsplit): the tile's first TF / 2
+// features are gate rows f0 / 2 + [0, TF / 2) of W, the others the same rows
+// of W2 (up), so the tile holds both inputs of TF / 2 outputs
+// silu(g) u (swiglu8, the row kernel's function of the same bf16-rounded g
+// and u), written to y[m][ldy] at column f0 / 2: n is twice the output width.
+template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT, bool YBF16, bool ACC, bool GLU = false>
 __global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
     constexpr int TF = 32 * IF, TT = 32 * JT;
     constexpr int NW = 2 * WT, NT = 64 * NW, BJ = TT / (16 * WT);  // waves, threads, token blocks per wave
@@ -158,6 +165,7 @@ __global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
     constexpr int AHEAD = LGKM ? S : S - 1;  // stages issued ahead of the one being read, plus one
     static_assert((2 * NB) % NW == 0 && BJ >= 1 && AHEAD >= 2 && C * (AHEAD - 1) <= 63, "tile shape");
     static_assert(S * kStageBytes <= 160 * 1024, "LDS");
+    static_assert(!GLU || (YBF16 && SPLIT == 1), "GLU: bf16 output, unsplit");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[S * kStageBytes];
     unsigned &s_role = *(unsigned *)lds;  // split role, once the ring is idle
     const int tid = threadIdx.x, lane = tid & 63;
@@ -188,9 +196,16 @@ __global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
         const int rl = (ga >> 1) + 8 * (ga & 1);
         const int piece = (lane & 7) ^ (ga >> 1);
         const bool isw = gb < NBF;
-        const int row = isw ? f0 + 16 * gb + rl : min(t0 + 16 * (gb - NBF) + rl, a.m - 1);
-        voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
-        sbase[j] = (isw ? a.W : a.x) + kbase;
+        if constexpr (GLU) {  // gate row blocks [0, NBF / 2), then up
+            const bool up = isw && gb >= NBF / 2;
+            const int row = isw ? f0 / 2 + 16 * (up ? gb - NBF / 2 : gb) + rl : min(t0 + 16 * (gb - NBF) + rl, a.m - 1);
+            voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
+            sbase[j] = (isw ? (up ? a.W2 : a.W) : a.x) + kbase;
+        } else {
+            const int row = isw ? f0 + 16 * gb + rl : min(t0 + 16 * (gb - NBF) + rl, a.m - 1);
+            voff[j] = (uint32_t)(((size_t)row * a.k + 8 * piece) * 2);
+            sbase[j] = (isw ? a.W : a.x) + kbase;
+        }
     }
     const uint32_t lds0 = lds_addr(lds) + wave * C * kFrag;
     // copy j of stage t into its ring slot t % S.  Stages past the last
@@ -369,6 +384,21 @@ __global__ __launch_bounds__(128 * WT, 1) void gemm_kernel(GemmArgs a) {
                 }
             }
             __syncthreads();
+            if constexpr (GLU) {
+                constexpr int CPO = TF / 16;        // 16-byte chunks of an output row (TF / 2 values)
+                constexpr int NO = TT * CPO / NT;   // chunks per thread
+                static_assert((TT * CPO) % NT == 0, "GLU restage");
+#pragma unroll
+                for (int n = 0; n < NO; n++) {
+                    const int q = n * NT + tid, row = q / CPO, col = q - row * CPO;
+                    const int t = t0 + row;
+                    if (t < a.m)
+                        *(uint4 *)((uint16_t *)a.y + (size_t)t * a.ldy + f0 / 2 + 8 * col) =
+                            swiglu8(*(const uint4 *)(st + row * RS + 8 * col),
+                                    *(const uint4 *)(st + row * RS + TF / 2 + 8 * col));
+                }
+                return;
+            }
 #pragma unroll
             for (int n = 0; n < NQ; n++) {
                 const int q = n * NT + tid, row = q / CPR, col = q - row * CPR;
@@ -416,8 +446,11 @@ constexpr TileShape kTiles[kGemmTiles] = {
     {"128x96", 4, 3}};
 
 template <int IF, int JT, int WT, int S, bool LGKM, int SPLIT>
-void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span) {
+void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s, const KernelSpan &span,
+                 bool glu = false) {
     const dim3 block(128 * WT);
+    if constexpr (SPLIT == 1)
+        if (glu) return launch(span, gemm_kernel<IF, JT, WT, S, LGKM, 1, true, false, true>, dim3(grid), block, 0, s, a);
     if (y_bf16) launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, true, false>, dim3(grid), block, 0, s, a);
     else if (acc) launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, false, true>, dim3(grid), block, 0, s, a);
     else launch(span, gemm_kernel<IF, JT, WT, S, LGKM, SPLIT, false, false>, dim3(grid), block, 0, s, a);
@@ -427,24 +460,24 @@ void launch_tile(const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t
 // stages, 4 ahead) were no faster, so the stream is not latency-bound.
 template <int SPLIT>
 void launch_shape(int tile, const GemmArgs &a, int grid, bool y_bf16, bool acc, hipStream_t s,
-                  const KernelSpan &span) {
+                  const KernelSpan &span, bool glu = false) {
     switch (tile) {
-    case 0: launch_tile<4, 4, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 32 KiB stages
-    case 1: launch_tile<8, 4, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
-    case 2: launch_tile<4, 8, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 48 KiB
-    case 3: launch_tile<6, 4, 4, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 40 KiB, 8 waves
+    case 0: launch_tile<4, 4, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;  // 32 KiB stages
+    case 1: launch_tile<8, 4, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;   // 48 KiB
+    case 2: launch_tile<4, 8, 2, 3, true, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;   // 48 KiB
+    case 3: launch_tile<6, 4, 4, 4, true, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;   // 40 KiB, 8 waves
     // 8 waves: 4 waves' 192 accumulators and operands each need more than
     // 256 VGPRs (the loop then moved accumulators through AGPRs); gate/up
     // at m = 2048 108 -> 94 us.  An 8-wave 256 x 256 tile took 105 us.  At
     // 192 x 128 8 waves gain 1-3 % (q/k/v at m = 2048, gate/up at 512); at
     // 128 x 128 they were mixed (down at m = 2048 2 % slower).
-    case 4: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span); break;   // 56 KiB
+    case 4: launch_tile<6, 8, 4, 2, true, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;   // 56 KiB
     // 128 x 64: short prompts, where 128 x 128 tiles leave a quarter of the
     // chip idle (at m = 512, split: o 11.4 against 15.0 us for 128 x 128 split,
     // down 22.9 against 28.1, q/k/v unsplit 13.3 against 15.3); a 192 x 64
     // tile was slower at every model shape
-    case 5: launch_tile<4, 2, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break;  // 24 KiB
-    default: launch_tile<4, 3, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span); break; // 28 KiB
+    case 5: launch_tile<4, 2, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break;  // 24 KiB
+    default: launch_tile<4, 3, 2, 4, false, SPLIT>(a, grid, y_bf16, acc, s, span, glu); break; // 28 KiB
     }
 }
 
@@ -547,7 +580,7 @@ hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, in
     if (p.split == 2 && (k % (4 * kBK) || !ws || ws->part_bytes < gemm_split_bytes(n, m, p) || ws->tickets < tiles))
         p.split = 1;
     const int TF = 32 * kTiles[p.tile].IF;
-    GemmArgs a;
+    GemmArgs a{};
     a.W = W;
     a.x = x;
     a.y = y;
@@ -566,6 +599,44 @@ hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, in
     KernelSpan span(y_bf16 ? "gemm_mfma_out_bf16" : "gemm_mfma_out_f32", s, true);
     if (p.split == 2) launch_shape<2>(p.tile, a, grid, y_bf16, accumulate, s, span);
     else launch_shape<1>(p.tile, a, grid, y_bf16, accumulate, s, span);
+    return hipGetLastError();
+}
+
+bool gemm_swiglu_fits(const uint16_t *Wg, const uint16_t *Wu, int f, int k, const uint16_t *x, int m,
+                      const uint16_t *act, int ld) {
+    auto a16 = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    return f > 0 && f % 64 == 0 && k >= 2 * kBK && k % (2 * kBK) == 0 && m > 0 && ld >= f && ld % 8 == 0 &&
+           (size_t)f * k * 2 < (1ull << 31) && (size_t)m * k * 2 < (1ull << 31) && a16(Wg) && a16(Wu) && a16(x) &&
+           a16(act);
+}
+
+hipError_t gemm_swiglu_mfma(const uint16_t *Wg, const uint16_t *Wu, int f, int k, const uint16_t *x, int m,
+                            uint16_t *act, int ld, hipStream_t s, GemmPlan p) {
+    if (!gemm_swiglu_fits(Wg, Wu, f, k, x, m, act, ld) || p.split != 1) return hipErrorInvalidValue;
+    if (p.tile < 0 || p.tile >= kGemmTiles) return hipErrorInvalidValue;
+    const int n = 2 * f;  // gate and up features, as the unfused GEMM sees them
+    int tiles = tiles_of(p.tile, n, m);
+    if (!tiles) {  // 2 f not a multiple of the tile's width (f % 64 == 0: 128 rows always fit)
+        p.tile = 0;
+        tiles = tiles_of(0, n, m);
+    }
+    const int TF = 32 * kTiles[p.tile].IF;
+    GemmArgs a{};
+    a.W = Wg;
+    a.W2 = Wu;
+    a.x = x;
+    a.y = act;
+    a.n = n;
+    a.k = k;
+    a.m = m;
+    a.ldy = ld;
+    a.tiles_f = n / TF;
+    a.tiles_t = tiles / a.tiles_f;
+    a.group_f = a.tiles_f % kGroupF == 0 ? kGroupF : 1;
+    a.kt = k / kBK;
+    a.xcd_per = tiles % 8 == 0 ? tiles / 8 : 0;
+    KernelSpan span("gemm_mfma_swiglu", s, true);
+    launch_shape<1>(p.tile, a, tiles, true, false, s, span, true);
     return hipGetLastError();
 }
 

@@ -1117,6 +1117,35 @@ int hymt_gemm(hymt_ctx *c, const hymt_weight *w, int row0, int nrows, const void
     return HYMT_OK;
 }
 
+int hymt_gemm_swiglu(hymt_ctx *c, const hymt_weight *gate, const hymt_weight *up, const void *x, int m, void *act) {
+    if (int r = check_ctx(c, false, true)) return r;
+    if (!gate || !x || !act) return fail(HYMT_E_ARG, "null weight or matrix");
+    TimedCall timed(call_timer(c), "gemm_swiglu", m);
+    if (!gate->dense || (up && !up->dense)) return fail(HYMT_E_STATE, "weight has no dense copy (hymt_weight_dense)");
+    const int k = gate->dev.cols;
+    const int f = up ? gate->dev.rows : gate->dev.rows / 2;
+    if (up ? up->dev.rows != f || up->dev.cols != k : gate->dev.rows % 2 != 0)
+        return fail(HYMT_E_ARG, "gate and up must have the same shape (or one weight an even number of rows)");
+    if (m < 0) return fail(HYMT_E_ARG, "negative row count");
+    if (int r = refuse_in_capture(c, "hymt_gemm_swiglu")) return r;
+    if (m == 0) return HYMT_OK;
+    try {
+        HIP_TRY(hipSetDevice(c->device));
+        if (!c->gemm && !(c->gemm = gemm_state_create())) return fail(HYMT_E_OOM, "host allocation failed");
+        const uint16_t *wu = up ? up->dense : gate->dense + (size_t)f * k;
+        hipError_t e = hipSuccess;
+        // gu: a 16-byte aligned [m][2 f] buffer of the unfused calls (only its
+        // alignment enters the choice)
+        if (!gemm_swiglu(c->gemm, c->stream, gate->dense, wu, up != nullptr, f, k, (const uint16_t *)x, m, nullptr,
+                         (uint16_t *)act, e))
+            return fail(HYMT_E_UNSUPPORTED, "no fused gate/up + SwiGLU with the unfused calls' bits for this shape");
+        HIP_TRY(e);
+    } catch (const HipError &e) {
+        return map_hip(e);
+    }
+    return HYMT_OK;
+}
+
 int hymt_embed_rows(hymt_ctx *c, const hymt_weight *w, const int32_t *rows, int n, float *out) {
     if (int r = check_ctx(c, false, true)) return r;
     if (!w || !rows || !out) return fail(HYMT_E_ARG, "null weight, rows or output");
@@ -1459,17 +1488,26 @@ int hymt_model_prefill(hymt_model *m, const int32_t *tokens, int n, int pos, flo
                     return r;
                 model_gemm(c, Ly.w[3], ao16, rows, x, H, false, true);
                 HIP_TRY(launch_rows_rmsnorm(x, rows, H, Ly.ffn_norm, m->eps, xn, c->stream));
-                if (!Ly.w[5]) {
-                    model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
-                } else {  // gate and up as two matrices into the halves of one row
-                    const size_t es = gu32 ? 4 : 2;
-                    model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
-                    model_gemm(c, Ly.w[5], xn, rows, (char *)gu + F * es, 2 * F, !gu32, false);
+                // gate/up GEMM + SwiGLU in one launch where that gives the
+                // bits of the two calls below (gemm_swiglu)
+                const uint16_t *wg = Ly.w[4]->dense, *wu = Ly.w[5] ? Ly.w[5]->dense : wg + (size_t)F * H;
+                hipError_t fe = hipSuccess;
+                if (!gu32 && gemm_swiglu(c->gemm, c->stream, wg, wu, Ly.w[5] != nullptr, F, H, xn, rows,
+                                         (const uint16_t *)gu, act, fe)) {
+                    HIP_TRY(fe);
+                } else {
+                    if (!Ly.w[5]) {
+                        model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
+                    } else {  // gate and up as two matrices into the halves of one row
+                        const size_t es = gu32 ? 4 : 2;
+                        model_gemm(c, Ly.w[4], xn, rows, gu, 2 * F, !gu32, false);
+                        model_gemm(c, Ly.w[5], xn, rows, (char *)gu + F * es, 2 * F, !gu32, false);
+                    }
+                    if (gu32)
+                        HIP_TRY(launch_rows_swiglu((const float *)gu, rows, F, act, c->stream));
+                    else
+                        HIP_TRY(launch_rows_swiglu_bf16((const uint16_t *)gu, rows, F, act, c->stream));
                 }
-                if (gu32)
-                    HIP_TRY(launch_rows_swiglu((const float *)gu, rows, F, act, c->stream));
-                else
-                    HIP_TRY(launch_rows_swiglu_bf16((const uint16_t *)gu, rows, F, act, c->stream));
                 model_gemm(c, Ly.down, act, rows, x, H, false, true);
             }
             if (r0 + rows == n)

@@ -129,20 +129,12 @@ __global__ __launch_bounds__(256) void rows_swiglu_bf16_kernel(const uint16_t *_
     }
 }
 
-// silu(g) = g / (1 + e^-g) from the hardware's base-2 exponential and
-// reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each): a few fp32 ulps from
-// the correctly rounded quotient, far inside the bf16 rounding of the result.
-// Large |g| behaves as the exact form: e^-g overflows to inf for g < -88 and
-// gives -0, and underflows to 0 for large g and gives g.
-__device__ __forceinline__ float silu_fast(float g) {
-    return g * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.4426950408889634f * g));
-}
-
 // As rows_swiglu_bf16_kernel with 16-byte accesses (8 values) when n is a
 // multiple of 8 and the buffers are 16-byte aligned, with 32-bit index
 // arithmetic (the launcher checks m n / 8 <= 2^30, so e plus the grid stride
-// stays below 2^31) and silu_fast: the exact quotient's exp and division were
-// most of its time.
+// stays below 2^31) and swiglu8 (silu_fast): the exact quotient's exp and
+// division were most of its time.  The gate/up GEMM's fused epilogue
+// (gemm_mfma.hip) computes the same swiglu8 of the same bf16 values.
 __global__ __launch_bounds__(256) void rows_swiglu_bf16_x8_kernel(const uint16_t *__restrict__ gu, int m, int n,
                                                                   uint16_t *__restrict__ out) {
     const int n8 = n / 8, total = m * n8;
@@ -150,16 +142,7 @@ __global__ __launch_bounds__(256) void rows_swiglu_bf16_x8_kernel(const uint16_t
         const int r = e / n8, i = e - r * n8;
         const uint4 gb = ((const uint4 *)(gu + (size_t)r * 2 * n))[i];
         const uint4 ub = ((const uint4 *)(gu + (size_t)r * 2 * n + n))[i];
-        const uint32_t gw[4] = {gb.x, gb.y, gb.z, gb.w};
-        const uint32_t uw[4] = {ub.x, ub.y, ub.z, ub.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const float g0 = bf16_to_f32(gw[k] & 0xFFFF), g1 = bf16_to_f32(gw[k] >> 16);
-            const float u0 = bf16_to_f32(uw[k] & 0xFFFF), u1 = bf16_to_f32(uw[k] >> 16);
-            o[k] = (uint32_t)f32_to_bf16(silu_fast(g0) * u0) | ((uint32_t)f32_to_bf16(silu_fast(g1) * u1) << 16);
-        }
-        ((uint4 *)(out + (size_t)r * n))[i] = make_uint4(o[0], o[1], o[2], o[3]);
+        ((uint4 *)(out + (size_t)r * n))[i] = swiglu8(gb, ub);
     }
 }
 

@@ -59,13 +59,12 @@ hipError_t launch_rows_swiglu_bf16(const uint16_t *gu, int m, int n, uint16_t *o
 hipError_t launch_to_bf16(const float *x, size_t count, uint16_t *out, hipStream_t s);
 // y[m][n] (+)= x[m][k] . W[n][k]^T, bf16 operands, fp32 accumulation
 // (gemm.cpp: this library's MFMA kernel, gemm_mfma.hip, wherever it fits,
-// except weights of 32 MiB or more over 1024 rows or more, which take
-// hipBLASLt's first heuristic choice); y is fp32 or, with y_bf16, bf16, rows
-// ldy elements apart.  The GemmState (library handle, workspace, chosen
-// kernels) belongs to one context.  HYMT_HIP_GEMM, read when the state is
-// created, changes the choice: =library hipBLASLt everywhere, =mfma the MFMA
-// kernel wherever it fits, =hipblaslt hipBLASLt's timed pick, =auto the faster
-// of the two on the first call of a shape.
+// hipBLASLt's first heuristic choice elsewhere); y is fp32 or, with y_bf16,
+// bf16, rows ldy elements apart.  The GemmState (library handle, workspace,
+// chosen kernels) belongs to one context.  HYMT_HIP_GEMM, read when the state
+// is created, changes the choice: =library hipBLASLt everywhere, =hipblaslt
+// hipBLASLt's timed pick, =auto the faster of the two on the first call of a
+// shape (=mfma is the default).
 struct GemmState;
 GemmState *gemm_state_create();
 void gemm_state_destroy(GemmState *g);
@@ -97,5 +96,24 @@ size_t gemm_split_bytes(int n, int m, GemmPlan p);
 int gemm_split_tiles(int n, int m, GemmPlan p);
 hipError_t gemm_bf16_mfma(const uint16_t *W, int n, int k, const uint16_t *x, int m, void *y, int ldy, bool y_bf16,
                           bool accumulate, hipStream_t s, GemmPlan p, const GemmSplitWs *ws);
+// act[m][f] (rows ld elements apart) = silu(g) u, bf16, with g and u the
+// bf16-rounded products x . Wg^T and x . Wu^T (Wg, Wu: [f][k]): the gate/up
+// GEMM and rows_swiglu_bf16 in one launch of the MFMA kernel, unsplit (plan:
+// the tile of the [gate; up] product, n = 2 f), the same bits as
+// gemm_bf16_mfma's unsplit bf16 output followed by launch_rows_swiglu_bf16's
+// 16-byte kernel.  f a multiple of 64; k, alignment and sizes as
+// gemm_mfma_fits; ld a multiple of 8.
+bool gemm_swiglu_fits(const uint16_t *Wg, const uint16_t *Wu, int f, int k, const uint16_t *x, int m,
+                      const uint16_t *act, int ld);
+hipError_t gemm_swiglu_mfma(const uint16_t *Wg, const uint16_t *Wu, int f, int k, const uint16_t *x, int m,
+                            uint16_t *act, int ld, hipStream_t s, GemmPlan p);
+// The state's fused gate/up + SwiGLU: runs it and returns true when the
+// state's choice for the unfused calls -- the gate/up GEMM(s) into gu (bf16
+// [m][2 f], as one [gate; up] matrix, or, separate, two [f][k] matrices) and
+// launch_rows_swiglu_bf16 -- is the MFMA kernel unsplit for every GEMM and the
+// 16-byte row kernel, so that the fused call's bits equal theirs; else returns
+// false having enqueued nothing (the caller issues the unfused calls).
+bool gemm_swiglu(GemmState *g, hipStream_t s, const uint16_t *Wg, const uint16_t *Wu, bool separate, int f, int k,
+                 const uint16_t *x, int m, const uint16_t *gu, uint16_t *act, hipError_t &err);
 
 }  // namespace hymt

@@ -38,7 +38,9 @@ separate C ABI calls:
         X += bf16(silu(gate) * up) . Wdown^T                hymt_rows_swiglu_bf16, hymt_gemm ACCUMULATE
     logits = Wout RMSNorm(X[last], output_norm)             hymt_gemv IN_RMSNORM
 (hymt_model_prefill has the attention write bf16(AO) itself, with the
-rounding of hymt_to_bf16, so the two sequences give the same bits.)
+rounding of hymt_to_bf16, and runs the gate/up GEMM and the SwiGLU as one
+launch (hymt_gemm_swiglu's kernel) wherever that gives the bits of the two
+calls, so the two sequences give the same bits.)
 """
 from __future__ import annotations
 

@@ -372,6 +372,21 @@ int hymt_rows_swiglu_bf16(hymt_ctx *ctx, const void *gate_up, int m, int n, void
 /* out[i] = bf16(x[i]) for count fp32 values (count a multiple of 4). */
 int hymt_to_bf16(hymt_ctx *ctx, const float *x, size_t count, void *out);
 
+/* act[m][f] = bf16(silu(g) u), g and u the bf16 products x . Wg^T and
+ * x . Wu^T over the dense copies: the gate/up GEMM with SwiGLU fused into
+ * its output, one launch (the reference's Gemm(..., swiglu: true), and the
+ * Gemm + pf_silumul pair it replaces, VulkanBackend.cs:845-853).  gate is
+ * one weight of 2 f rows [gate; up] with up NULL, or the f gate rows with up
+ * the f up rows.  It runs only where its bits equal those of hymt_gemm with
+ * HYMT_GEMM_OUT_BF16 into a bf16 [m][2 f] buffer (the two halves by two calls
+ * for two weights) followed by hymt_rows_swiglu_bf16: the context's GEMM
+ * choice is the hand-written MFMA kernel, unsplit, for those calls, f a
+ * multiple of 64, cols a multiple of 128; otherwise it returns
+ * HYMT_E_UNSUPPORTED and enqueues nothing, and the caller issues those calls.
+ * x, act device pointers, 16-byte aligned; not recordable. */
+int hymt_gemm_swiglu(hymt_ctx *ctx, const hymt_weight *gate, const hymt_weight *up, const void *x, int m,
+                     void *act);
+
 /* ---- the model's decode step, enqueued natively ---------------------------------
  * IComputeBackend.ForwardStep for one token (IComputeBackend.cs:40-47) in one
  * call: the sequence of HunyuanDenseModel.DecodeBlock

@@ -154,14 +154,14 @@ def test_auto_choice_is_correct(monkeypatch, hip_available):
 @pytest.mark.parametrize("rows,cols,m,mfma", [
     (2048, 2048, 2048, True),    # o at a 2048-row prompt: the MFMA kernel
     (1024, 6144, 300, True),
-    (8192, 2048, 1024, False),   # a 32 MiB weight over 1024 rows: hipBLASLt's first choice
+    (8192, 2048, 1024, True),    # a 32 MiB weight over 1024 rows
+    (200, 2048, 64, False),      # a width the MFMA kernel does not take: hipBLASLt's first choice
 ])
 def test_default_choice_is_reproducible(monkeypatch, hip_available, rows, cols, m, mfma):
-    """Unset HYMT_HIP_GEMM: the MFMA kernel where it fits, except a weight of
-    32 MiB or more over 1024 or more rows, which takes hipBLASLt's first
-    heuristic choice; no timing either way, so two contexts (each choosing on
-    its own) give the same bits for the same inputs, and the results hold the
-    bound."""
+    """Unset HYMT_HIP_GEMM: the MFMA kernel wherever it fits, hipBLASLt's
+    first heuristic choice elsewhere; no timing either way, so two contexts
+    (each choosing on its own) give the same bits for the same inputs, and the
+    results hold the bound."""
     monkeypatch.delenv("HYMT_HIP_GEMM", raising=False)
     monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
     a, counts, ref, mag, y0 = run_case(rows, cols, m, 91, MFMA)
@@ -173,6 +173,21 @@ def test_default_choice_is_reproducible(monkeypatch, hip_available, rows, cols, 
         assert not any(counts.values()), counts
     for key in a:
         assert np.array_equal(a[key], b[key]), key
+
+
+def test_unsplit_tiles_agree_bitwise(monkeypatch, hip_available):
+    """Every unsplit tile gives the same bits (each output's k order is the
+    same 32-k MFMA chain): what lets the fused gate/up + SwiGLU launch use its
+    own tile and still equal the unfused calls."""
+    monkeypatch.setenv("HYMT_HIP_GEMM", "mfma")
+    base = None
+    for tile in ["128x128", "256x128", "128x256", "192x128", "192x256", "128x64", "128x96"]:
+        monkeypatch.setenv("HYMT_HIP_GEMM_TILE", tile)
+        out, _, _, _, _ = run_case(768, 2048, 130, 5150, MFMA)
+        if base is None:
+            base = out
+        for key in out:
+            assert np.array_equal(out[key], base[key]), (tile, key)
 
 
 def test_library_choice_is_reproducible(monkeypatch, hip_available):
