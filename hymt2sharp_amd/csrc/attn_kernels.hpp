@@ -101,11 +101,20 @@ struct PrepArgs {
     int norm_k;         // apply the k RMSNorm
     float eps;
     int kv_ld;          // elements from one k (and v) row to the next, >= Hkv*D
+    // with qready (split flash items): q prepared for prefill_flash in the
+    // same launch (grid rows kv_heads and up), RoPE + RMSNorm + the softmax
+    // scale, rounded to the cache type
+    const void *q;      // [seq][q_ld]    fp32 or bf16 (io_bf16)
+    const float *qnw;   // [D] gamma of q (a ones vector when the norm is off)
+    void *qready;       // [seq][heads*D] in the cache type, or null
+    int q_ld, heads, norm_q;
+    float qscale;       // log2(e) / sqrt(D)
 };
 
 struct FlashArgs {
     const void *q;      // [seq][Hq*D]    fp32 or bf16 (io_bf16), before RoPE/norm
     const float *qnw;   // [D] gamma of q (a ones vector when the norm is off)
+    const uint16_t *qready;  // null, or [seq][Hq*D] q after RoPE, norm and qscale in the cache type (prefill_kv)
     const float *rope_cos, *rope_sin;  // table base [cap][rope_half]
     const int32_t *tab;
     const void *kpool, *vpool;

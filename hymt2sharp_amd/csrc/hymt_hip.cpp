@@ -115,8 +115,8 @@ struct hymt_ctx {
 
     // decode workspace: split partials (m, l) and acc
     DevBuf dec_ml, dec_acc;
-    // prefill workspace
-    DevBuf part_o, part_ml;
+    // prefill workspace: split partials; q prepared by prefill_kv for the flash kernel
+    DevBuf part_o, part_ml, qready;
     // staging for host-pointer calls
     DevBuf in_q, in_k, in_v, in_qnw, in_knw, out_o, up_k, up_v;
     DevBuf rows_idx;  // token ids of hymt_embed_rows
@@ -137,8 +137,8 @@ struct hymt_ctx {
     uint64_t gen = 0;
 
     hymt_ctx() {
-        for (DevBuf *b : {&kpool, &vpool, &tab, &rope_cos, &rope_sin, &ones, &dec_ml, &dec_acc, &part_o, &part_ml, &in_q,
-                          &in_k, &in_v, &in_qnw, &in_knw, &out_o, &up_k, &up_v, &rows_idx})
+        for (DevBuf *b : {&kpool, &vpool, &tab, &rope_cos, &rope_sin, &ones, &dec_ml, &dec_acc, &part_o, &part_ml,
+                          &qready, &in_q, &in_k, &in_v, &in_qnw, &in_knw, &out_o, &up_k, &up_v, &rows_idx})
             b->gen = &gen;
     }
 
@@ -340,7 +340,7 @@ int hymt_destroy(hymt_ctx *c) {
         }
         (void)hipStreamSynchronize(c->stream);
         for (DevBuf *b : {&c->kpool, &c->vpool, &c->tab, &c->rope_cos, &c->rope_sin, &c->ones, &c->dec_ml,
-                          &c->dec_acc, &c->part_o, &c->part_ml, &c->in_q,
+                          &c->dec_acc, &c->part_o, &c->part_ml, &c->qready, &c->in_q,
                           &c->in_k, &c->in_v, &c->in_qnw, &c->in_knw, &c->out_o, &c->up_k, &c->up_v, &c->rows_idx})
             b->release();
         c->h_in.release();
@@ -691,11 +691,18 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         p.io_bf16 = io_dtype == HYMT_BF16;
         p.eps = c->eps;
         p.kv_ld = kv_ld ? kv_ld : c->kv_heads * (int)D;
-        HIP_TRY(launch_prefill_prep(c->kv_dtype, p, c->stream));
+        p.q = dev ? q : c->in_q.p;
+        p.qnw = !qnw ? (const float *)c->ones.p : dev ? qnw : (const float *)c->in_qnw.p;
+        p.norm_q = qnw != nullptr;
+        p.q_ld = q_ld ? q_ld : c->heads * (int)D;
+        p.heads = c->heads;
+        p.qscale = 1.4426950408889634f / sqrtf((float)D);
+        p.qready = nullptr;
 
-        FlashArgs f;
-        f.q = dev ? q : c->in_q.p;
-        f.qnw = !qnw ? (const float *)c->ones.p : dev ? qnw : (const float *)c->in_qnw.p;
+        FlashArgs f{};
+        f.q = p.q;
+        f.qnw = p.qnw;
+        f.qready = nullptr;
         f.norm_q = qnw != nullptr;
         f.rope_cos = (const float *)c->rope_cos.p;
         f.rope_sin = (const float *)c->rope_sin.p;
@@ -711,8 +718,8 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         f.rope_dim = c->rope_dim;
         f.io_bf16 = io_dtype == HYMT_BF16;
         f.eps = c->eps;
-        f.qscale = 1.4426950408889634f / sqrtf((float)D);
-        f.q_ld = q_ld ? q_ld : c->heads * (int)D;
+        f.qscale = p.qscale;
+        f.q_ld = p.q_ld;
         f.out_bf16 = out_bf16;
         f.nb16 = (seq + 15) / 16;
         f.npairs = (f.nb16 + 1) / 2;
@@ -749,15 +756,24 @@ static int prefill_impl(hymt_ctx *c, int layer, int pos, int seq, const void *q,
         f.items_per_kvh = items;
         if (split) {
             const size_t slots = (size_t)c->kv_heads * items;
-            // partial O / l in the 16-bit cache type, (m, l) in fp32
+            // partial O / l in the 16-bit cache type, (m, l) in fp32; the q
+            // rows prepared once by prefill_kv for the pair's split items
+            // (each item would otherwise repeat the q prologue: config 4's
+            // call 36.8 -> 33.2 us; unsplit, the 16 MB of q traffic cost what
+            // the shorter flash prologue saves)
             if (c->capturing &&
-                (slots * kGroup * 32 * D * 2 > c->part_o.bytes || slots * kGroup * 32 * 2 * 4 > c->part_ml.bytes))
+                (slots * kGroup * 32 * D * 2 > c->part_o.bytes || slots * kGroup * 32 * 2 * 4 > c->part_ml.bytes ||
+                 qn * 2 > c->qready.bytes))
                 return fail_capture(c, "prefill workspace growth");
             c->part_o.reserve(slots * kGroup * 32 * D * 2);
             c->part_ml.reserve(slots * kGroup * 32 * 2 * 4);
+            c->qready.reserve(qn * 2);
+            p.qready = c->qready.p;
+            f.qready = (const uint16_t *)c->qready.p;
         }
         f.part_o = c->part_o.p;
         f.part_ml = (float *)c->part_ml.p;
+        HIP_TRY(launch_prefill_prep(c->kv_dtype, p, c->stream));
         HIP_TRY(launch_prefill_flash(c->kv_dtype, f, items * c->kv_heads, c->stream));
         if (split) HIP_TRY(launch_prefill_merge(c->kv_dtype, f, c->stream));
         if (!dev) stage_out(c, c->out_o.p, out, qn * 4);

@@ -9,13 +9,18 @@
 // Kernels:
 //  prefill_kv     one workgroup per (32-position block, kv head): RoPE + norm
 //                 of k, k and v rounded into the paged cache (v transposed
-//                 through LDS into whole V chunks).
+//                 through LDS into whole V chunks); when the flash items are
+//                 split, also one per (32-position block, q head): RoPE +
+//                 norm of the q rows times the softmax scale, rounded to the
+//                 operand type (qready), which the split items then load
+//                 instead of each preparing the same rows again.
 //  prefill_flash  one workgroup per (kv head, 32-row q block, kv tile range):
 //                 8 waves = the 4 q heads of the GQA group x the two parities
 //                 of the range's 64-position tiles, so every SIMD runs two
 //                 waves; each staged K/V tile in LDS serves the 4 heads.  The
 //                 prologue applies RoPE + norm to the wave's 32 q rows
-//                 straight into MFMA operand registers.  S^T - m = K Q^T - m
+//                 straight into MFMA operand registers (or, QREADY, loads
+//                 them prepared by prefill_kv).  S^T - m = K Q^T - m
 //                 (accumulated onto -m) and O^T += V^T P^T on
 //                 v_mfma_f32_16x16x32_{bf16,f16}; single-pass online softmax
 //                 in base 2 with a lazy running maximum that starts at the
@@ -111,6 +116,62 @@ template <int HK> __device__ __forceinline__ float rope_partner_dpp(float x, int
     }
 }
 
+// q row m of head h for the split flash items: lane c of the row's 16 takes
+// dims 8 c .. 8 c + 7 -- RoPE (partner by DPP, as for k below), RMSNorm (sum
+// of squares by DPP over the row), gamma, the softmax scale log2(e)/sqrt(D),
+// rounded to the cache type -- one 16-byte load and one 16-byte store.
+template <typename T, bool IN_BF16, int HK>
+__device__ __forceinline__ void q_row(const PrepArgs &a, int h, int m, int mc, bool valid, int c) {
+    constexpr int D = kHeadDim;
+    const int d0 = 8 * c, rh = a.rope_half;
+    const size_t src = (size_t)mc * a.q_ld + (size_t)h * D + d0;
+    float x[8], cs[8], sn[8], gw[8];
+    if constexpr (IN_BF16) {
+        const uint4 u = *(const uint4 *)((const uint16_t *)a.q + src);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[2 * e] = __uint_as_float(w[e] << 16);
+            x[2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
+        }
+    } else {
+        const float4 q0 = *(const float4 *)((const float *)a.q + src), q1 = *(const float4 *)((const float *)a.q + src + 4);
+        x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w; x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
+    }
+    if constexpr (HK > 0) {
+        const size_t rb = (size_t)(a.pos0 + mc) * rh + (d0 & (rh - 1));
+        const float4 c0 = *(const float4 *)(a.rope_cos + rb), c1 = *(const float4 *)(a.rope_cos + rb + 4);
+        const float4 s0 = *(const float4 *)(a.rope_sin + rb), s1 = *(const float4 *)(a.rope_sin + rb + 4);
+        cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+        sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    }
+    {
+        const float4 g0 = *(const float4 *)(a.qnw + d0), g1 = *(const float4 *)(a.qnw + d0 + 4);
+        gw[0] = g0.x; gw[1] = g0.y; gw[2] = g0.z; gw[3] = g0.w; gw[4] = g1.x; gw[5] = g1.y; gw[6] = g1.z; gw[7] = g1.w;
+    }
+    float y[8], ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        float yv = x[e];
+        if constexpr (HK > 0) {
+            const float xp = rope_partner_dpp<HK>(x[e], c);
+            const bool rot = d0 < 64 * HK, lower = (d0 & rh) == 0;
+            yv = !rot ? x[e] : lower ? x[e] * cs[e] - xp * sn[e] : xp * sn[e] + x[e] * cs[e];
+        }
+        y[e] = yv;
+        ss += yv * yv;
+    }
+    ss = dpp_sum16(ss);
+    const float rr = a.norm_q ? 1.0f / sqrtf(ss / (float)D + a.eps) : 1.0f;
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        w[e] = (uint32_t)to_elem<T>(y[2 * e] * rr * gw[2 * e] * a.qscale) |
+               ((uint32_t)to_elem<T>(y[2 * e + 1] * rr * gw[2 * e + 1] * a.qscale) << 16);
+    if (valid)
+        *(uint4 *)((uint16_t *)a.qready + (size_t)m * a.heads * D + (size_t)h * D + d0) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 template <typename T, bool IN_BF16, int HK>
 __global__ __launch_bounds__(512) void prefill_kv_kernel(PrepArgs a) {
     constexpr int D = kHeadDim, P = kPage;
@@ -123,6 +184,10 @@ __global__ __launch_bounds__(512) void prefill_kv_kernel(PrepArgs a) {
     const int m = pstart + r - a.pos0;                    // row within the chunk
     const bool valid = m >= 0 && m < a.seq;
     const int mc = m < 0 ? 0 : (m < a.seq ? m : a.seq - 1);  // clamped for loads
+    if (kvh >= Hkv) {  // a q block: head kvh - Hkv (uniform over the workgroup)
+        q_row<T, IN_BF16, HK>(a, kvh - Hkv, m, mc, valid, c);
+        return;
+    }
     const int phys = __builtin_amdgcn_readfirstlane(a.tab[pstart / P]);
     const int d0 = 8 * c, rh = a.rope_half;
     const size_t src = (size_t)mc * a.kv_ld + (size_t)kvh * D + d0;
@@ -229,7 +294,8 @@ hipError_t launch_prefill_prep(int kv_dtype, const PrepArgs &a, hipStream_t s) {
     // blocks of 32 positions from the chunk's first to the end of the page
     // holding its last position (the V rows past the chunk are zeroed)
     const int first = a.pos0 & ~31, last = ((a.pos0 + a.seq + kPage - 1) & ~(kPage - 1)) - 1;
-    dim3 grid((last - first) / 32 + 1, a.kv_heads);
+    // grid rows [0, kv_heads): k/v; with qready, [kv_heads, kv_heads + heads): q
+    dim3 grid((last - first) / 32 + 1, a.kv_heads + (a.qready ? a.heads : 0));
     if (a.rope_dim != 0 && a.rope_dim != 64 && a.rope_dim != 128) return hipErrorInvalidValue;
     switch (kv_dtype) {
     case 1: a.io_bf16 ? launch_kv<F16, true>(a, grid, s) : launch_kv<F16, false>(a, grid, s); break;
@@ -501,7 +567,7 @@ constexpr float kLazy = 8.0f;
 // the 16 of its long block B (qq = 1); tiles past A's causal range run B
 // alone.  Tile pair j sits in LDS buffer j & 1 (one slot per parity); the
 // two halves' (m, l, O) are combined through LDS at the end.
-template <typename T, bool IN_BF16, int HK, bool PAGES_ARG>
+template <typename T, bool IN_BF16, int HK, bool PAGES_ARG, bool QREADY>
 __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     // The arguments pass through one empty asm (scalars as outputs, pointers
     // as inputs, which keeps their global address space): the compiler then
@@ -513,8 +579,8 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
                  : "+s"(a.pos0), "+s"(a.seq), "+s"(a.heads), "+s"(a.kv_heads), "+s"(a.rope_half), "+s"(a.io_bf16),
                    "+s"(a.norm_q), "+s"(a.eps), "+s"(a.qscale), "+s"(a.nb16), "+s"(a.npairs), "+s"(a.cap),
                    "+s"(a.items_per_kvh), "+s"(a.q_ld), "+s"(a.out_bf16)
-                 : "s"(a.q), "s"(a.qnw), "s"(a.rope_cos), "s"(a.rope_sin), "s"(a.tab), "s"(a.kpool), "s"(a.vpool),
-                   "s"(a.out), "s"(a.part_o), "s"(a.part_ml));
+                 : "s"(a.q), "s"(a.qnw), "s"(a.qready), "s"(a.rope_cos), "s"(a.rope_sin), "s"(a.tab), "s"(a.kpool),
+                   "s"(a.vpool), "s"(a.out), "s"(a.part_o), "s"(a.part_ml));
     constexpr int D = kHeadDim, P = kPage, G = kGroup;
     constexpr int KT = P * D;  // elements of one staged K or V tile (16 KiB)
     typedef typename Mfma<T>::vec vec;
@@ -592,43 +658,68 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
     int phys_first;
     if constexpr (PAGES_ARG) phys_first = args.pages[min(it.t0 + min(half_u, nt - 1), kArgPages - 1)];
     else phys_first = __builtin_amdgcn_readfirstlane(a.tab[it.t0 + min(half_u, nt - 1)]);
-    QRaw<IN_BF16> raw;
-    bool qok[2];
-    q_load<IN_BF16>(a, h, rowq, okq, grp, c, raw, qok);
-    // RoPE rows: float4 (table, 4 dims, row) i = tid + 512 k of 16 * rope_half
-    // (k = 0, 1; named values, not an array, which the compiler would place
-    // in LDS and store before the tile copies)
-    constexpr int RH = 32 * HK;  // rope_half
-    auto rope_src = [&](int k) {
-        const int i = min(tid + 512 * k, max(16 * RH - 1, 0));
-        const int r = i & 31, f4 = RH ? (i >> 5) % (RH / 4) : 0, tbl = RH ? i / (8 * RH) : 0;
-        const int row = min((r < 16 ? 16 * blkA : 16 * blkB) + (r & 15), a.seq - 1);
-        return (const float4 *)((tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * RH + 4 * f4);
-    };
-    float4 rope_v0 = make_float4(0.f, 0.f, 0.f, 0.f), rope_v1 = rope_v0;
-    if constexpr (HK > 0) {
-        rope_v0 = *rope_src(0);
-        rope_v1 = *rope_src(1);
-    }
-    if (half_u < nt) fetch(phys_first, 0);
-    if (tid < nt) sTab[tid] = tab0;
-    if (tid + 512 < nt) sTab[tid + 512] = tab1;
-    // the V slot of buffer 1, parity 0 (16 KiB = 2 * kRopeF4 * 32 float4)
-    float *rope_lds = (float *)(sKV + (4 + 2) * KT);
-    if constexpr (HK > 0) {
-        auto rope_put = [&](int k, float4 v) {
-            const int i = tid + 512 * k;
-            if (i < 16 * RH) {
-                const int r = i & 31, f4 = (i >> 5) % (RH / 4), tbl = i / (8 * RH);
-                ((float4 *)rope_lds)[(tbl * kRopeF4 + f4) * 32 + r] = v;
-            }
-        };
-        rope_put(0, rope_v0);
-        rope_put(1, rope_v1);
-    }
     vec qf[2][4];
-    __syncthreads();
-    q_finish<T, IN_BF16, HK>(a, raw, qok, grp, c, rope_lds, qf);
+    if constexpr (QREADY) {
+        // the wave's q rows, prepared by prefill_kv, as S^T B operands: lane
+        // (grp, c) holds dims 32 ks + 8 grp + [0, 8) of row rowq[qq] + c;
+        // rows past the chunk or of an absent block are 0 (results discarded)
+        const size_t qrow = (size_t)a.heads * D;
+        uint4 qu[2][4];
+        bool qok[2];
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++) {
+            const int row0 = rowq[qq] + c;
+            qok[qq] = okq[qq] && row0 < a.seq;
+            const size_t base = (size_t)min(row0, a.seq - 1) * qrow + (size_t)h * D + 8 * grp;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) qu[qq][ks] = *(const uint4 *)(a.qready + base + 32 * ks);
+        }
+        if (half_u < nt) fetch(phys_first, 0);
+        if (tid < nt) sTab[tid] = tab0;
+        if (tid + 512 < nt) sTab[tid + 512] = tab1;
+#pragma unroll
+        for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++)
+                qf[qq][ks] = __builtin_bit_cast(vec, qok[qq] ? qu[qq][ks] : make_uint4(0, 0, 0, 0));
+    } else {
+        QRaw<IN_BF16> raw;
+        bool qok[2];
+        q_load<IN_BF16>(a, h, rowq, okq, grp, c, raw, qok);
+        // RoPE rows: float4 (table, 4 dims, row) i = tid + 512 k of 16 * rope_half
+        // (k = 0, 1; named values, not an array, which the compiler would place
+        // in LDS and store before the tile copies)
+        constexpr int RH = 32 * HK;  // rope_half
+        auto rope_src = [&](int k) {
+            const int i = min(tid + 512 * k, max(16 * RH - 1, 0));
+            const int r = i & 31, f4 = RH ? (i >> 5) % (RH / 4) : 0, tbl = RH ? i / (8 * RH) : 0;
+            const int row = min((r < 16 ? 16 * blkA : 16 * blkB) + (r & 15), a.seq - 1);
+            return (const float4 *)((tbl ? a.rope_sin : a.rope_cos) + (size_t)(a.pos0 + row) * RH + 4 * f4);
+        };
+        float4 rope_v0 = make_float4(0.f, 0.f, 0.f, 0.f), rope_v1 = rope_v0;
+        if constexpr (HK > 0) {
+            rope_v0 = *rope_src(0);
+            rope_v1 = *rope_src(1);
+        }
+        if (half_u < nt) fetch(phys_first, 0);
+        if (tid < nt) sTab[tid] = tab0;
+        if (tid + 512 < nt) sTab[tid + 512] = tab1;
+        // the V slot of buffer 1, parity 0 (16 KiB = 2 * kRopeF4 * 32 float4)
+        float *rope_lds = (float *)(sKV + (4 + 2) * KT);
+        if constexpr (HK > 0) {
+            auto rope_put = [&](int k, float4 v) {
+                const int i = tid + 512 * k;
+                if (i < 16 * RH) {
+                    const int r = i & 31, f4 = (i >> 5) % (RH / 4), tbl = i / (8 * RH);
+                    ((float4 *)rope_lds)[(tbl * kRopeF4 + f4) * 32 + r] = v;
+                }
+            };
+            rope_put(0, rope_v0);
+            rope_put(1, rope_v1);
+        }
+        __syncthreads();
+        q_finish<T, IN_BF16, HK>(a, raw, qok, grp, c, rope_lds, qf);
+    }
 
     f32x4 o[8][2];
 #pragma unroll
@@ -915,9 +1006,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
 template <typename T, bool IN_BF16, bool PA> void launch_flash_pa(const FlashArgs &a, dim3 grid, hipStream_t s) {
     const int hk = a.rope_half >> 5;
     KernelSpan span("prefill_flash", s, true);
-    if (hk == 2) launch(span, prefill_flash_kernel<T, IN_BF16, 2, PA>, grid, dim3(512), 0, s, a);
-    else if (hk == 1) launch(span, prefill_flash_kernel<T, IN_BF16, 1, PA>, grid, dim3(512), 0, s, a);
-    else launch(span, prefill_flash_kernel<T, IN_BF16, 0, PA>, grid, dim3(512), 0, s, a);
+    if (a.qready) launch(span, prefill_flash_kernel<T, false, 0, PA, true>, grid, dim3(512), 0, s, a);
+    else if (hk == 2) launch(span, prefill_flash_kernel<T, IN_BF16, 2, PA, false>, grid, dim3(512), 0, s, a);
+    else if (hk == 1) launch(span, prefill_flash_kernel<T, IN_BF16, 1, PA, false>, grid, dim3(512), 0, s, a);
+    else launch(span, prefill_flash_kernel<T, IN_BF16, 0, PA, false>, grid, dim3(512), 0, s, a);
 }
 template <typename T, bool IN_BF16> void launch_flash(const FlashArgs &a, dim3 grid, hipStream_t s) {
     if (a.pages_in_args) launch_flash_pa<T, IN_BF16, true>(a, grid, s);
