@@ -701,7 +701,10 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
             rope_v0 = *rope_src(0);
             rope_v1 = *rope_src(1);
         }
-        if (half_u < nt) fetch(phys_first, 0);
+        // the small loads (page ids, q rows, gamma, RoPE rows) land first, with
+        // no tile copy queued behind them; then the first tile's copies go out
+        // and the RoPE staging, barrier and q_finish run while they land
+        __builtin_amdgcn_s_waitcnt(0);
         if (tid < nt) sTab[tid] = tab0;
         if (tid + 512 < nt) sTab[tid + 512] = tab1;
         // the V slot of buffer 1, parity 0 (16 KiB = 2 * kRopeF4 * 32 float4)
@@ -717,6 +720,7 @@ __global__ __launch_bounds__(512, 1) void prefill_flash_kernel(FlashArgs args) {
             rope_put(0, rope_v0);
             rope_put(1, rope_v1);
         }
+        if (half_u < nt) fetch(phys_first, 0);
         __syncthreads();
         q_finish<T, IN_BF16, HK>(a, raw, qok, grp, c, rope_lds, qf);
     }
