@@ -148,6 +148,18 @@ def test_prefill_split_merge_widths(oracle, hip_available, dtype, pos, seq):
     assert np.array_equal(vd, vref)
 
 
+@pytest.mark.parametrize("dtype,io_bf16,norm", [(BF16, True, "gamma"), (F16, True, None), (BF16, False, "gamma")])
+def test_split_items_take_prepared_q(oracle, hip_available, dtype, io_bf16, norm):
+    """A chunk over a long cache splits its block pairs into several items,
+    which load q prepared once by the k/v kernel (RoPE, RMSNorm and the
+    softmax scale in the operand type) instead of preparing it themselves:
+    bf16 and fp32 inputs, the norm on and off, against the oracle."""
+    got, ref, model, vf, (kd, vd), (kref, vref) = run_prefill(oracle, dtype, 6144, 96, norm, 15,
+                                                              salt=97, io_bf16=io_bf16)
+    check(got, ref, vf, dtype, model)
+    assert np.array_equal(vd, vref)
+
+
 def test_decode_equals_prefill_row(oracle, hip_available):
     """Benchmark --verify-prefill invariant (Benchmark/Program.cs:124-145):
     decoding token p over a cache of p rows equals row p of a prefill, up to
