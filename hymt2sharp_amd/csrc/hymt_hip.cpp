@@ -1154,7 +1154,9 @@ int hymt_gemm_swiglu(hymt_ctx *c, const hymt_weight *gate, const hymt_weight *up
         // alignment enters the choice)
         if (!gemm_swiglu(c->gemm, c->stream, gate->dense, wu, up != nullptr, f, k, (const uint16_t *)x, m, nullptr,
                          (uint16_t *)act, e))
-            return fail(HYMT_E_UNSUPPORTED, "no fused gate/up + SwiGLU with the unfused calls' bits for this shape");
+            return fail(HYMT_E_UNSUPPORTED,
+                        "no fused gate/up + SwiGLU with the unfused calls' bits here (the GEMM mode, a k split for "
+                        "this prompt length, the shape or a misaligned x / act)");
         HIP_TRY(e);
     } catch (const HipError &e) {
         return map_hip(e);
