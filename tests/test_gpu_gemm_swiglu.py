@@ -121,3 +121,25 @@ def test_fused_argument_errors(hip_available):
         be.weight_free(u)
     finally:
         be.Dispose()
+
+
+_rng = np.random.default_rng(20261203)
+SWEEP = [(64 * int(_rng.integers(1, 97)), int(_rng.choice([2048, 4096])), int(_rng.integers(1, 2500)),
+          bool(_rng.integers(0, 2))) for _ in range(10)]
+
+
+def test_fused_random_sweep(monkeypatch, hip_available):
+    """Seeded shapes (f a multiple of 64 up to 6144, k 2048 or 4096, m up to
+    2500, one [gate; up] weight or two): wherever the fused launch runs it
+    equals the unfused calls bit for bit; where it refuses (a k split, a width
+    the MFMA GEMM does not take) the unfused calls are what the model runs."""
+    monkeypatch.delenv("HYMT_HIP_GEMM", raising=False)
+    monkeypatch.delenv("HYMT_HIP_GEMM_TILE", raising=False)
+    ran = 0
+    for i, (f, k, m, separate) in enumerate(SWEEP):
+        print(f"sweep f={f} k={k} m={m} separate={separate}", flush=True)
+        fused, composed = fused_and_composed(f, k, m, 900 + i, separate)
+        if fused is not None:
+            ran += 1
+            assert np.array_equal(fused, composed), (f, k, m, separate)
+    assert ran >= 3, ran
